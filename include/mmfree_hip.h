@@ -1,0 +1,161 @@
+/* mmfree_hip.h -- C ABI of the MI355X (gfx950) HGRN-Bit engine, libmmfree_hip.so.
+ *
+ * The drop-in boundary between the host engine (the mmfree C++17 API: Model, Weights,
+ * TernaryBackend, the kernels.hpp free functions) and the HIP kernels. Plain C types only:
+ * no HIP or torch types cross it. Each entry point names the reference interface it
+ * replaces (files of aebarthyi/matmulfreellmCPU, cpp/...).
+ *
+ * Conventions
+ *   - Every function returns MMF_OK (0) or an MMF_ERR_* code; mmf_last_error(ctx) then
+ *     holds a message. The C++ layer turns a non-zero status into std::runtime_error,
+ *     which is the reference's error channel (weights.cpp:193-209, weights.hpp:49).
+ *   - "dev" pointers are device memory (from mmf_malloc or any HIP allocation on the
+ *     context's device); work on them is enqueued on the context's stream and is complete
+ *     after mmf_sync. "host" pointers are read or written before the call returns.
+ *   - A context is single-threaded, like the reference Model (bitlinear.cpp:47-53 shares
+ *     static staging buffers): calls on one context must not overlap.
+ *   - Activation modes (kernels.hpp:21-26): MMF_FLOAT (fp32 activations), MMF_FIXED_Q510
+ *     (static Q(15-f).f codes, int32 accumulation), and MMF_INT8_ABSMAX, a third mode with
+ *     per-row int8 absmax codes (tools/reference.py:131-135,180-184).
+ */
+#ifndef MMFREE_HIP_H
+#define MMFREE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mmf_ctx mmf_ctx;
+
+enum {
+  MMF_OK = 0,
+  MMF_ERR_ARG = 1,      /* invalid argument (shape, id, pointer, mode) */
+  MMF_ERR_HIP = 2,      /* HIP runtime error */
+  MMF_ERR_STATE = 3,    /* call out of order (e.g. no model loaded) */
+  MMF_ERR_NODEV = 4,    /* no usable gfx950 device */
+  MMF_ERR_MISSING = 5   /* a required tensor is missing (weights.hpp:47-50) */
+};
+
+enum { MMF_FLOAT = 0, MMF_FIXED_Q510 = 1, MMF_INT8_ABSMAX = 2 };
+
+/* ---- context ------------------------------------------------------------------------ */
+/* Open device `device` (must be gfx950); creates the context's stream. */
+int mmf_create(mmf_ctx** out, int device);
+void mmf_destroy(mmf_ctx* ctx);
+/* Message of the last failed call on ctx (or of the last failed mmf_create if ctx is NULL). */
+const char* mmf_last_error(const mmf_ctx* ctx);
+/* Wait for all work enqueued on the context's stream. */
+int mmf_sync(mmf_ctx* ctx);
+/* The context's hipStream_t, as an opaque pointer (for timing with events). */
+void* mmf_stream(mmf_ctx* ctx);
+/* Device name and compute-unit count, for reports. */
+int mmf_device_info(mmf_ctx* ctx, char* name, size_t name_cap, int* cus);
+
+/* ---- device memory (so callers need no HIP headers) ----------------------------------- */
+int mmf_malloc(mmf_ctx* ctx, void** dev, size_t bytes);
+int mmf_free(mmf_ctx* ctx, void* dev);
+int mmf_upload(mmf_ctx* ctx, void* dev, const void* host, size_t bytes);
+int mmf_download(mmf_ctx* ctx, void* host, const void* dev, size_t bytes);
+
+/* ---- resident projections: the TernaryBackend seam ------------------------------------ */
+/* Register a ternary projection wq [N, K] (int8 in {-1, 0, +1}, nn.Linear layout, host
+ * memory, as the blob stores it: tools/provision.py:98-99,122) with its per-tensor
+ * scale_w and BitLinear norm weight normw [K] (may be NULL if only the integer matmul is
+ * used). The weights are repacked on the device to 2 bits per weight. Returns the
+ * proj_id that the calls below and TernaryBackend::matmul take
+ * (ternary_backend.hpp:26-31: proj_id addresses resident weights). */
+int mmf_proj_register(mmf_ctx* ctx, const int8_t* wq, size_t N, size_t K, float scale_w,
+                      const float* normw, int* proj_id);
+/* Shape of a registered projection. */
+int mmf_proj_shape(mmf_ctx* ctx, int proj_id, size_t* N, size_t* K);
+
+/* TernaryBackend::matmul_batch (ternary_backend.hpp:43-48, 96-103):
+ * acc[i*N + o] = sum_k x[i*K + k] * wq[o, k] for b rows; x holds int16-range Q5.10 codes
+ * stored as int32 (ternary_backend.hpp:8-13). dev pointers. */
+int mmf_ternary_matmul(mmf_ctx* ctx, int proj_id, const int32_t* x, int32_t* acc, size_t b);
+
+/* ---- operators (kernels.hpp:29-68), dev pointers ----------------------------------------- */
+/* bitlinear (kernels.hpp:41-44, bitlinear.cpp:21-117) with the projection's registered
+ * weights, scale and norm: x [rows, K] -> out [rows, N]. acc (may be NULL) receives the
+ * int32 accumulators in the integer modes. */
+int mmf_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps, const float* x,
+                  float* out, size_t rows, int32_t* acc);
+/* bitlinear_cluster (kernels.hpp:46-50, bitlinear.cpp:119-160): k (<= 3) projections with
+ * equal shapes sharing the input x; bit-identical to k mmf_bitlinear calls. */
+int mmf_bitlinear_cluster(mmf_ctx* ctx, const int* proj_ids, int k, int mode, int frac_bits,
+                          float eps, const float* x, float* const* outs, size_t rows);
+/* rmsnorm (kernels.hpp:29-31, rmsnorm.cpp:11-22) */
+int mmf_rmsnorm(mmf_ctx* ctx, float* y, const float* x, const float* w, size_t rows, size_t cols,
+                float eps);
+/* swiglu: out = silu(a) * b (kernels.hpp:52-53, activations.cpp:9-15) */
+int mmf_swiglu(mmf_ctx* ctx, float* out, const float* a, const float* b, size_t n);
+/* hgrn_scan (kernels.hpp:55-59, hgrn_scan.cpp:11-19): state may be NULL (zeros) */
+int mmf_hgrn_scan(mmf_ctx* ctx, float* out, const float* i, const float* f, size_t T, size_t D,
+                  float* state);
+/* rmsnorm_swishgate (kernels.hpp:61-63, rmsnorm_swishgate.cpp:13-30) */
+int mmf_rmsnorm_swishgate(mmf_ctx* ctx, float* out, const float* g, const float* o,
+                          const float* w, size_t rows, size_t cols, float eps);
+
+/* ---- model (model.hpp:33-120) ----------------------------------------------------------- */
+typedef struct {
+  size_t vocab_size, hidden_size, num_hidden_layers, intermediate_size; /* config.hpp:8-21 */
+  int use_lower_bound;
+  float rms_norm_eps;
+} mmf_config;
+
+/* Begin a model (replaces Model::Model + the Weights tensor table, model.hpp:37,
+ * weights.cpp:191-254): the tensors of the MMFREE1 blob are then handed over one by one
+ * with mmf_model_tensor (names and shapes of tools/provision.py:101-124), and
+ * mmf_model_finalize checks that every tensor is present, repacks the projections and
+ * prepares the decode plan for (mode, frac_bits). */
+int mmf_model_begin(mmf_ctx* ctx, const mmf_config* cfg);
+/* dtype: 0 = f32, 1 = i8. host data, numel = product of shape. */
+int mmf_model_tensor(mmf_ctx* ctx, const char* name, int dtype, const size_t* shape, int ndim,
+                     const void* data);
+int mmf_model_finalize(mmf_ctx* ctx, int mode, int frac_bits);
+int mmf_model_config(mmf_ctx* ctx, mmf_config* cfg);
+
+/* Greedy Model::generate (model.hpp:44-50, hgrn_model.cpp:249-347), decode loop on the
+ * device. Writes the id stream (prompt + generated) to out (capacity cap) and its length to
+ * out_len. on_token (may be NULL) is called with each generated id, in order; eos_id < 0
+ * disables the stop. The recurrent state is reset at entry. */
+typedef void (*mmf_token_cb)(void* user, int64_t id);
+int mmf_model_generate(mmf_ctx* ctx, const int64_t* ids, size_t n, size_t new_tokens,
+                       int64_t eos_id, int64_t* out, size_t cap, size_t* out_len,
+                       mmf_token_cb on_token, void* user);
+
+/* Step-wise interface for sampling and serving (Model::generate with temperature > 0,
+ * Model::generate_serve, hgrn_model.cpp:263-303,349-454):
+ *   mmf_model_reset(B)      zero the recurrent state of B streams ([L][B][H])
+ *   mmf_model_prefill(b)    run the prompt of stream b through all layers (time scan)
+ *   mmf_model_step(tokens)  one batched decode step of all B streams
+ * logits (host [rows, V], may be NULL) and argmax (host [rows], may be NULL) receive the
+ * result for the last prompt position / each stream. */
+int mmf_model_reset(mmf_ctx* ctx, size_t streams);
+int mmf_model_prefill(mmf_ctx* ctx, size_t stream, const int64_t* ids, size_t n, float* logits,
+                      int64_t* argmax);
+int mmf_model_step(mmf_ctx* ctx, const int64_t* tokens, float* logits, int64_t* argmax);
+/* Recurrent state [L][B][H] after the last generate / prefill / step (host out). */
+int mmf_model_state(mmf_ctx* ctx, float* out);
+
+/* Model::forward (model.hpp:40-41, hgrn_model.cpp:239-247): stateless, logits [T, V] host. */
+int mmf_model_forward(mmf_ctx* ctx, const int64_t* ids, size_t T, float* logits);
+
+/* Layer-by-layer prefill trace for parity checks: after each layer l, h [L][T][H], the
+ * state [L][H] and the block internals [L][5][T][H] (i, gated f, g, scan input,
+ * recurrence output). host outputs; internals may be NULL. */
+int mmf_model_trace(mmf_ctx* ctx, const int64_t* ids, size_t T, float* h, float* state,
+                    float* internals);
+
+/* Timing of the single-row decode kernels on the context's stream (HIP events around
+ * `reps` decode steps, after `warmup` untimed ones): average microseconds per step and
+ * per launch of the kernel kinds {IFG, O, GATE, DOWN, LM} (kind_us[5], may be NULL). */
+int mmf_model_time_decode(mmf_ctx* ctx, int warmup, int reps, double* step_us, double* kind_us);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

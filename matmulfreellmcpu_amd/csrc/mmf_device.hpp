@@ -1,0 +1,142 @@
+// mmf_device.hpp -- device-side numerics shared by the HIP kernels (gfx950).
+//
+// Every function reproduces, operation for operation and rounding for rounding, the
+// reference engine's arithmetic as g++ compiles it (-O2 -mavx2 -mfma, GNU mode, so each
+// mul+add pair in cpp/include/mmfree/simd.hpp that is not an explicit intrinsic FMA is
+// fused). All HIP sources are compiled with -ffp-contract=off and every FMA below is an
+// explicit __builtin_fmaf; division and sqrt are the correctly rounded IEEE forms
+// (-fhip-fp32-correctly-rounded-divide-sqrt).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mmf {
+
+// ---- packed ternary weights --------------------------------------------------------
+// A 32-bit word holds 16 two-bit two's-complement codes (00 = 0, 01 = +1, 11 = -1). Code
+// t (0..15) sits at bit 8*(t%4) + 2*(t/4), so (word >> 2i) & 0x03030303 puts the codes
+// of t = 4i..4i+3 in the low bits of bytes 0..3 (a v_perm_b32 selector).
+__device__ __forceinline__ constexpr int code_shift(int t) { return 8 * (t & 3) + 2 * (t >> 2); }
+
+// signed code of position t as float (-1, 0, +1): one v_bfe_i32 + v_cvt_f32_i32
+__device__ __forceinline__ float code_f(uint32_t w, int t) {
+  return static_cast<float>(static_cast<int32_t>(w << (30 - code_shift(t))) >> 30);
+}
+
+// weights t = 4i..4i+3 as four int8 lanes: v_perm_b32 with the byte table {0, +1, 0, -1}
+__device__ __forceinline__ uint32_t w4_i8(uint32_t w, int i) {
+  return __builtin_amdgcn_perm(0u, 0xFF000100u, (w >> (2 * i)) & 0x03030303u);
+}
+
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot4(static_cast<int32_t>(a), static_cast<int32_t>(b), c, false);
+}
+
+// ---- reductions in the reference order ---------------------------------------------
+// hsum_ps (simd.hpp:48-57): ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+__device__ __forceinline__ float hsum8(const float* a) {
+  float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+  return (s0 + s1) + (s2 + s3);
+}
+
+// The same tree across the 8 consecutive lanes that hold the 8 chain partials of one
+// output (lane j holds a_j). Valid in lane j == 0 of each group of 8.
+__device__ __forceinline__ float hsum8_lanes(float a) {
+  float s = a + __shfl_down(a, 4, 8);  // lanes 0..3: a_j + a_{j+4}
+  s = s + __shfl_down(s, 1, 8);        // lane 0: s0+s1, lane 2: s2+s3
+  return s + __shfl_down(s, 2, 8);     // lane 0: (s0+s1)+(s2+s3)
+}
+
+__device__ __forceinline__ int32_t isum8_lanes(int32_t a) {
+  a += __shfl_down(a, 4, 8);
+  a += __shfl_down(a, 2, 8);
+  return a + __shfl_down(a, 1, 8);
+}
+
+// rstd = 1 / sqrt(sumsq / n + eps) (bitlinear.cpp:69, rmsnorm.cpp:19)
+__device__ __forceinline__ float rstd_of(float ss, int n, float eps) {
+  return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
+// ---- Cephes exp (simd.hpp:212-249) ----------------------------------------------------
+constexpr float kExpHi = 88.3762626647949f;
+constexpr float kExpLo = -88.3762626647949f;
+
+__device__ __forceinline__ float pow2_of(float fx) {
+  return __int_as_float((static_cast<int32_t>(fx) + 127) << 23);
+}
+
+__device__ __forceinline__ float exp_poly(float r) {
+  float p = 1.9875691500E-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507E-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073E-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894E-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459E-1f);
+  return __builtin_fmaf(p, r, 5.0000001201E-1f);
+}
+
+// 1 + exp(-a), the denominator of sigmoid/silu/swiglu. Body = one lane of the AVX2 path
+// (exp8_ps with max/min clamp, p = fma(p, r*r, r+1)); tail = the scalar expf_poly as g++
+// contracts it (p = fma(p, r*r, r) + 1). Callers fuse 1 + p*2^n into fma(p, 2^n, 1).
+__device__ __forceinline__ float den_body(float a) {
+  float x = -a;
+  x = (x > kExpLo) ? x : kExpLo;
+  x = (x < kExpHi) ? x : kExpHi;
+  float fx = floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
+  float r = __builtin_fmaf(-fx, 0.693359375f, x);
+  r = __builtin_fmaf(-fx, -2.12194440e-4f, r);
+  float p = __builtin_fmaf(exp_poly(r), r * r, r + 1.0f);
+  return __builtin_fmaf(p, pow2_of(fx), 1.0f);
+}
+
+__device__ __noinline__ float den_tail(float a) {
+  float x = -a;
+  if (x > kExpHi) x = kExpHi;
+  else if (x < kExpLo) x = kExpLo;
+  float fx = floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
+  float r = __builtin_fmaf(-fx, 0.693359375f, x);
+  r = __builtin_fmaf(-fx, -2.12194440e-4f, r);
+  float p = __builtin_fmaf(exp_poly(r), r * r, r) + 1.0f;
+  return __builtin_fmaf(p, pow2_of(fx), 1.0f);
+}
+
+// `tail` selects the scalar-tail form: element e of an n-element SIMD call is a tail
+// element iff e >= (n & ~7).
+__device__ __forceinline__ float den_of(float a, bool tail) { return tail ? den_tail(a) : den_body(a); }
+__device__ __forceinline__ float sigmoid_of(float x, bool tail) { return 1.0f / den_of(x, tail); }
+__device__ __forceinline__ float silu_of(float x, bool tail) { return x / den_of(x, tail); }
+__device__ __forceinline__ float swiglu_of(float a, float b, bool tail) { return (a / den_of(a, tail)) * b; }
+
+// ---- activation quantisers --------------------------------------------------------------
+// Q5.10 (simd.hpp:162-187). Body: _mm256_cvtps_epi32 semantics (out of int32 range or
+// NaN -> INT32_MIN) then clamp. Tail: nearbyintf, clamp in float, convert.
+__device__ __forceinline__ int32_t q510_body(float y, float qs) {
+  float v = y * qs;
+  int32_t r = (fabsf(v) < 2147483648.0f) ? static_cast<int32_t>(rintf(v)) : INT32_MIN;
+  return r < -32768 ? -32768 : (r > 32767 ? 32767 : r);
+}
+__device__ __forceinline__ int32_t q510_tail(float y, float qs) {
+  float v = rintf(y * qs);
+  if (v > 32767.0f) v = 32767.0f;
+  else if (v < -32768.0f) v = -32768.0f;
+  return (v != v) ? INT32_MIN : static_cast<int32_t>(v);
+}
+// int8 absmax (tools/reference.py:131-135): q = clamp(round_half_even(y * scale_a), -128, 127)
+__device__ __forceinline__ int32_t q8_of(float y, float sa) {
+  float v = rintf(y * sa);
+  v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+  return static_cast<int32_t>(v);
+}
+
+// Argmax key: order-preserving float bits in the high word (-0 folded onto +0, which the
+// reference's `>` cannot tell apart), 0xFFFFFFFF - index in the low word, so the largest key
+// is the first index of the largest value (hgrn_model.cpp:270-273).
+__device__ __forceinline__ unsigned long long amax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(idx));
+}
+
+}  // namespace mmf

@@ -1,0 +1,1081 @@
+// mmf_host.cpp -- host side of libmmfree_hip.so: the C ABI of include/mmfree_hip.h.
+//
+// Owns the device state of one engine instance: resident 2-bit projections, the model's
+// fp32 tensors, the recurrent state and scratch, and the single-row decode plan (4 fused
+// launches per layer + the lm_head, captured once into a HIP graph and replayed per
+// token). Prefill, batched serving steps and the stateless forward run the row kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/mmfree_hip.h"
+#include "mmf_internal.hpp"
+
+using namespace mmf;
+
+namespace {
+
+struct Err {
+  int code;
+  std::string msg;
+};
+
+#define MMF_HIP(expr)                                                                     \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      throw Err{MMF_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)};          \
+  } while (0)
+
+[[noreturn]] void fail(int code, const std::string& m) { throw Err{code, m}; }
+
+// Grow-only device buffer.
+struct DBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  void* get(size_t bytes) {
+    if (bytes > n) {
+      if (p) MMF_HIP(hipFree(p));
+      p = nullptr;
+      n = 0;
+      MMF_HIP(hipMalloc(&p, bytes));
+      n = bytes;
+    }
+    return p;
+  }
+  template <class T> T* as(size_t count) { return static_cast<T*>(get(count * sizeof(T))); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+struct Proj {
+  ProjDev d;
+  void* mem = nullptr;  // pk | tail | rowsum | normw in one allocation
+};
+
+struct DevTensor {
+  void* p = nullptr;
+  std::vector<size_t> shape;
+  int dtype = 0;  // 0 f32, 1 i8
+  int proj = -1;  // for ".wq": index into ctx->projs
+  std::vector<float> host_small;  // f32 tensors of <= 16 elements (scale_w)
+  size_t numel() const {
+    size_t n = 1;
+    for (auto s : shape) n *= s;
+    return shape.empty() ? 0 : n;
+  }
+};
+
+struct LayerDev {
+  int proj[6];
+  const float *attn = nullptr, *mlp = nullptr, *gn = nullptr, *lb = nullptr;
+};
+
+// Scratch for row (multi-token) passes.
+struct RowScratch {
+  DBuf ids, h, resid, i, f, g, recur, scan, z, logits, state0, am;
+  DBuf acty, actq, actct, actsa;
+};
+
+struct Model {
+  mmf_config cfg{};
+  bool begun = false, finalized = false;
+  int mode = kFloat, frac = 10;
+  float qs = 1024.0f;
+  std::unordered_map<std::string, DevTensor> tensors;
+  const float* emb = nullptr;
+  const float* norm_w = nullptr;
+  int lm = -1;
+  std::vector<LayerDev> layers;
+  // decode buffers (single row)
+  DBuf h, resid, g, recur, z, logits, key, hist, hist_pos;
+  size_t hist_cap = 0;
+  DBuf state;  // [L][B][H]
+  size_t streams = 0;
+  RowScratch rs;
+  // decode graph
+  hipGraphExec_t graph = nullptr;
+  bool graph_tried = false;
+};
+
+}  // namespace
+
+struct mmf_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::vector<Proj> projs;
+  Model model;
+  DBuf raw;  // staging for int8 weights before the repack
+  DBuf opy, opq, opct, opsa, opstate;
+  hipDeviceProp_t prop{};
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+template <class F>
+int guard(mmf_ctx* ctx, F&& f) {
+  if (!ctx) return MMF_ERR_ARG;
+  try {
+    MMF_HIP(hipSetDevice(ctx->device));
+    f();
+    return MMF_OK;
+  } catch (const Err& e) {
+    ctx->err = e.msg;
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    ctx->err = "out of host memory";
+    return MMF_ERR_ARG;
+  } catch (const std::exception& e) {
+    ctx->err = e.what();
+    return MMF_ERR_ARG;
+  }
+}
+
+const Proj& proj_of(mmf_ctx* c, int id) {
+  if (id < 0 || id >= static_cast<int>(c->projs.size())) fail(MMF_ERR_ARG, "invalid proj_id " + std::to_string(id));
+  return c->projs[id];
+}
+
+float inv_fixed_of(float scale_w, int frac) {
+  const float qs = static_cast<float>(1u << frac);
+  return 1.0f / (qs * scale_w);  // bitlinear.cpp:29-30
+}
+
+int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float scale_w, const float* normw_host,
+                  const float* normw_dev) {
+  if (N == 0 || K == 0 || N > (1u << 30) || K > (1u << 20)) fail(MMF_ERR_ARG, "invalid projection shape");
+  Proj P;
+  P.d.g = make_geom(static_cast<int>(N), static_cast<int>(K));
+  const Geom& g = P.d.g;
+  const size_t words = static_cast<size_t>(g.ngroups) * g.Wc * kGroup * 8;
+  const size_t npad = static_cast<size_t>(g.ngroups) * kGroup;
+  const size_t b_pk = words * 4, b_tail = npad * 8, b_rs = npad * 4, b_nw = normw_host ? K * 4 : 0;
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  MMF_HIP(hipMalloc(&P.mem, al(b_pk) + al(b_tail) + al(b_rs) + al(b_nw) + 256));
+  char* base = static_cast<char*>(P.mem);
+  P.d.pk = reinterpret_cast<uint32_t*>(base);
+  P.d.tail = reinterpret_cast<int8_t*>(base + al(b_pk));
+  P.d.rowsum = reinterpret_cast<int32_t*>(base + al(b_pk) + al(b_tail));
+  float* nw = reinterpret_cast<float*>(base + al(b_pk) + al(b_tail) + al(b_rs));
+  if (normw_host) {
+    MMF_HIP(hipMemcpy(nw, normw_host, b_nw, hipMemcpyHostToDevice));
+    P.d.normw = nw;
+  } else {
+    P.d.normw = normw_dev;
+  }
+  P.d.scale_w = scale_w;
+  P.d.inv_scale_w = 1.0f / scale_w;  // bitlinear.cpp:28
+  P.d.inv_fixed = inv_fixed_of(scale_w, 10);
+  hipError_t e = launch_pack(wq_dev, g, const_cast<uint32_t*>(P.d.pk), const_cast<int8_t*>(P.d.tail),
+                             const_cast<int32_t*>(P.d.rowsum), c->stream);
+  if (e == hipErrorInvalidValue) {
+    (void)hipFree(P.mem);
+    fail(MMF_ERR_ARG, "projection weights must be ternary (-1, 0, +1)");
+  }
+  MMF_HIP(e);
+  c->projs.push_back(P);
+  return static_cast<int>(c->projs.size() - 1);
+}
+
+// ---- activation buffers ---------------------------------------------------------------
+ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, int rows, int na) {
+  ActBuf a;
+  a.Lc = g.Lc;
+  a.K = g.K;
+  a.K8 = g.K8;
+  a.nb = g.nb;
+  a.ntail = g.ntail;
+  a.rows = rows;
+  a.na = na;
+  const size_t nr = static_cast<size_t>(rows) * na;
+  if (mode == kFloat) {
+    a.y = y.as<float>(nr * a.ystride());
+  } else {
+    a.q = q.as<int8_t>(nr * a.qstride());
+    a.ct = ct.as<int32_t>(nr * 8);
+    a.sa = sa.as<float>(nr);
+  }
+  return a;
+}
+
+GemmArgs gemm_args(mmf_ctx* c, const int* ids, int n, int rows, Mode mode, int frac) {
+  GemmArgs a{};
+  a.nmat = n;
+  a.rows = rows;
+  a.mode = mode;
+  for (int z = 0; z < n; ++z) {
+    a.p[z] = proj_of(c, ids[z]).d;
+    a.inv_fixed[z] = inv_fixed_of(a.p[z].scale_w, frac);
+  }
+  a.epi = kEpiStore;
+  return a;
+}
+
+// ---- model helpers -------------------------------------------------------------------
+Model& model_of(mmf_ctx* c) {
+  if (!c->model.finalized) fail(MMF_ERR_STATE, "no model: call mmf_model_begin/tensor/finalize first");
+  return c->model;
+}
+
+const DevTensor& tensor_of(Model& m, const std::string& name) {
+  auto it = m.tensors.find(name);
+  if (it == m.tensors.end()) fail(MMF_ERR_MISSING, "weights: missing tensor " + name);
+  return it->second;
+}
+
+void check_shape(const DevTensor& t, const std::string& name, std::vector<size_t> want) {
+  if (t.shape != want) {
+    std::string s = "weights: tensor " + name + " has shape [";
+    for (size_t i = 0; i < t.shape.size(); ++i) s += (i ? "," : "") + std::to_string(t.shape[i]);
+    fail(MMF_ERR_ARG, s + "], expected another");
+  }
+}
+
+void check_ids(const Model& m, const int64_t* ids, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || static_cast<size_t>(ids[i]) >= m.cfg.vocab_size)
+      fail(MMF_ERR_ARG, "token id " + std::to_string(ids[i]) + " outside the vocabulary");
+}
+
+void alloc_decode(Model& m) {
+  const size_t H = m.cfg.hidden_size, I = m.cfg.intermediate_size, V = m.cfg.vocab_size;
+  m.h.as<float>(H);
+  m.resid.as<float>(H);
+  m.g.as<float>(H);
+  m.recur.as<float>(H);
+  m.z.as<float>(I);
+  m.logits.as<float>(V);
+  m.key.as<unsigned long long>(1);
+  m.hist_pos.as<int32_t>(1);
+}
+
+// One layer over `rows` rows with the row kernels. h [rows, H] in/out; state: this
+// layer's state ([H] time scan or [rows, H] streams); internals (may be null): device
+// [5][rows][H] copy targets for the trace.
+void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, bool stream_state,
+                float* trace_dev) {
+  const int H = static_cast<int>(m.cfg.hidden_size), I = static_cast<int>(m.cfg.intermediate_size);
+  const Mode mode = static_cast<Mode>(m.mode);
+  const LayerDev& L = m.layers[l];
+  RowScratch& s = m.rs;
+  hipStream_t st = c->stream;
+  float* ib = s.i.as<float>(static_cast<size_t>(rows) * H);
+  float* fb = s.f.as<float>(static_cast<size_t>(rows) * H);
+  float* gb = s.g.as<float>(static_cast<size_t>(rows) * H);
+  float* rb = s.recur.as<float>(static_cast<size_t>(rows) * H);
+  float* resid = s.resid.as<float>(static_cast<size_t>(rows) * H);
+  float* zb = s.z.as<float>(static_cast<size_t>(rows) * I * 2);
+  float* scan = trace_dev ? s.scan.as<float>(static_cast<size_t>(rows) * H) : nullptr;
+
+  // attention: attn_norm -> i/f/g BitLinears (hgrn_model.cpp:95-107)
+  {
+    const Geom& g = proj_of(c, L.proj[0]).d.g;
+    ActBuf act = make_act(s.acty, s.actq, s.actct, s.actsa, mode, g, rows, 3);
+    PrologueArgs pa{};
+    pa.x = h;
+    pa.pre = kPreNorm;
+    pa.pre_w = L.attn;
+    pa.na = 3;
+    for (int k = 0; k < 3; ++k) pa.normw[k] = proj_of(c, L.proj[k]).d.normw;
+    pa.eps = m.cfg.rms_norm_eps;
+    pa.qs = m.qs;
+    MMF_HIP(launch_prologue(mode, pa, act, st));
+    GemmArgs ga = gemm_args(c, L.proj, 3, rows, mode, m.frac);
+    ga.out[0] = ib;
+    ga.out[1] = fb;
+    ga.out[2] = gb;
+    MMF_HIP(launch_gemm(ga, act, st));
+  }
+  // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
+  MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, st));
+  if (trace_dev) {
+    const size_t n = static_cast<size_t>(rows) * H * sizeof(float);
+    MMF_HIP(hipMemcpyAsync(trace_dev + 0 * rows * H, ib, n, hipMemcpyDeviceToDevice, st));
+    MMF_HIP(hipMemcpyAsync(trace_dev + 1 * rows * H, fb, n, hipMemcpyDeviceToDevice, st));
+    MMF_HIP(hipMemcpyAsync(trace_dev + 2 * rows * H, gb, n, hipMemcpyDeviceToDevice, st));
+    MMF_HIP(hipMemcpyAsync(trace_dev + 3 * static_cast<size_t>(rows) * H, scan, n, hipMemcpyDeviceToDevice, st));
+    MMF_HIP(hipMemcpyAsync(trace_dev + 4 * static_cast<size_t>(rows) * H, rb, n, hipMemcpyDeviceToDevice, st));
+  }
+  // g_norm -> o_proj -> resid = h + o (hgrn_model.cpp:153-166)
+  {
+    const Geom& g = proj_of(c, L.proj[3]).d.g;
+    ActBuf act = make_act(s.acty, s.actq, s.actct, s.actsa, mode, g, rows, 1);
+    PrologueArgs pa{};
+    pa.x = gb;
+    pa.x2 = rb;
+    pa.pre = kPreSwish;
+    pa.pre_w = L.gn;
+    pa.na = 1;
+    pa.normw[0] = proj_of(c, L.proj[3]).d.normw;
+    pa.eps = m.cfg.rms_norm_eps;
+    pa.qs = m.qs;
+    MMF_HIP(launch_prologue(mode, pa, act, st));
+    GemmArgs ga = gemm_args(c, &L.proj[3], 1, rows, mode, m.frac);
+    ga.epi = kEpiAdd;
+    ga.add = h;
+    ga.out[0] = resid;
+    MMF_HIP(launch_gemm(ga, act, st));
+  }
+  // mlp_norm -> gate_proj -> swiglu (hgrn_model.cpp:167-185)
+  {
+    const Geom& g = proj_of(c, L.proj[4]).d.g;
+    ActBuf act = make_act(s.acty, s.actq, s.actct, s.actsa, mode, g, rows, 1);
+    PrologueArgs pa{};
+    pa.x = resid;
+    pa.pre = kPreNorm;
+    pa.pre_w = L.mlp;
+    pa.na = 1;
+    pa.normw[0] = proj_of(c, L.proj[4]).d.normw;
+    pa.eps = m.cfg.rms_norm_eps;
+    pa.qs = m.qs;
+    MMF_HIP(launch_prologue(mode, pa, act, st));
+    GemmArgs ga = gemm_args(c, &L.proj[4], 1, rows, mode, m.frac);
+    ga.epi = kEpiSwigluPair;
+    ga.out[0] = zb;
+    ga.swiglu_n = rows * I;
+    MMF_HIP(launch_gemm(ga, act, st));
+  }
+  // down_proj -> h = resid + d (hgrn_model.cpp:187-194)
+  {
+    const Geom& g = proj_of(c, L.proj[5]).d.g;
+    ActBuf act = make_act(s.acty, s.actq, s.actct, s.actsa, mode, g, rows, 1);
+    PrologueArgs pa{};
+    pa.x = zb;
+    pa.pre = kPreNone;
+    pa.na = 1;
+    pa.normw[0] = proj_of(c, L.proj[5]).d.normw;
+    pa.eps = m.cfg.rms_norm_eps;
+    pa.qs = m.qs;
+    MMF_HIP(launch_prologue(mode, pa, act, st));
+    GemmArgs ga = gemm_args(c, &L.proj[5], 1, rows, mode, m.frac);
+    ga.epi = kEpiAdd;
+    ga.add = resid;
+    ga.out[0] = h;
+    MMF_HIP(launch_gemm(ga, act, st));
+  }
+}
+
+// Final norm + lm_head over rows (hgrn_model.cpp:235,245,440-441) -> logits [rows, V].
+void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
+  const Mode mode = static_cast<Mode>(m.mode);
+  RowScratch& s = m.rs;
+  const Geom& g = proj_of(c, m.lm).d.g;
+  ActBuf act = make_act(s.acty, s.actq, s.actct, s.actsa, mode, g, rows, 1);
+  PrologueArgs pa{};
+  pa.x = h;
+  pa.pre = kPreNorm;
+  pa.pre_w = m.norm_w;
+  pa.na = 1;
+  pa.normw[0] = proj_of(c, m.lm).d.normw;
+  pa.eps = m.cfg.rms_norm_eps;
+  pa.qs = m.qs;
+  MMF_HIP(launch_prologue(mode, pa, act, c->stream));
+  GemmArgs ga = gemm_args(c, &m.lm, 1, rows, mode, m.frac);
+  ga.out[0] = logits;
+  MMF_HIP(launch_gemm(ga, act, c->stream));
+}
+
+DecArgs dec_base(Model& m) {
+  DecArgs a{};
+  a.H = static_cast<int>(m.cfg.hidden_size);
+  a.I = static_cast<int>(m.cfg.intermediate_size);
+  a.vocab = static_cast<int>(m.cfg.vocab_size);
+  a.eps = m.cfg.rms_norm_eps;
+  a.qs = m.qs;
+  a.emb = m.emb;
+  a.key = m.key.as<unsigned long long>(1);
+  return a;
+}
+
+void set_proj(mmf_ctx* c, Model& m, DecArgs& a, int slot, int id) {
+  a.p[slot] = proj_of(c, id).d;
+  a.inv_fixed[slot] = inv_fixed_of(a.p[slot].scale_w, m.frac);
+}
+
+// Single-row lm_head on device row x: logits (may be null) and, if want_key, the argmax
+// key (atomicMax into a cleared key).
+void lm_single(mmf_ctx* c, Model& m, const float* x, float* logits, bool want_key) {
+  DecArgs a = dec_base(m);
+  set_proj(c, m, a, 0, m.lm);
+  a.x = x;
+  a.pre_w = m.norm_w;
+  a.out = logits;
+  if (!want_key) a.key = nullptr;
+  MMF_HIP(launch_decode(kLM, static_cast<Mode>(m.mode), a, c->stream));
+}
+
+// One single-row decode step for stream 0: reads the token from the argmax key, writes the
+// next key. `kinds` masks which kernel kinds run (timing), `first_from_key` selects the
+// embedding gather of layer 0.
+void decode_launches(mmf_ctx* c, Model& m, unsigned kinds = 0x1F) {
+  const Mode mode = static_cast<Mode>(m.mode);
+  const size_t H = m.cfg.hidden_size;
+  float* h = m.h.as<float>(H);
+  float* resid = m.resid.as<float>(H);
+  float* g = m.g.as<float>(H);
+  float* recur = m.recur.as<float>(H);
+  float* z = m.z.as<float>(m.cfg.intermediate_size);
+  float* state = static_cast<float*>(m.state.p);
+  for (size_t l = 0; l < m.layers.size(); ++l) {
+    const LayerDev& L = m.layers[l];
+    if (kinds & 1) {
+      DecArgs a = dec_base(m);
+      for (int k = 0; k < 3; ++k) set_proj(c, m, a, k, L.proj[k]);
+      a.layer = static_cast<int>(l);
+      a.x = (l == 0 && kinds == 0x1F) ? nullptr : h;
+      if (a.x == nullptr) {
+        a.out = h;  // layer 0: the embedding row becomes h
+        a.hist = m.hist.as<int64_t>(1);
+        a.hist_pos = m.hist_pos.as<int32_t>(1);
+        a.hist_cap = static_cast<int>(m.hist_cap);
+      }
+      a.pre_w = L.attn;
+      a.lb = L.lb;
+      a.state = state + l * H;
+      a.recur = recur;
+      a.gout = g;
+      MMF_HIP(launch_decode(kIFG, mode, a, c->stream));
+    }
+    if (kinds & 2) {
+      DecArgs a = dec_base(m);
+      set_proj(c, m, a, 0, L.proj[3]);
+      a.x = g;
+      a.x2 = recur;
+      a.pre_w = L.gn;
+      a.hin = h;
+      a.out = resid;
+      if (l == 0 && kinds == 0x1F) a.key_reset = a.key;
+      MMF_HIP(launch_decode(kO, mode, a, c->stream));
+    }
+    if (kinds & 4) {
+      DecArgs a = dec_base(m);
+      set_proj(c, m, a, 0, L.proj[4]);
+      a.x = resid;
+      a.pre_w = L.mlp;
+      a.out = z;
+      MMF_HIP(launch_decode(kGate, mode, a, c->stream));
+    }
+    if (kinds & 8) {
+      DecArgs a = dec_base(m);
+      set_proj(c, m, a, 0, L.proj[5]);
+      a.x = z;
+      a.hin = resid;
+      a.out = h;
+      MMF_HIP(launch_decode(kDown, mode, a, c->stream));
+    }
+  }
+  if (kinds & 16) lm_single(c, m, h, nullptr, true);
+}
+
+void decode_step(mmf_ctx* c, Model& m) {
+  static const bool use_graph = [] {
+    const char* e = std::getenv("MMF_GRAPH");
+    return !(e && std::strcmp(e, "0") == 0);
+  }();
+  if (use_graph && !m.graph_tried) {
+    m.graph_tried = true;
+    hipGraph_t gr = nullptr;
+    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+      bool ok = true;
+      try {
+        decode_launches(c, m);
+      } catch (const Err&) {
+        ok = false;
+      }
+      if (hipStreamEndCapture(c->stream, &gr) != hipSuccess) ok = false;
+      if (ok && gr && hipGraphInstantiate(&m.graph, gr, nullptr, nullptr, 0) != hipSuccess) {
+        m.graph = nullptr;
+      }
+      if (gr) (void)hipGraphDestroy(gr);
+    }
+    (void)hipGetLastError();
+  }
+  if (m.graph) {
+    MMF_HIP(hipGraphLaunch(m.graph, c->stream));
+  } else {
+    decode_launches(c, m);
+  }
+}
+
+void drop_graph(Model& m) {
+  if (m.graph) (void)hipGraphExecDestroy(m.graph);
+  m.graph = nullptr;
+  m.graph_tried = false;
+}
+
+void reset_state(mmf_ctx* c, Model& m, size_t B) {
+  const size_t n = m.cfg.num_hidden_layers * B * m.cfg.hidden_size;
+  void* old = m.state.p;
+  m.state.as<float>(n);
+  if (m.state.p != old) drop_graph(m);  // the graph holds the state pointer
+  MMF_HIP(hipMemsetAsync(m.state.p, 0, n * sizeof(float), c->stream));
+  m.streams = B;
+}
+
+// Prefill T ids of stream b (time scan) and leave the final hidden rows in rs.h.
+float* prefill_rows(mmf_ctx* c, Model& m, size_t b, const int64_t* ids, size_t T, float* trace_h,
+                    float* trace_state, float* trace_int) {
+  check_ids(m, ids, T);
+  const size_t H = m.cfg.hidden_size, L = m.cfg.num_hidden_layers, B = m.streams;
+  RowScratch& s = m.rs;
+  int64_t* dids = s.ids.as<int64_t>(T);
+  MMF_HIP(hipMemcpyAsync(dids, ids, T * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+  float* h = s.h.as<float>(T * H);
+  MMF_HIP(launch_embed(m.emb, dids, h, static_cast<int>(T), static_cast<int>(H), c->stream));
+  float* tint = nullptr;
+  DBuf tbuf;
+  if (trace_int) tint = tbuf.as<float>(5 * T * H);
+  for (size_t l = 0; l < L; ++l) {
+    float* st = static_cast<float*>(m.state.p) + (l * B + b) * H;
+    layer_rows(c, m, static_cast<int>(l), static_cast<int>(T), h, st, false, tint);
+    if (trace_h)
+      MMF_HIP(hipMemcpyAsync(trace_h + l * T * H, h, T * H * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    if (trace_state)
+      MMF_HIP(hipMemcpyAsync(trace_state + l * H, st, H * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    if (trace_int) {
+      MMF_HIP(hipMemcpyAsync(trace_int + l * 5 * T * H, tint, 5 * T * H * sizeof(float), hipMemcpyDeviceToHost,
+                             c->stream));
+      MMF_HIP(hipStreamSynchronize(c->stream));
+    }
+  }
+  if (trace_int || trace_h || trace_state) MMF_HIP(hipStreamSynchronize(c->stream));
+  tbuf.release();
+  return h;
+}
+
+int64_t read_key(mmf_ctx* c, Model& m) {
+  unsigned long long k = 0;
+  MMF_HIP(hipMemcpyAsync(&k, m.key.p, sizeof(k), hipMemcpyDeviceToHost, c->stream));
+  MMF_HIP(hipStreamSynchronize(c->stream));
+  return key_index(k);
+}
+
+void clear_key(mmf_ctx* c, Model& m) {
+  MMF_HIP(hipMemsetAsync(m.key.p, 0, sizeof(unsigned long long), c->stream));
+  MMF_HIP(hipMemsetAsync(m.hist_pos.p, 0, sizeof(int32_t), c->stream));
+}
+
+}  // namespace
+
+// =========================================================================================
+// C ABI
+// =========================================================================================
+extern "C" {
+
+int mmf_create(mmf_ctx** out, int device) {
+  if (!out) return MMF_ERR_ARG;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) {
+    g_create_err = "no HIP device " + std::to_string(device);
+    return MMF_ERR_NODEV;
+  }
+  hipDeviceProp_t prop{};
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+    g_create_err = "hipGetDeviceProperties failed";
+    return MMF_ERR_NODEV;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    g_create_err = std::string("device is ") + prop.gcnArchName + ", this build targets gfx950";
+    return MMF_ERR_NODEV;
+  }
+  auto* c = new (std::nothrow) mmf_ctx;
+  if (!c) return MMF_ERR_ARG;
+  c->device = device;
+  c->prop = prop;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    g_create_err = "stream creation failed";
+    delete c;
+    return MMF_ERR_HIP;
+  }
+  *out = c;
+  return MMF_OK;
+}
+
+void mmf_destroy(mmf_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  drop_graph(c->model);
+  for (auto& p : c->projs) (void)hipFree(p.mem);
+  for (auto& kv : c->model.tensors)
+    if (kv.second.p) (void)hipFree(kv.second.p);
+  Model& m = c->model;
+  for (DBuf* b : {&m.h, &m.resid, &m.g, &m.recur, &m.z, &m.logits, &m.key, &m.hist, &m.hist_pos, &m.state})
+    b->release();
+  RowScratch& s = m.rs;
+  for (DBuf* b : {&s.ids, &s.h, &s.resid, &s.i, &s.f, &s.g, &s.recur, &s.scan, &s.z, &s.logits, &s.state0, &s.am,
+                  &s.acty, &s.actq, &s.actct, &s.actsa})
+    b->release();
+  for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate}) b->release();
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* mmf_last_error(const mmf_ctx* c) { return c ? c->err.c_str() : g_create_err.c_str(); }
+
+int mmf_sync(mmf_ctx* c) {
+  return guard(c, [&] { MMF_HIP(hipStreamSynchronize(c->stream)); });
+}
+
+void* mmf_stream(mmf_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int mmf_device_info(mmf_ctx* c, char* name, size_t cap, int* cus) {
+  return guard(c, [&] {
+    if (name && cap) {
+      std::snprintf(name, cap, "%s (%s)", c->prop.name, c->prop.gcnArchName);
+    }
+    if (cus) *cus = c->prop.multiProcessorCount;
+  });
+}
+
+int mmf_malloc(mmf_ctx* c, void** dev, size_t bytes) {
+  return guard(c, [&] {
+    if (!dev) fail(MMF_ERR_ARG, "null out pointer");
+    MMF_HIP(hipMalloc(dev, bytes ? bytes : 1));
+  });
+}
+
+int mmf_free(mmf_ctx* c, void* dev) {
+  return guard(c, [&] { MMF_HIP(hipFree(dev)); });
+}
+
+int mmf_upload(mmf_ctx* c, void* dev, const void* host, size_t bytes) {
+  return guard(c, [&] {
+    MMF_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_download(mmf_ctx* c, void* host, const void* dev, size_t bytes) {
+  return guard(c, [&] {
+    MMF_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_proj_register(mmf_ctx* c, const int8_t* wq, size_t N, size_t K, float scale_w, const float* normw,
+                      int* proj_id) {
+  return guard(c, [&] {
+    if (!wq || !proj_id) fail(MMF_ERR_ARG, "null argument");
+    void* raw = c->raw.get(N * K);
+    MMF_HIP(hipMemcpyAsync(raw, wq, N * K, hipMemcpyHostToDevice, c->stream));
+    *proj_id = register_proj(c, static_cast<const int8_t*>(raw), N, K, scale_w, normw, nullptr);
+  });
+}
+
+int mmf_proj_shape(mmf_ctx* c, int id, size_t* N, size_t* K) {
+  return guard(c, [&] {
+    const Proj& p = proj_of(c, id);
+    if (N) *N = p.d.g.N;
+    if (K) *K = p.d.g.K;
+  });
+}
+
+int mmf_ternary_matmul(mmf_ctx* c, int id, const int32_t* x, int32_t* acc, size_t b) {
+  return guard(c, [&] {
+    if (b == 0) return;
+    const Proj& p = proj_of(c, id);
+    ActBuf act = make_act(c->opy, c->opq, c->opct, c->opsa, kFixed, p.d.g, static_cast<int>(b), 1);
+    MMF_HIP(launch_codes_to_planes(x, act, c->stream));
+    GemmArgs ga = gemm_args(c, &id, 1, static_cast<int>(b), kFixed, 10);
+    ga.raw_acc = true;
+    ga.acc[0] = acc;
+    MMF_HIP(launch_gemm(ga, act, c->stream));
+  });
+}
+
+static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac, float eps, const float* x,
+                           float* const* outs, size_t rows, int32_t* acc) {
+  if (k < 1 || k > 3) fail(MMF_ERR_ARG, "cluster size must be 1..3");
+  if (mode < 0 || mode > 2) fail(MMF_ERR_ARG, "invalid mode");
+  if (frac < 0 || frac > 30) fail(MMF_ERR_ARG, "invalid frac_bits");
+  if (rows == 0) return;
+  const Proj& p0 = proj_of(c, ids[0]);
+  for (int z = 0; z < k; ++z) {
+    const Proj& p = proj_of(c, ids[z]);
+    if (p.d.g.N != p0.d.g.N || p.d.g.K != p0.d.g.K) fail(MMF_ERR_ARG, "cluster projections differ in shape");
+    if (!p.d.normw) fail(MMF_ERR_ARG, "projection registered without a norm weight");
+  }
+  ActBuf act = make_act(c->opy, c->opq, c->opct, c->opsa, static_cast<Mode>(mode), p0.d.g, static_cast<int>(rows), k);
+  PrologueArgs pa{};
+  pa.x = x;
+  pa.pre = kPreNone;
+  pa.na = k;
+  for (int z = 0; z < k; ++z) pa.normw[z] = proj_of(c, ids[z]).d.normw;
+  pa.eps = eps;
+  pa.qs = static_cast<float>(1u << frac);
+  MMF_HIP(launch_prologue(static_cast<Mode>(mode), pa, act, c->stream));
+  GemmArgs ga = gemm_args(c, ids, k, static_cast<int>(rows), static_cast<Mode>(mode), frac);
+  for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
+  ga.acc[0] = acc;
+  MMF_HIP(launch_gemm(ga, act, c->stream));
+}
+
+int mmf_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out, size_t rows,
+                  int32_t* acc) {
+  return guard(c, [&] { bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, acc); });
+}
+
+int mmf_bitlinear_cluster(mmf_ctx* c, const int* ids, int k, int mode, int frac, float eps, const float* x,
+                          float* const* outs, size_t rows) {
+  return guard(c, [&] {
+    if (!ids || !outs) fail(MMF_ERR_ARG, "null argument");
+    bitlinear_impl(c, ids, k, mode, frac, eps, x, outs, rows, nullptr);
+  });
+}
+
+int mmf_rmsnorm(mmf_ctx* c, float* y, const float* x, const float* w, size_t rows, size_t cols, float eps) {
+  return guard(c, [&] {
+    if (rows && cols) MMF_HIP(launch_rmsnorm(x, w, y, static_cast<int>(rows), static_cast<int>(cols), eps, c->stream));
+  });
+}
+
+int mmf_swiglu(mmf_ctx* c, float* out, const float* a, const float* b, size_t n) {
+  return guard(c, [&] {
+    if (n) MMF_HIP(launch_swiglu(a, b, out, n, c->stream));
+  });
+}
+
+int mmf_hgrn_scan(mmf_ctx* c, float* out, const float* i, const float* f, size_t T, size_t D, float* state) {
+  return guard(c, [&] {
+    if (T && D) MMF_HIP(launch_scan(i, f, out, state, static_cast<int>(T), static_cast<int>(D), c->stream));
+  });
+}
+
+int mmf_rmsnorm_swishgate(mmf_ctx* c, float* out, const float* g, const float* o, const float* w, size_t rows,
+                          size_t cols, float eps) {
+  return guard(c, [&] {
+    if (rows && cols)
+      MMF_HIP(launch_swishgate(g, o, w, out, static_cast<int>(rows), static_cast<int>(cols), eps, c->stream));
+  });
+}
+
+// ---- model ------------------------------------------------------------------------------
+int mmf_model_begin(mmf_ctx* c, const mmf_config* cfg) {
+  return guard(c, [&] {
+    if (!cfg || !cfg->vocab_size || !cfg->hidden_size || !cfg->num_hidden_layers || !cfg->intermediate_size)
+      fail(MMF_ERR_ARG, "invalid config");
+    if (c->model.begun) fail(MMF_ERR_STATE, "a model was already begun on this context");
+    c->model.cfg = *cfg;
+    c->model.begun = true;
+  });
+}
+
+int mmf_model_tensor(mmf_ctx* c, const char* name, int dtype, const size_t* shape, int ndim, const void* data) {
+  return guard(c, [&] {
+    Model& m = c->model;
+    if (!m.begun || m.finalized) fail(MMF_ERR_STATE, "mmf_model_tensor outside begin/finalize");
+    if (!name || !data || ndim < 0 || ndim > 4 || (dtype != 0 && dtype != 1)) fail(MMF_ERR_ARG, "invalid tensor");
+    DevTensor t;
+    t.dtype = dtype;
+    t.shape.assign(shape, shape + ndim);
+    const size_t bytes = t.numel() * (dtype == 0 ? 4 : 1);
+    const std::string nm(name);
+    const bool is_wq = nm.size() > 3 && nm.compare(nm.size() - 3, 3, ".wq") == 0;
+    if (is_wq) {
+      if (dtype != 1 || ndim != 2) fail(MMF_ERR_ARG, "weights: " + nm + " must be a 2-D i8 tensor");
+      void* raw = c->raw.get(bytes);
+      MMF_HIP(hipMemcpyAsync(raw, data, bytes, hipMemcpyHostToDevice, c->stream));
+      t.proj = register_proj(c, static_cast<const int8_t*>(raw), t.shape[0], t.shape[1], 1.0f, nullptr, nullptr);
+    } else {
+      MMF_HIP(hipMalloc(&t.p, bytes ? bytes : 1));
+      MMF_HIP(hipMemcpyAsync(t.p, data, bytes, hipMemcpyHostToDevice, c->stream));
+      MMF_HIP(hipStreamSynchronize(c->stream));
+      if (dtype == 0 && t.numel() <= 16) {
+        t.host_small.resize(t.numel());
+        std::memcpy(t.host_small.data(), data, bytes);
+      }
+    }
+    auto it = m.tensors.find(nm);
+    if (it != m.tensors.end()) {
+      if (it->second.p) (void)hipFree(it->second.p);
+      m.tensors.erase(it);
+    }
+    m.tensors.emplace(nm, std::move(t));
+  });
+}
+
+int mmf_model_finalize(mmf_ctx* c, int mode, int frac) {
+  return guard(c, [&] {
+    Model& m = c->model;
+    if (!m.begun) fail(MMF_ERR_STATE, "mmf_model_begin first");
+    if (mode < 0 || mode > 2) fail(MMF_ERR_ARG, "invalid mode");
+    if (frac < 0 || frac > 30) fail(MMF_ERR_ARG, "invalid frac_bits");
+    const size_t V = m.cfg.vocab_size, H = m.cfg.hidden_size, L = m.cfg.num_hidden_layers,
+                 I = m.cfg.intermediate_size;
+    if (I % 16 != 0) fail(MMF_ERR_ARG, "intermediate_size must be a multiple of 16");
+    auto f32 = [&](const std::string& n, std::vector<size_t> shape) -> const float* {
+      const DevTensor& t = tensor_of(m, n);
+      if (t.dtype != 0) fail(MMF_ERR_ARG, "weights: " + n + " must be f32");
+      check_shape(t, n, shape);
+      return static_cast<const float*>(t.p);
+    };
+    auto proj = [&](const std::string& tag, size_t N, size_t K) -> int {
+      const DevTensor& w = tensor_of(m, tag + ".wq");
+      check_shape(w, tag + ".wq", {N, K});
+      const DevTensor& sw = tensor_of(m, tag + ".scale_w");
+      if (sw.host_small.size() != 1) fail(MMF_ERR_ARG, "weights: " + tag + ".scale_w must hold one f32");
+      Proj& p = c->projs[w.proj];
+      p.d.scale_w = sw.host_small[0];
+      p.d.inv_scale_w = 1.0f / p.d.scale_w;
+      p.d.inv_fixed = inv_fixed_of(p.d.scale_w, frac);
+      p.d.normw = f32(tag + ".normw", {K});
+      return w.proj;
+    };
+    m.emb = f32("model.embeddings", {V, H});
+    m.norm_w = f32("model.norm.w", {H});
+    m.lm = proj("lm_head", V, H);
+    const float* lb = nullptr;
+    if (m.cfg.use_lower_bound) lb = f32("lower_bounds", {L, H});
+    m.layers.assign(L, LayerDev{});
+    static const char* names[6] = {"i_proj", "f_proj", "g_proj", "o_proj", "gate_proj", "down_proj"};
+    for (size_t l = 0; l < L; ++l) {
+      const std::string p = "model.layers." + std::to_string(l);
+      LayerDev& Ld = m.layers[l];
+      Ld.attn = f32(p + ".attn_norm.w", {H});
+      Ld.mlp = f32(p + ".mlp_norm.w", {H});
+      Ld.gn = f32(p + ".g_norm.w", {H});
+      for (int j = 0; j < 6; ++j) {
+        const size_t N = j == 4 ? 2 * I : H, K = j == 5 ? I : H;
+        Ld.proj[j] = proj(p + "." + names[j], N, K);
+      }
+      Ld.lb = (lb && l > 0) ? lb + l * H : nullptr;  // hgrn_model.cpp:116-117
+    }
+    m.mode = mode;
+    m.frac = frac;
+    m.qs = static_cast<float>(1u << frac);
+    alloc_decode(m);
+    m.finalized = true;
+    drop_graph(m);
+    reset_state(c, m, 1);
+    MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_model_config(mmf_ctx* c, mmf_config* cfg) {
+  return guard(c, [&] {
+    if (!cfg) fail(MMF_ERR_ARG, "null cfg");
+    *cfg = c->model.cfg;
+  });
+}
+
+int mmf_model_generate(mmf_ctx* c, const int64_t* ids, size_t n, size_t new_tokens, int64_t eos_id, int64_t* out,
+                       size_t cap, size_t* out_len, mmf_token_cb cb, void* user) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (!ids || n == 0) fail(MMF_ERR_ARG, "empty prompt");
+    if (!out || cap < n + new_tokens) fail(MMF_ERR_ARG, "output capacity below prompt + new_tokens");
+    std::memcpy(out, ids, n * sizeof(int64_t));
+    size_t len = n;
+    reset_state(c, m, 1);  // hgrn_model.cpp:315
+    if (new_tokens + 1 > m.hist_cap) {
+      m.hist.as<int64_t>(new_tokens + 1);
+      m.hist_cap = new_tokens + 1;
+      drop_graph(m);
+    }
+    clear_key(c, m);
+    float* h = prefill_rows(c, m, 0, ids, n, nullptr, nullptr, nullptr);
+    if (new_tokens == 0) {
+      if (out_len) *out_len = len;
+      return;
+    }
+    lm_single(c, m, h + (n - 1) * m.cfg.hidden_size, nullptr, true);
+    int64_t t = read_key(c, m);
+    out[len++] = t;
+    if (cb) cb(user, t);
+    if (t == eos_id) {
+      if (out_len) *out_len = len;
+      return;
+    }
+    const size_t rest = new_tokens - 1;
+    if (eos_id < 0) {
+      // no stop condition: run ahead in chunks, report tokens after each chunk
+      const size_t chunk = cb ? 16 : rest;
+      size_t done = 0;
+      std::vector<int64_t> hv;
+      while (done < rest) {
+        const size_t k = std::min(chunk, rest - done);
+        for (size_t s = 0; s < k; ++s) decode_step(c, m);
+        done += k;
+        // hist[0..done) = tokens consumed by the steps; the last produced one is in key
+        hv.resize(done);
+        MMF_HIP(hipMemcpyAsync(hv.data(), m.hist.p, done * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
+        const int64_t last = read_key(c, m);
+        for (size_t s = len - n; s < done; ++s) {
+          out[len++] = hv[s];
+          if (cb) cb(user, hv[s]);
+        }
+        (void)last;
+        if (done == rest) {
+          out[len++] = last;
+          if (cb) cb(user, last);
+        }
+      }
+    } else {
+      for (size_t s = 0; s < rest; ++s) {
+        decode_step(c, m);
+        t = read_key(c, m);
+        out[len++] = t;
+        if (cb) cb(user, t);
+        if (t == eos_id) break;
+      }
+    }
+    if (out_len) *out_len = len;
+  });
+}
+
+int mmf_model_reset(mmf_ctx* c, size_t streams) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (streams == 0) fail(MMF_ERR_ARG, "streams must be >= 1");
+    reset_state(c, m, streams);
+    if (m.hist_cap == 0) {
+      m.hist.as<int64_t>(1);
+      m.hist_cap = 1;
+    }
+    clear_key(c, m);
+  });
+}
+
+static void deliver_rows(mmf_ctx* c, Model& m, const float* logits_dev, size_t rows, float* logits, int64_t* argmax) {
+  const size_t V = m.cfg.vocab_size;
+  if (logits)
+    MMF_HIP(hipMemcpyAsync(logits, logits_dev, rows * V * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  if (argmax) {
+    int64_t* d = m.rs.am.as<int64_t>(rows);
+    MMF_HIP(launch_argmax_rows(logits_dev, static_cast<int>(rows), static_cast<int>(V), d, c->stream));
+    MMF_HIP(hipMemcpyAsync(argmax, d, rows * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
+  }
+  MMF_HIP(hipStreamSynchronize(c->stream));
+}
+
+int mmf_model_prefill(mmf_ctx* c, size_t stream, const int64_t* ids, size_t n, float* logits, int64_t* argmax) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (stream >= m.streams) fail(MMF_ERR_ARG, "stream index beyond mmf_model_reset's count");
+    if (!ids || n == 0) fail(MMF_ERR_ARG, "empty prompt");
+    float* h = prefill_rows(c, m, stream, ids, n, nullptr, nullptr, nullptr);
+    float* lg = m.logits.as<float>(m.cfg.vocab_size);
+    lm_single(c, m, h + (n - 1) * m.cfg.hidden_size, lg, false);
+    deliver_rows(c, m, lg, 1, logits, argmax);
+  });
+}
+
+int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* argmax) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    const size_t B = m.streams, H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    if (!tokens) fail(MMF_ERR_ARG, "null tokens");
+    check_ids(m, tokens, B);
+    RowScratch& s = m.rs;
+    int64_t* d = s.ids.as<int64_t>(B);
+    MMF_HIP(hipMemcpyAsync(d, tokens, B * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    float* h = s.h.as<float>(B * H);
+    MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
+    for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
+      layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H, true,
+                 nullptr);
+    float* lg = s.logits.as<float>(B * V);
+    lm_rows(c, m, static_cast<int>(B), h, lg);
+    deliver_rows(c, m, lg, B, logits, argmax);
+  });
+}
+
+int mmf_model_state(mmf_ctx* c, float* out) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    const size_t n = m.cfg.num_hidden_layers * m.streams * m.cfg.hidden_size;
+    MMF_HIP(hipMemcpyAsync(out, m.state.p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_model_forward(mmf_ctx* c, const int64_t* ids, size_t T, float* logits) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (!ids || T == 0 || !logits) fail(MMF_ERR_ARG, "invalid forward arguments");
+    check_ids(m, ids, T);
+    const size_t H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    RowScratch& s = m.rs;
+    int64_t* d = s.ids.as<int64_t>(T);
+    MMF_HIP(hipMemcpyAsync(d, ids, T * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    float* h = s.h.as<float>(T * H);
+    MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(T), static_cast<int>(H), c->stream));
+    float* st = s.state0.as<float>(H);
+    for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l) {
+      MMF_HIP(hipMemsetAsync(st, 0, H * sizeof(float), c->stream));  // fresh state (hgrn_model.cpp:233)
+      layer_rows(c, m, static_cast<int>(l), static_cast<int>(T), h, st, false, nullptr);
+    }
+    float* lg = s.logits.as<float>(T * V);
+    lm_rows(c, m, static_cast<int>(T), h, lg);
+    MMF_HIP(hipMemcpyAsync(logits, lg, T * V * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_model_trace(mmf_ctx* c, const int64_t* ids, size_t T, float* h, float* state, float* internals) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (!ids || T == 0 || !h || !state) fail(MMF_ERR_ARG, "invalid trace arguments");
+    reset_state(c, m, 1);
+    prefill_rows(c, m, 0, ids, T, h, state, internals);
+  });
+}
+
+int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, double* kind_us) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid reps");
+    if (m.streams != 1) reset_state(c, m, 1);
+    if (m.hist_cap < static_cast<size_t>(warmup + reps) + 1) {
+      m.hist.as<int64_t>(warmup + reps + 1);
+      m.hist_cap = warmup + reps + 1;
+      drop_graph(m);
+    }
+    clear_key(c, m);
+    hipEvent_t e0, e1;
+    MMF_HIP(hipEventCreate(&e0));
+    MMF_HIP(hipEventCreate(&e1));
+    for (int i = 0; i < warmup; ++i) decode_step(c, m);
+    MMF_HIP(hipEventRecord(e0, c->stream));
+    for (int i = 0; i < reps; ++i) decode_step(c, m);
+    MMF_HIP(hipEventRecord(e1, c->stream));
+    MMF_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    MMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    if (step_us) *step_us = 1000.0 * ms / reps;
+    if (kind_us) {
+      const double launches[5] = {static_cast<double>(m.layers.size()), static_cast<double>(m.layers.size()),
+                                  static_cast<double>(m.layers.size()), static_cast<double>(m.layers.size()), 1.0};
+      for (int k = 0; k < 5; ++k) {
+        decode_launches(c, m, 1u << k);  // warm
+        MMF_HIP(hipEventRecord(e0, c->stream));
+        for (int i = 0; i < reps; ++i) decode_launches(c, m, 1u << k);
+        MMF_HIP(hipEventRecord(e1, c->stream));
+        MMF_HIP(hipEventSynchronize(e1));
+        MMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+        kind_us[k] = 1000.0 * ms / (reps * launches[k]);
+      }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,167 @@
+// mmf_internal.hpp -- layouts and kernel launchers shared by the HIP sources.
+//
+// Device layout of a ternary projection wq [N, K] (int8 in the blob, nn.Linear layout):
+//   K8 = K & ~7 elements are split into 8 "chains" j = 0..7, chain j holding k = j + 8t
+//   for t < nb = K8/8 -- exactly the 8 AVX2 lanes of the reference dot products
+//   (simd.hpp:92-154), so a chain summed in t order is one reference lane. Chains are
+//   padded to Lc = roundup(nb, 16) codes (Wc = Lc/16 words, zero codes in the padding).
+//   Outputs are grouped by 16; group og's slab is contiguous:
+//       pk[((og * Wc + m) * 16 + ol) * 8 + j]   (word m of chain j of output og*16+ol)
+//   so a 128-thread block (16 outputs x 8 chains) streams one contiguous slab, 512 bytes
+//   per step. The K - K8 < 8 tail codes are kept as int8 tail[o * 8 + t]; rowsum[o] is the
+//   sum of the chain part of row o (for the split Q5.10 product).
+// Activations for one row use the same chain-transposed order: element k < K8 sits at
+// j * Lc + t (k = j + 8t), the tail after 8 * Lc.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace mmf {
+
+constexpr int kGroup = 16;  // outputs per slab
+constexpr int kBlock = 128; // threads of a GEMV block: 16 outputs x 8 chains
+
+enum Mode : int { kFloat = 0, kFixed = 1, kInt8 = 2 };
+
+struct Geom {
+  int N, K, K8, nb, ntail, Lc, Wc, ngroups;
+};
+
+__host__ __device__ inline Geom make_geom(int N, int K) {
+  Geom g;
+  g.N = N;
+  g.K = K;
+  g.K8 = K & ~7;
+  g.nb = g.K8 / 8;
+  g.ntail = K - g.K8;
+  g.Lc = (g.nb + 15) / 16 * 16;
+  if (g.Lc == 0) g.Lc = 16;
+  g.Wc = g.Lc / 16;
+  g.ngroups = (N + kGroup - 1) / kGroup;
+  return g;
+}
+
+// Device view of one resident projection.
+struct ProjDev {
+  const uint32_t* pk = nullptr;
+  const int8_t* tail = nullptr;
+  const int32_t* rowsum = nullptr;
+  const float* normw = nullptr;
+  Geom g{};
+  float scale_w = 1.0f;
+  float inv_scale_w = 1.0f;  // 1.0f / scale_w (bitlinear.cpp:28)
+  float inv_fixed = 1.0f;    // 1.0f / (2^frac * scale_w) (bitlinear.cpp:30), for the model frac
+};
+
+// ---- fused single-row decode kernels (mmf_decode.hip) -------------------------------
+enum DecKind : int { kIFG = 0, kO = 1, kGate = 2, kDown = 3, kLM = 4 };
+
+struct DecArgs {
+  ProjDev p[3];
+  int H, I, vocab, layer, use_lb;
+  float eps, qs, inv_fixed[3];
+  const float* x;         // input vector; nullptr for layer 0 (embedding row of *key,
+                          // a cleared key or one outside [0, vocab) reads row 0)
+  const float* emb;
+  const float* x2;        // kO: recurrence output (silu-gated)
+  const float* pre_w;     // stage-1 norm weight (attn / g / mlp / final norm), or nullptr
+  const float* lb;        // lower bound row of this layer (kIFG), or nullptr
+  const float* hin;       // kO: layer input h; kDown: resid
+  float* state;           // kIFG: this layer's recurrent state [H]
+  float* recur;           // kIFG out
+  float* gout;            // kIFG out
+  float* out;             // kIFG layer 0: copy of the embedding row (h); kO: resid;
+                          // kGate: z; kDown: next h; kLM: logits (may be null)
+  unsigned long long* key;  // argmax key: written by kLM, read by layer-0 kIFG
+  unsigned long long* key_reset;  // kO of layer 0 clears it
+  int64_t* hist;          // kIFG layer 0: token history, hist[*hist_pos]++ (below hist_cap)
+  int32_t* hist_pos;
+  int hist_cap;
+};
+
+hipError_t launch_decode(DecKind kind, Mode mode, const DecArgs& a, hipStream_t s);
+
+// Argmax key: (orderable float bits << 32) | (0xFFFFFFFF - index): the max key is the first
+// index of the largest value (the reference's strict `>` scan, hgrn_model.cpp:270-273).
+__host__ __device__ inline int64_t key_index(unsigned long long k) {
+  return static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(k & 0xFFFFFFFFull));
+}
+
+// ---- generic row kernels (mmf_ops.hip) ------------------------------------------------
+// Chain-transposed activations of `rows` rows for NA projections:
+//   float: y  [NA][rows][8*Lc + 8]
+//   int:   q  [NA][rows][2][8*Lc] int8 planes (plane 1 unused in kInt8),
+//          ct [NA][rows][8] int32 tail codes, sa [NA][rows] int8 scales
+struct ActBuf {
+  float* y = nullptr;
+  int8_t* q = nullptr;
+  int32_t* ct = nullptr;
+  float* sa = nullptr;
+  int Lc = 0, K = 0, K8 = 0, nb = 0, ntail = 0, rows = 0, na = 0;
+  __host__ __device__ size_t ystride() const { return static_cast<size_t>(8 * Lc + 8); }
+  __host__ __device__ size_t qstride() const { return static_cast<size_t>(2 * 8 * Lc); }
+};
+
+// Stage kinds of the row prologue (what happens before the BitLinear's own RMSNorm).
+enum PreKind : int { kPreNone = 0, kPreNorm = 1, kPreSwish = 2 };
+
+struct PrologueArgs {
+  const float* x;      // [rows, K]
+  const float* x2;     // kPreSwish: recurrence output rows [rows, K]
+  const float* pre_w;  // stage-1 norm weight
+  const float* normw[3];
+  int na;
+  PreKind pre;
+  float eps, qs;
+};
+hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s);
+
+// Integer codes [rows, K] (int16-range, as int32) -> planes (TernaryBackend path).
+hipError_t launch_codes_to_planes(const int32_t* x, ActBuf& act, hipStream_t s);
+
+enum EpiKind : int { kEpiStore = 0, kEpiAdd = 1, kEpiSwigluPair = 2 };
+
+struct GemmArgs {
+  ProjDev p[3];
+  int nmat;            // matrices (grid.z)
+  int rows;
+  Mode mode;
+  float inv_fixed[3];
+  bool raw_acc;        // int modes: write integer accumulators only (TernaryBackend)
+  EpiKind epi;
+  const float* add;    // kEpiAdd: out = add + val (same shape as out)
+  float* out[3];       // [rows, N] per matrix (kEpiSwigluPair: out[0] = z [rows, N/2])
+  int32_t* acc[3];     // optional int32 accumulators [rows, N]
+  int swiglu_n;        // kEpiSwigluPair: rows * (N/2), for the tail rule
+};
+hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+
+// HGRN gate + recurrence over rows (hgrn_model.cpp:109-150). i, f, g: [rows, H].
+// stream_state = false: rows are time steps of one sequence, state [H] carried in order.
+// stream_state = true: rows are independent streams, state [rows, H].
+hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
+                        const float* lb, int rows, int H, bool stream_state, hipStream_t s);
+
+// Embedding gather rows (hgrn_model.cpp:321-326).
+hipError_t launch_embed(const float* emb, const int64_t* ids, float* h, int rows, int H,
+                        hipStream_t s);
+// Final RMSNorm rows (hgrn_model.cpp:235,440): plain rmsnorm kernel.
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps,
+                          hipStream_t s);
+// Row argmax over [rows, V] logits -> ids.
+hipError_t launch_argmax_rows(const float* logits, int rows, int V, int64_t* ids, hipStream_t s);
+// Elementwise ops for the op-level API (kernels.hpp:54-68).
+hipError_t launch_swiglu(const float* a, const float* b, float* out, size_t n, hipStream_t s);
+hipError_t launch_swishgate(const float* g, const float* o, const float* w, float* out, int rows,
+                            int cols, float eps, hipStream_t s);
+hipError_t launch_scan(const float* i, const float* f, float* out, float* state, int T, int D,
+                       hipStream_t s);
+
+// ---- weight repack (mmf_ops.hip) ----------------------------------------------------------
+hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* tail, int32_t* rowsum,
+                       hipStream_t s);
+
+}  // namespace mmf

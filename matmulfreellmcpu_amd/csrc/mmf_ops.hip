@@ -1,0 +1,644 @@
+// mmf_ops.hip -- multi-row kernels: weight repack, BitLinear prologue (norms + activation
+// quantisation), the ternary GEMM over row tiles, the HGRN mixer/recurrence and the
+// elementwise ops. These serve prefill, batched (serving) decode, the stateless forward
+// and the op-level entry points; single-row decode has fused kernels in mmf_decode.hip.
+//
+// Numerics follow the reference engine exactly (see mmf_device.hpp): every fp32
+// reduction keeps the 8-lane order of the AVX2 code, every int32 sum is exact.
+#include "mmf_device.hpp"
+#include "mmf_internal.hpp"
+
+namespace mmf {
+
+namespace {
+
+__device__ __forceinline__ int act_pos(int k, int K8, int Lc) {
+  return k < K8 ? (k & 7) * Lc + (k >> 3) : 8 * Lc + (k - K8);
+}
+
+// Reference sumsq (simd.hpp:69-89) of a chain-transposed vector in LDS; every thread gets
+// the result. `red` is 8 floats of LDS.
+__device__ float block_sumsq(const float* X, int Lc, int nb, int ntail, float* red) {
+  if (threadIdx.x < 8) {
+    const float* c = X + threadIdx.x * Lc;
+    float a = 0.0f;
+    int t = 0;
+    for (; t + 4 <= nb; t += 4) {
+      float4 v = *reinterpret_cast<const float4*>(c + t);
+      a = __builtin_fmaf(v.x, v.x, a);
+      a = __builtin_fmaf(v.y, v.y, a);
+      a = __builtin_fmaf(v.z, v.z, a);
+      a = __builtin_fmaf(v.w, v.w, a);
+    }
+    for (; t < nb; ++t) a = __builtin_fmaf(c[t], c[t], a);
+    red[threadIdx.x] = a;
+  }
+  __syncthreads();
+  float s = hsum8(red);
+  for (int t = 0; t < ntail; ++t) {
+    float v = X[8 * Lc + t];
+    s = __builtin_fmaf(v, v, s);
+  }
+  __syncthreads();
+  return s;
+}
+
+__device__ float block_max(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+  for (int i = 1; i < nw; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+// Load row x[0..K) into chain-transposed LDS X (zero padding).
+__device__ void load_T(float* X, const float* x, int K, int K8, int Lc, int nb) {
+  for (int k = threadIdx.x; k < K; k += blockDim.x) X[act_pos(k, K8, Lc)] = x[k];
+  for (int j = 0; j < 8; ++j)
+    for (int t = nb + threadIdx.x; t < Lc; t += blockDim.x) X[j * Lc + t] = 0.0f;
+  for (int t = (K - K8) + threadIdx.x; t < 8; t += blockDim.x) X[8 * Lc + t] = 0.0f;
+}
+
+// ------------------------------------------------------------------------------------
+// weight repack
+// ------------------------------------------------------------------------------------
+__global__ void k_pack(const int8_t* __restrict__ wq, Geom g, uint32_t* __restrict__ pk,
+                       int8_t* __restrict__ tail, int32_t* __restrict__ rowsum,
+                       int* __restrict__ bad) {
+  const size_t nwords = static_cast<size_t>(g.ngroups) * g.Wc * kGroup * 8;
+  for (size_t w = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; w < nwords;
+       w += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int j = static_cast<int>(w & 7);
+    const int ol = static_cast<int>((w >> 3) & 15);
+    const size_t gm = w >> 7;  // og * Wc + m
+    const int m = static_cast<int>(gm % g.Wc);
+    const int og = static_cast<int>(gm / g.Wc);
+    const int o = og * kGroup + ol;
+    uint32_t word = 0;
+    if (o < g.N) {
+      const int8_t* row = wq + static_cast<size_t>(o) * g.K;
+      for (int t = 0; t < 16; ++t) {
+        const int tt = 16 * m + t;
+        if (tt < g.nb) {
+          const int v = row[j + 8 * tt];
+          if (v < -1 || v > 1) atomicOr(bad, 1);
+          word |= static_cast<uint32_t>(v & 3) << code_shift(t);
+        }
+      }
+    }
+    pk[w] = word;
+  }
+  const int npad = g.ngroups * kGroup;
+  for (int o = blockIdx.x * blockDim.x + threadIdx.x; o < npad; o += gridDim.x * blockDim.x) {
+    int32_t s = 0;
+    if (o < g.N) {
+      const int8_t* row = wq + static_cast<size_t>(o) * g.K;
+      for (int k = 0; k < g.K8; ++k) s += row[k];
+    }
+    rowsum[o] = s;
+    for (int t = 0; t < 8; ++t) {
+      int8_t v = (o < g.N && t < g.ntail) ? wq[static_cast<size_t>(o) * g.K + g.K8 + t] : 0;
+      if (v < -1 || v > 1) atomicOr(bad, 1);
+      tail[o * 8 + t] = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// BitLinear prologue over rows: optional stage-1 norm, the BitLinear RMSNorm
+// (bitlinear.cpp:62-78, 99-107) and the activation encoding of each of na projections.
+// ------------------------------------------------------------------------------------
+template <int MODE>
+__global__ void k_prologue(PrologueArgs a, ActBuf act) {
+  extern __shared__ float smem[];
+  const int row = blockIdx.x;
+  const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail;
+  float* X = smem;                   // [8*Lc + 8]
+  float* S = X + 8 * Lc + 8;         // [8*Lc + 8] silu(x2) for kPreSwish
+  float* red = S + 8 * Lc + 8;       // [16]
+  load_T(X, a.x + static_cast<size_t>(row) * K, K, K8, Lc, nb);
+  if (a.pre == kPreSwish) {
+    // silu over one row of `cols` = K elements (rmsnorm_swishgate.cpp:24): tail k >= K & ~7
+    const float* o = a.x2 + static_cast<size_t>(row) * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x)
+      S[act_pos(k, K8, Lc)] = silu_of(o[k], k >= (K & ~7));
+  }
+  __syncthreads();
+  if (a.pre != kPreNone) {
+    const float r1 = rstd_of(block_sumsq(X, Lc, nb, nt, red), K, a.eps);
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+      const int p = act_pos(k, K8, Lc);
+      float v = (X[p] * r1) * a.pre_w[k];
+      if (a.pre == kPreSwish) v = v * S[p];
+      X[p] = v;
+    }
+    __syncthreads();
+  }
+  const float r2 = rstd_of(block_sumsq(X, Lc, nb, nt, red), K, a.eps);
+  for (int ai = 0; ai < a.na; ++ai) {
+    const float* nw = a.normw[ai];
+    const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+    if (MODE == kFloat) {
+      float* yo = act.y + ar * act.ystride();
+      for (int j = 0; j < 8; ++j)
+        for (int t = threadIdx.x; t < Lc; t += blockDim.x)
+          yo[j * Lc + t] = (t < nb) ? (X[j * Lc + t] * r2) * nw[j + 8 * t] : 0.0f;
+      for (int t = threadIdx.x; t < 8; t += blockDim.x)
+        yo[8 * Lc + t] = (t < nt) ? (X[8 * Lc + t] * r2) * nw[K8 + t] : 0.0f;
+    } else {
+      float sa = 0.0f;
+      if (MODE == kInt8) {
+        float m = 0.0f;
+        for (int k = threadIdx.x; k < K; k += blockDim.x)
+          m = fmaxf(m, fabsf((X[act_pos(k, K8, Lc)] * r2) * nw[k]));
+        m = block_max(m, red);
+        sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+        if (threadIdx.x == 0) act.sa[ar] = sa;
+      }
+      int8_t* q = act.q + ar * act.qstride();
+      // 4 consecutive chain positions per thread -> one 32-bit store per plane
+      for (int j = 0; j < 8; ++j)
+        for (int t4 = threadIdx.x * 4; t4 < Lc; t4 += blockDim.x * 4) {
+          uint32_t hi = 0, lo = 0;
+          for (int u = 0; u < 4; ++u) {
+            const int t = t4 + u;
+            if (t < nb) {
+              const float y = (X[j * Lc + t] * r2) * nw[j + 8 * t];
+              if (MODE == kFixed) {
+                const int32_t c = q510_body(y, a.qs);
+                hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
+                lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
+              } else {
+                hi |= static_cast<uint32_t>(q8_of(y, sa) & 0xFF) << (8 * u);
+              }
+            }
+          }
+          *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
+          if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
+        }
+      for (int t = threadIdx.x; t < 8; t += blockDim.x) {
+        int32_t c = 0;
+        if (t < nt) {
+          const float y = (X[8 * Lc + t] * r2) * nw[K8 + t];
+          c = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
+        }
+        act.ct[ar * 8 + t] = c;
+      }
+    }
+  }
+}
+
+// int16-range codes -> split planes (the TernaryBackend path: codes arrive quantised)
+__global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
+  const int row = blockIdx.x, Lc = act.Lc, nb = act.nb;
+  const int32_t* xr = x + static_cast<size_t>(row) * act.K;
+  int8_t* q = act.q + static_cast<size_t>(row) * act.qstride();
+  for (int j = 0; j < 8; ++j)
+    for (int t4 = threadIdx.x * 4; t4 < Lc; t4 += blockDim.x * 4) {
+      uint32_t hi = 0, lo = 0;
+      for (int u = 0; u < 4; ++u) {
+        const int t = t4 + u;
+        if (t < nb) {
+          const int32_t c = xr[j + 8 * t];
+          hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
+          lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
+        }
+      }
+      *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
+      *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
+    }
+  for (int t = threadIdx.x; t < 8; t += blockDim.x)
+    act.ct[static_cast<size_t>(row) * 8 + t] = (t < act.ntail) ? xr[act.K8 + t] : 0;
+}
+
+// ------------------------------------------------------------------------------------
+// Ternary GEMM over row tiles. Block = 16 outputs x 8 chains; R rows per block; the
+// activations of one chunk of MW words per chain are staged in LDS for all R rows.
+// PAIR: the block computes rows o and o + N/2 of one matrix (the MLP gate/up halves,
+// hgrn_model.cpp:171-185) and applies swiglu in the epilogue.
+// ------------------------------------------------------------------------------------
+constexpr int kMW = 8;  // words per chain per LDS chunk
+
+template <int MODE, int R, bool PAIR>
+__global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a, ActBuf act) {
+  extern __shared__ float smem[];
+  const int z = blockIdx.z;
+  const ProjDev& P = a.p[z];
+  const Geom& g = P.g;
+  const int Lc = act.Lc;
+  const int tid = threadIdx.x, ol = tid >> 3, j = tid & 7;
+  const int og = blockIdx.x;
+  const int row0 = blockIdx.y * R;
+  const int nrows = min(R, a.rows - row0);
+  const int ai = (act.na > 1) ? z : 0;
+  constexpr int NM = PAIR ? 2 : 1;
+  const int half_groups = g.ngroups / 2;  // PAIR: N/2 is a multiple of 16
+  const uint32_t* slab[NM];
+  slab[0] = P.pk + static_cast<size_t>(og) * g.Wc * 128 + ol * 8 + j;
+  if (PAIR) slab[NM - 1] = P.pk + static_cast<size_t>(og + half_groups) * g.Wc * 128 + ol * 8 + j;
+
+  float facc[NM][R];
+  int32_t iacc[NM][R], lacc[NM][R];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int r = 0; r < R; ++r) { facc[mi][r] = 0.0f; iacc[mi][r] = 0; lacc[mi][r] = 0; }
+
+  for (int m0 = 0; m0 < g.Wc; m0 += kMW) {
+    const int mw = min(kMW, g.Wc - m0);
+    __syncthreads();
+    // stage activations [r][chain][mw*16] of this chunk
+    if (MODE == kFloat) {
+      float* L = smem;
+      const int per_row = 8 * mw * 16;
+      for (int e = tid * 4; e < R * per_row; e += kBlock * 4) {
+        const int r = e / per_row, rem = e - r * per_row, jj = rem / (mw * 16), t = rem - jj * mw * 16;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nrows)
+          v = *reinterpret_cast<const float4*>(
+              act.y + (static_cast<size_t>(ai) * act.rows + row0 + r) * act.ystride() + jj * Lc + m0 * 16 + t);
+        *reinterpret_cast<float4*>(L + r * per_row + jj * mw * 16 + t) = v;
+      }
+    } else {
+      uint32_t* L = reinterpret_cast<uint32_t*>(smem);
+      const int np = (MODE == kFixed) ? 2 : 1;
+      const int per_row = np * 8 * mw * 4;  // dwords
+      for (int e = tid; e < R * per_row; e += kBlock) {
+        const int r = e / per_row, rem = e - r * per_row, pl = rem / (8 * mw * 4),
+                  rem2 = rem - pl * 8 * mw * 4, jj = rem2 / (mw * 4), d = rem2 - jj * mw * 4;
+        uint32_t v = 0;
+        if (r < nrows)
+          v = *reinterpret_cast<const uint32_t*>(
+              act.q + (static_cast<size_t>(ai) * act.rows + row0 + r) * act.qstride() + pl * 8 * Lc +
+              jj * Lc + m0 * 16 + d * 4);
+        L[e] = v;
+      }
+    }
+    __syncthreads();
+    for (int mm = 0; mm < mw; ++mm) {
+      const int m = m0 + mm;
+      uint32_t w[NM];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) w[mi] = slab[mi][static_cast<size_t>(m) * 128];
+      if (MODE == kFloat) {
+        const float* L = smem;
+        const int per_row = 8 * mw * 16;
+        float wf[NM][16];
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+          for (int t = 0; t < 16; ++t) wf[mi][t] = code_f(w[mi], t);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float* yl = L + r * per_row + j * mw * 16 + mm * 16;
+          float y[16];
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            float4 v = *reinterpret_cast<const float4*>(yl + 4 * q4);
+            y[4 * q4] = v.x; y[4 * q4 + 1] = v.y; y[4 * q4 + 2] = v.z; y[4 * q4 + 3] = v.w;
+          }
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) facc[mi][r] = __builtin_fmaf(y[t], wf[mi][t], facc[mi][r]);
+        }
+      } else {
+        const uint32_t* L = reinterpret_cast<const uint32_t*>(smem);
+        const int np = (MODE == kFixed) ? 2 : 1;
+        const int per_row = np * 8 * mw * 4;
+        uint32_t wv[NM][4];
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wv[mi][i] = w4_i8(w[mi], i);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint4 h = *reinterpret_cast<const uint4*>(L + r * per_row + j * mw * 4 + mm * 4);
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) {
+            iacc[mi][r] = dot4(wv[mi][0], h.x, iacc[mi][r]);
+            iacc[mi][r] = dot4(wv[mi][1], h.y, iacc[mi][r]);
+            iacc[mi][r] = dot4(wv[mi][2], h.z, iacc[mi][r]);
+            iacc[mi][r] = dot4(wv[mi][3], h.w, iacc[mi][r]);
+          }
+          if (MODE == kFixed) {
+            const uint4 l = *reinterpret_cast<const uint4*>(L + r * per_row + 8 * mw * 4 + j * mw * 4 + mm * 4);
+#pragma unroll
+            for (int mi = 0; mi < NM; ++mi) {
+              lacc[mi][r] = dot4(wv[mi][0], l.x, lacc[mi][r]);
+              lacc[mi][r] = dot4(wv[mi][1], l.y, lacc[mi][r]);
+              lacc[mi][r] = dot4(wv[mi][2], l.z, lacc[mi][r]);
+              lacc[mi][r] = dot4(wv[mi][3], l.w, lacc[mi][r]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // reduce the 8 chains of each output and apply the epilogue
+  const int Nout = PAIR ? g.N / 2 : g.N;
+  const int o = og * kGroup + ol;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float val[NM];
+    int32_t tot[NM];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int oo = o + (mi ? Nout : 0);
+      const size_t ar = static_cast<size_t>(ai) * act.rows + row0 + r;
+      if (MODE == kFloat) {
+        float s = hsum8_lanes(facc[mi][r]);
+        if (j == 0 && r < nrows && oo < g.N) {
+          const float* yt = act.y + ar * act.ystride() + 8 * Lc;
+          for (int t = 0; t < g.ntail; ++t) {
+            const int8_t wt = P.tail[oo * 8 + t];
+            if (wt > 0) s += yt[t];
+            else if (wt < 0) s -= yt[t];
+          }
+        }
+        val[mi] = s * P.inv_scale_w;
+        tot[mi] = 0;
+      } else {
+        int32_t s = isum8_lanes(iacc[mi][r]);
+        if (MODE == kFixed) s = s * 256 + isum8_lanes(lacc[mi][r]);
+        if (j == 0 && r < nrows && oo < g.N) {
+          if (MODE == kFixed) s += 128 * P.rowsum[oo];
+          const int32_t* ct = act.ct + ar * 8;
+          for (int t = 0; t < g.ntail; ++t) s += static_cast<int32_t>(P.tail[oo * 8 + t]) * ct[t];
+        }
+        tot[mi] = s;
+        if (MODE == kFixed) val[mi] = static_cast<float>(s) * a.inv_fixed[z];
+        else if (j == 0 && r < nrows) val[mi] = static_cast<float>(s) / (P.scale_w * act.sa[ar]);
+        else val[mi] = 0.0f;
+      }
+    }
+    if (j != 0 || r >= nrows || o >= Nout) continue;
+    const size_t grow = static_cast<size_t>(row0 + r);
+    if (MODE != kFloat && a.acc[z]) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) a.acc[z][grow * g.N + o + (mi ? Nout : 0)] = tot[mi];
+    }
+    if (MODE != kFloat && a.raw_acc) continue;
+    if (PAIR) {
+      const size_t e = grow * Nout + o;
+      a.out[0][e] = swiglu_of(val[0], val[NM - 1], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+    } else if (a.epi == kEpiAdd) {
+      const size_t e = grow * g.N + o;
+      a.out[z][e] = a.add[e] + val[0];
+    } else {
+      a.out[z][grow * g.N + o] = val[0];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// HGRN gate + recurrence (hgrn_model.cpp:109-150)
+// ------------------------------------------------------------------------------------
+__global__ void k_mixer(const float* __restrict__ i, float* __restrict__ f, float* __restrict__ scan_out,
+                        float* __restrict__ recur, float* __restrict__ state,
+                        const float* __restrict__ lb, int rows, int H, int stream_state) {
+  const int n = rows * H;  // the sigmoid / swiglu element count (tail rule)
+  const int body = n & ~7;
+  if (stream_state) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int c = e % H;
+    float fv = sigmoid_of(f[e], e >= body);
+    if (lb) fv = __builtin_fmaf(1.0f - lb[c], fv, lb[c]);
+    const float in = swiglu_of(i[e], 1.0f - fv, e >= body);
+    const float s = __builtin_fmaf(fv, state[e], in);
+    state[e] = s;
+    recur[e] = s;
+    f[e] = fv;
+    if (scan_out) scan_out[e] = in;
+    return;
+  }
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= H) return;
+  float s = state[c];
+  const float lbc = lb ? lb[c] : 0.0f;
+  constexpr int U = 8;
+  int t = 0;
+  for (; t + U <= rows; t += U) {
+    float iv[U], fv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      iv[u] = i[static_cast<size_t>(t + u) * H + c];
+      fv[u] = f[static_cast<size_t>(t + u) * H + c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = (t + u) * H + c;
+      float g = sigmoid_of(fv[u], e >= body);
+      if (lb) g = __builtin_fmaf(1.0f - lbc, g, lbc);
+      const float in = swiglu_of(iv[u], 1.0f - g, e >= body);
+      s = __builtin_fmaf(g, s, in);
+      recur[e] = s;
+      f[e] = g;
+      if (scan_out) scan_out[e] = in;
+    }
+  }
+  for (; t < rows; ++t) {
+    const int e = t * H + c;
+    float g = sigmoid_of(f[e], e >= body);
+    if (lb) g = __builtin_fmaf(1.0f - lbc, g, lbc);
+    const float in = swiglu_of(i[e], 1.0f - g, e >= body);
+    s = __builtin_fmaf(g, s, in);
+    recur[e] = s;
+    f[e] = g;
+    if (scan_out) scan_out[e] = in;
+  }
+  state[c] = s;
+}
+
+__global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict__ ids,
+                        float* __restrict__ h, int rows, int H) {
+  const size_t n = static_cast<size_t>(rows) * H;
+  for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t r = e / H, c = e - r * H;
+    h[e] = emb[static_cast<size_t>(ids[r]) * H + c];
+  }
+}
+
+// rmsnorm / swishgate rows: one block per row, chain-transposed copy in LDS for the sumsq
+__global__ void k_rownorm(const float* __restrict__ x, const float* __restrict__ o,
+                          const float* __restrict__ w, float* __restrict__ y, int cols, float eps) {
+  extern __shared__ float smem[];
+  const int K = cols, K8 = K & ~7, nb = K8 / 8, Lc = (nb + 15) / 16 * 16 + 16;
+  float* X = smem;
+  float* red = X + 8 * Lc + 8;
+  const float* xr = x + static_cast<size_t>(blockIdx.x) * K;
+  load_T(X, xr, K, K8, Lc, nb);
+  __syncthreads();
+  const float r = rstd_of(block_sumsq(X, Lc, nb, K - K8, red), K, eps);
+  float* yr = y + static_cast<size_t>(blockIdx.x) * K;
+  const float* orow = o ? o + static_cast<size_t>(blockIdx.x) * K : nullptr;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    float v = (xr[k] * r) * w[k];
+    if (orow) v = v * silu_of(orow[k], k >= K8);
+    yr[k] = v;
+  }
+}
+
+__global__ void k_argmax_rows(const float* __restrict__ lg, int V, int64_t* __restrict__ ids) {
+  __shared__ unsigned long long red[16];
+  const float* r = lg + static_cast<size_t>(blockIdx.x) * V;
+  unsigned long long best = 0;
+  for (int v = threadIdx.x; v < V; v += blockDim.x) {
+    const unsigned long long k = amax_key(r[v], v);
+    best = k > best ? k : best;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long other = __shfl_xor(best, o);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) best = red[i] > best ? red[i] : best;
+    best = red[0] > best ? red[0] : best;
+    ids[blockIdx.x] = key_index(best);
+  }
+}
+
+__global__ void k_swiglu(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
+                         size_t n) {
+  const size_t body = n & ~static_cast<size_t>(7);
+  for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[e] = swiglu_of(a[e], b[e], e >= body);
+}
+
+__global__ void k_scan(const float* __restrict__ i, const float* __restrict__ f, float* __restrict__ out,
+                       float* __restrict__ state, int T, int D) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float s = state ? state[d] : 0.0f;
+  for (int t = 0; t < T; ++t) {
+    const size_t e = static_cast<size_t>(t) * D + d;
+    s = __builtin_fmaf(f[e], s, i[e]);
+    out[e] = s;
+  }
+  if (state) state[d] = s;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------
+// launchers
+// ------------------------------------------------------------------------------------
+hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* tail, int32_t* rowsum,
+                       hipStream_t s) {
+  int* bad = nullptr;
+  hipError_t e = hipMalloc(&bad, sizeof(int));
+  if (e != hipSuccess) return e;
+  e = hipMemsetAsync(bad, 0, sizeof(int), s);
+  if (e != hipSuccess) { (void)hipFree(bad); return e; }
+  const size_t nwords = static_cast<size_t>(g.ngroups) * g.Wc * kGroup * 8;
+  const int blocks = static_cast<int>(std::min<size_t>((nwords + 255) / 256, 65536));
+  k_pack<<<blocks, 256, 0, s>>>(wq, g, pk, tail, rowsum, bad);
+  e = hipGetLastError();
+  int hbad = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&hbad, bad, sizeof(int), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  (void)hipFree(bad);
+  if (e == hipSuccess && hbad) return hipErrorInvalidValue;
+  return e;
+}
+
+hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
+  const size_t lds = (2 * static_cast<size_t>(8 * act.Lc + 8) + 16) * sizeof(float);
+  const int threads = 256;
+  switch (mode) {
+    case kFloat: k_prologue<kFloat><<<act.rows, threads, lds, s>>>(a, act); break;
+    case kFixed: k_prologue<kFixed><<<act.rows, threads, lds, s>>>(a, act); break;
+    default: k_prologue<kInt8><<<act.rows, threads, lds, s>>>(a, act); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_codes_to_planes(const int32_t* x, ActBuf& act, hipStream_t s) {
+  k_codes<<<act.rows, 256, 0, s>>>(x, act);
+  return hipGetLastError();
+}
+
+template <int MODE, int R, bool PAIR>
+static hipError_t gemm_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const Geom& g = a.p[0].g;
+  const int np = (MODE == kFixed) ? 2 : 1;
+  const size_t lds = (MODE == kFloat) ? static_cast<size_t>(R) * 8 * kMW * 16 * sizeof(float)
+                                      : static_cast<size_t>(R) * np * 8 * kMW * 16;
+  dim3 grid(PAIR ? g.ngroups / 2 : g.ngroups, (a.rows + R - 1) / R, PAIR ? 1 : a.nmat);
+  k_gemm<MODE, R, PAIR><<<grid, kBlock, lds, s>>>(a, act);
+  return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const bool pair = a.epi == kEpiSwigluPair;
+  if (a.rows <= 1) return pair ? gemm_inst<MODE, 1, true>(a, act, s) : gemm_inst<MODE, 1, false>(a, act, s);
+  if (a.rows <= 4) return pair ? gemm_inst<MODE, 4, true>(a, act, s) : gemm_inst<MODE, 4, false>(a, act, s);
+  return pair ? gemm_inst<MODE, 8, true>(a, act, s) : gemm_inst<MODE, 8, false>(a, act, s);
+}
+
+hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  switch (a.mode) {
+    case kFloat: return gemm_mode<kFloat>(a, act, s);
+    case kFixed: return gemm_mode<kFixed>(a, act, s);
+    default: return gemm_mode<kInt8>(a, act, s);
+  }
+}
+
+hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
+                        const float* lb, int rows, int H, bool stream_state, hipStream_t s) {
+  const int n = stream_state ? rows * H : H;
+  k_mixer<<<(n + 255) / 256, 256, 0, s>>>(i, f, scan_out, recur, state, lb, rows, H, stream_state ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const float* emb, const int64_t* ids, float* h, int rows, int H, hipStream_t s) {
+  const size_t n = static_cast<size_t>(rows) * H;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
+  k_embed<<<blocks, 256, 0, s>>>(emb, ids, h, rows, H);
+  return hipGetLastError();
+}
+
+static size_t rownorm_lds(int cols) {
+  const int nb = (cols & ~7) / 8, Lc = (nb + 15) / 16 * 16 + 16;
+  return (static_cast<size_t>(8 * Lc + 8) + 16) * sizeof(float);
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps,
+                          hipStream_t s) {
+  k_rownorm<<<rows, 256, rownorm_lds(cols), s>>>(x, nullptr, w, y, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_swishgate(const float* g, const float* o, const float* w, float* out, int rows, int cols,
+                            float eps, hipStream_t s) {
+  k_rownorm<<<rows, 256, rownorm_lds(cols), s>>>(g, o, w, out, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* logits, int rows, int V, int64_t* ids, hipStream_t s) {
+  k_argmax_rows<<<rows, 1024, 0, s>>>(logits, V, ids);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* a, const float* b, float* out, size_t n, hipStream_t s) {
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
+  k_swiglu<<<blocks > 0 ? blocks : 1, 256, 0, s>>>(a, b, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_scan(const float* i, const float* f, float* out, float* state, int T, int D, hipStream_t s) {
+  k_scan<<<(D + 255) / 256, 256, 0, s>>>(i, f, out, state, T, D);
+  return hipGetLastError();
+}
+
+}  // namespace mmf

@@ -1,0 +1,238 @@
+"""Parity of the HIP path (through the C ABI) with the CPU restatement of the reference.
+
+Bar: bit-exact everywhere -- integer accumulators and codes, and fp32 outputs of the Float
+and FixedQ510 modes (the HIP kernels keep the reference's summation order and FMA sites).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+FLOAT, FIXED, INT8 = 0, 1, 2
+
+
+@pytest.fixture(scope="module")
+def eng():
+    from matmulfreellmcpu_amd import Engine
+    e = Engine(0)
+    print("device:", e.device_info(), flush=True)
+    yield e
+    e.close()
+
+
+class Dev:
+    """Device buffer from the engine's allocator, filled from / read into numpy."""
+
+    def __init__(self, eng, arr=None, shape=None, dtype=np.float32):
+        self.eng = eng
+        if arr is not None:
+            arr = np.ascontiguousarray(arr)
+            shape, dtype = arr.shape, arr.dtype
+        self.shape, self.dtype = tuple(shape), np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = C.c_void_p()
+        eng._chk(eng.lib.mmf_malloc(eng.h, C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+        if arr is not None:
+            eng._chk(eng.lib.mmf_upload(eng.h, self.ptr, arr.ctypes.data_as(C.c_void_p), self.nbytes))
+
+    def get(self):
+        out = np.empty(self.shape, self.dtype)
+        self.eng._chk(self.eng.lib.mmf_download(self.eng.h, out.ctypes.data_as(C.c_void_p), self.ptr, self.nbytes))
+        return out
+
+    def __del__(self):
+        try:
+            self.eng.lib.mmf_free(self.eng.h, self.ptr)
+        except Exception:
+            pass
+
+
+SHAPES = [(1, 64, 64), (3, 176, 48), (5, 1024, 333), (1, 1031, 17), (9, 100, 40), (2, 7, 19), (17, 256, 128)]
+
+
+@pytest.mark.parametrize("rows,K,N", SHAPES)
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_bitlinear_op(eng, oracle, rows, K, N, mode):
+    print(f"bitlinear rows={rows} K={K} N={N} mode={mode}", flush=True)
+    rng = np.random.default_rng(rows * 1000 + K + N + mode)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, mode)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    dacc = Dev(eng, shape=(rows, N), dtype=np.int32)
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=mode, acc=dacc.ptr if mode else None)
+    eng.sync()
+    if mode:
+        np.testing.assert_array_equal(dacc.get(), want["acc"])
+    assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
+
+
+def test_bitlinear_cluster_matches_single(eng, oracle):
+    rng = np.random.default_rng(5)
+    rows, K, N = 4, 256, 96
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    pids, wants = [], []
+    for j in range(3):
+        nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+        wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+        pids.append(eng.register_proj(wq, 40.0 + j, nw))
+        wants.append(oracle.bitlinear(x, nw, wq, 40.0 + j, 1e-6, FIXED)["out"])
+    dx = Dev(eng, x)
+    outs = [Dev(eng, shape=(rows, N)) for _ in range(3)]
+    eng.bitlinear_cluster(pids, dx.ptr, [o.ptr for o in outs], rows, mode=FIXED)
+    eng.sync()
+    for o, w in zip(outs, wants):
+        assert_bitexact(o.get(), w, "cluster")
+
+
+@pytest.mark.parametrize("b,K,N", [(1, 1024, 256), (4, 2816, 64), (3, 13, 5)])
+def test_ternary_matmul(eng, oracle, b, K, N):
+    rng = np.random.default_rng(b + K)
+    x = rng.integers(-32768, 32768, (b, K)).astype(np.int32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    pid = eng.register_proj(wq, 1.0)
+    dx, dacc = Dev(eng, x), Dev(eng, shape=(b, N), dtype=np.int32)
+    eng.ternary_matmul(pid, dx.ptr, dacc.ptr, b)
+    eng.sync()
+    np.testing.assert_array_equal(dacc.get(), oracle.ternary_matmul(x, wq))
+
+
+def test_elementwise_ops(eng, oracle):
+    rng = np.random.default_rng(3)
+    for n in (8, 13, 8192 + 5, 20000):
+        a = (rng.standard_normal(n) * 8).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        da, db, do = Dev(eng, a), Dev(eng, b), Dev(eng, shape=(n,))
+        eng.swiglu(do.ptr, da.ptr, db.ptr, n)
+        eng.sync()
+        # activations.cpp:9-15 splits into 8192-element SIMD calls
+        want = np.concatenate([oracle.swiglu(a[o:o + 8192], b[o:o + 8192]) for o in range(0, n, 8192)])
+        assert_bitexact(do.get(), want, f"swiglu n={n}")
+    for rows, cols in ((3, 64), (2, 100), (1, 2560)):
+        g = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+        o = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+        w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+        dg, dob, dw, dy = Dev(eng, g), Dev(eng, o), Dev(eng, w), Dev(eng, shape=(rows, cols))
+        eng.rmsnorm(dy.ptr, dg.ptr, dw.ptr, rows, cols)
+        eng.sync()
+        assert_bitexact(dy.get(), oracle.rmsnorm(g, w, 1e-6), "rmsnorm")
+        eng.rmsnorm_swishgate(dy.ptr, dg.ptr, dob.ptr, dw.ptr, rows, cols)
+        eng.sync()
+        assert_bitexact(dy.get(), oracle.rmsnorm_swishgate(g, o, w, 1e-6), "swishgate")
+    T, D = 37, 200
+    i = rng.standard_normal((T, D)).astype(np.float32)
+    f = rng.uniform(0, 1, (T, D)).astype(np.float32)
+    st = rng.standard_normal(D).astype(np.float32)
+    di, df, dout, dst = Dev(eng, i), Dev(eng, f), Dev(eng, shape=(T, D)), Dev(eng, st)
+    eng.hgrn_scan(dout.ptr, di.ptr, df.ptr, T, D, dst.ptr)
+    eng.sync()
+    wo, wst = oracle.hgrn_scan(i, f, st)
+    assert_bitexact(dout.get(), wo, "scan out")
+    assert_bitexact(dst.get(), wst, "scan state")
+
+
+def _model(eng_cls, blob, mode):
+    e = eng_cls(0)
+    e.load_blob(blob, mode)
+    return e
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_nolb", "small", "odd"])
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_generate_matches_oracle(blobs, oracle, name, mode):
+    from matmulfreellmcpu_amd import Engine, read_blob
+    print(f"generate blob={name} mode={mode}", flush=True)
+    blob = read_blob(blobs(name))
+    om = oracle.model(blob)
+    rng = np.random.default_rng(42)
+    V = blob.config.vocab_size
+    ids = rng.integers(3, V, 9)
+    want, wst, wlg = om.generate(ids, 24, mode, want_state=True, want_logits=True)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    got = e.generate(ids, 24)
+    np.testing.assert_array_equal(got, want)
+    assert_bitexact(e.state()[:, 0, :], wst, "final recurrent state")
+    # second call replays the captured decode graph from a fresh state
+    np.testing.assert_array_equal(e.generate(ids, 24), want)
+    e.close()
+
+
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_trace_per_layer(blobs, oracle, mode):
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("small"))
+    om = oracle.model(blob)
+    ids = np.arange(5, 5 + 33) * 97 % blob.config.vocab_size
+    wh, wst, wtr = om.trace(ids, mode)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    h, st, tr = e.trace(ids)
+    for l in range(blob.config.num_hidden_layers):
+        for k, nm in enumerate(("i", "f", "g", "scan", "recur")):
+            assert_bitexact(tr[l, k], wtr[l, k], f"layer {l} {nm}")
+        assert_bitexact(h[l], wh[l], f"layer {l} h")
+        assert_bitexact(st[l], wst[l], f"layer {l} state")
+    e.close()
+
+
+@pytest.mark.parametrize("mode", [FLOAT, FIXED])
+def test_forward_logits(blobs, oracle, mode):
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("tiny"))
+    om = oracle.model(blob)
+    ids = np.array([3, 17, 200, 45, 7, 300, 2, 99, 511, 0, 1])
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    assert_bitexact(e.forward(ids), om.forward(ids, mode), "forward logits")
+    e.close()
+
+
+@pytest.mark.parametrize("mode", [FLOAT, FIXED])
+def test_serve_matches_oracle(blobs, oracle, mode):
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("small"))
+    om = oracle.model(blob)
+    rng = np.random.default_rng(9)
+    V = blob.config.vocab_size
+    prompts = [rng.integers(3, V, n) for n in (5, 12, 1, 7, 5)]
+    prompts[4] = prompts[0].copy()  # identical prompts must give identical streams
+    want = om.generate_serve(prompts, 10, mode)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    B = len(prompts)
+    e.reset(B)
+    streams = [list(p) for p in prompts]
+    for b in range(B):
+        streams[b].append(e.prefill(b, prompts[b]))
+    for _ in range(9):
+        nxt = e.step([s[-1] for s in streams])
+        for b in range(B):
+            streams[b].append(int(nxt[b]))
+    for b in range(B):
+        np.testing.assert_array_equal(np.array(streams[b]), want[b])
+    np.testing.assert_array_equal(streams[0], streams[4])
+    e.close()
+
+
+@pytest.mark.parametrize("mode", [FLOAT, FIXED])
+def test_generate_370m(blobs, oracle, mode):
+    """Full 370M shape: 16-token prompt, 32 greedy tokens, bit-exact state."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("s0"))
+    om = oracle.model(blob)
+    ids = np.random.default_rng(0).integers(3, 32000, 16)
+    want, wst = om.generate(ids, 32, mode, want_state=True)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    np.testing.assert_array_equal(e.generate(ids, 32), want)
+    assert_bitexact(e.state()[:, 0, :], wst, "370M final state")
+    e.close()
