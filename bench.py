@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Decode throughput of the HGRN-Bit engine on one MI355X.
+
+Headline (`value`): greedy decode tok/s at batch 1 on the 370M shape in float mode -- the
+reference CLI's own benchmark (mmfree-cli --bench: 16-token prompt, greedy, decode tok/s),
+on a seeded synthetic blob of that architecture. A step is one decode token: W untimed
+steps, then exactly K timed steps (HIP events on the engine's stream, synchronised before
+and after). The 1.3B and 2.7B shapes are reported beside it (`decode_tok_s`).
+
+roofline: the decode kernel with the most time per token, its algorithmic bytes per launch
+(2-bit packed weights + the fp32 vectors it must read and write once) over its average
+launch duration, measured with an event pair around each launch; peak = 8 TB/s HBM.
+
+cpu_baseline: the reference engine compiled from its own sources (oracle/_ref/mmfree-cli,
+built by oracle/Makefile) timed on this host's cores with its own --bench harness on the
+same blob and prompt; its greedy id stream is also compared with the GPU's.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s (B=1) 370M/1.3B/2.7B; BitLinear GB/s & % roofline, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+SHAPES = {"370M": "s0", "1.3B": "s2", "2.7B": "s3"}
+DIMS = {"s0": (32000, 1024, 24, 2816), "s2": (32000, 2048, 24, 5632), "s3": (32000, 2560, 32, 6912)}
+KINDS = ("ifg", "o", "gate", "down", "lm")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_bytes(V, H, L, I):
+    """Algorithmic HBM bytes per launch of each decode kernel: packed ternary weights
+    (N*K/4) plus every fp32 vector read or written once (inputs, norm weights, state,
+    outputs). Launches per token: L of each layer kind, one lm_head."""
+    return {
+        "ifg": 3 * H * H / 4 + 4 * (H + H + 3 * H + H + H) + 4 * 3 * H,  # h, attn_norm, 3 normw, lb, state | state, recur, g
+        "o": H * H / 4 + 4 * (3 * H + 2 * H) + 4 * H,                    # g, recur, h, g_norm, normw | resid
+        "gate": 2 * I * H / 4 + 4 * 3 * H + 4 * I,                       # resid, mlp_norm, normw | z
+        "down": I * H / 4 + 4 * (2 * I + H) + 4 * H,                     # z, normw, resid | h
+        "lm": V * H / 4 + 4 * 3 * H,                                     # h, norm, normw
+    }, {"ifg": L, "o": L, "gate": L, "down": L, "lm": 1}
+
+
+def blob_path(d, preset):
+    from matmulfreellmcpu_amd import make_blob
+    p = os.path.join(d, f"{preset}.mmfree")
+    if not os.path.exists(p):
+        t = time.time()
+        make_blob(p, preset=preset, seed=1234)
+        log(f"[bench] wrote {p} in {time.time() - t:.1f}s")
+    return p
+
+
+def measure(eng, preset, steps, warmup):
+    V, H, L, I = DIMS[preset]
+    step_us, kind_us = eng.time_decode(warmup=warmup, reps=steps)
+    nbytes, nlaunch = kernel_bytes(V, H, L, I)
+    kernels = {}
+    for k in KINDS:
+        us = kind_us[k]
+        kernels[k] = {"us_per_launch": round(us, 3), "launches_per_token": nlaunch[k],
+                      "bytes_per_launch": int(nbytes[k]), "GBps": round(nbytes[k] / us / 1e3, 1)}
+    tok_bytes = sum(nbytes[k] * nlaunch[k] for k in KINDS)
+    return step_us, kernels, tok_bytes
+
+
+def cpu_reference(blob, ids, gen, threads):
+    cli = os.path.join(ROOT, "oracle", "_ref", "mmfree-cli")
+    if not os.path.exists(cli):
+        return None, None
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    idarg = ",".join(str(int(i)) for i in ids)
+    r = subprocess.run([cli, "--blob", blob, "--ids", idarg, "--gen", str(gen), "--mode", "float", "--print-ids"],
+                       capture_output=True, text=True, env=env, check=True)
+    ref_ids = np.array([int(t) for t in r.stdout.split()], np.int64)
+    t = time.time()
+    r = subprocess.run([cli, "--blob", blob, "--ids", idarg, "--bench", "--gen", str(gen), "--warmup", "1",
+                        "--reps", "3", "--mode", "float"], capture_output=True, text=True, env=env, check=True)
+    wall = time.time() - t
+    m = re.search(r"avg decode:\s+([0-9.]+) tok/s", r.stdout)
+    tps = float(m.group(1)) if m else None
+    return ref_ids, {"value": tps, "unit": "tok/s", "cores": threads, "kind": "reference",
+                     "sample": f"370M float, 16-token prompt, {gen} greedy tokens, reference --bench warmup 1 "
+                               f"reps 3 ({wall:.1f}s wall), OMP_NUM_THREADS={threads}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512, help="timed decode steps (tokens) on the headline shape")
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--shapes", default="370M,1.3B,2.7B")
+    ap.add_argument("--blob-dir", default=os.environ.get("MMF_BLOB_DIR", "/tmp/mmf_bench_blobs"))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the HGRN-Bit hot path here runs on a single MI355X and this "
+              f"build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    os.makedirs(args.blob_dir, exist_ok=True)
+    from matmulfreellmcpu_amd import FLOAT, Engine
+
+    eng = Engine(0)
+    devname, cus = eng.device_info()
+    log(f"[bench] device {devname}, {cus} CUs")
+    shapes = [s.strip() for s in args.shapes.split(",") if s.strip()]
+    if "370M" not in shapes:
+        shapes.insert(0, "370M")
+    results = {}
+    ids = np.random.default_rng(1234).integers(3, 32000, 16)
+    gpu_ids = None
+    for name in shapes:
+        preset = SHAPES[name]
+        p = blob_path(args.blob_dir, preset)
+        t = time.time()
+        eng.close()
+        eng = Engine(0)
+        eng.load_blob(p, FLOAT)
+        log(f"[bench] {name}: loaded + repacked in {time.time() - t:.1f}s")
+        if name == "370M":
+            gpu_ids = eng.generate(ids, 128)
+            eng.generate(ids, 16)
+        steps = args.steps if name == "370M" else max(64, args.steps // 4)
+        eng.sync()
+        t0 = time.perf_counter()
+        step_us, kernels, tok_bytes = measure(eng, preset, steps, args.warmup)
+        eng.sync()
+        wall = time.perf_counter() - t0
+        results[name] = dict(step_us=step_us, kernels=kernels, tok_bytes=tok_bytes, steps=steps, wall=wall)
+        log(f"[bench] {name}: {1e6 / step_us:.1f} tok/s ({step_us:.1f} us/token), "
+            + ", ".join(f"{k} {v['us_per_launch']:.2f}us {v['GBps']:.0f}GB/s" for k, v in kernels.items()))
+    eng.close()
+
+    head = results["370M"]
+    value = 1e6 / head["step_us"]
+    kern = head["kernels"]
+    dom = max(KINDS, key=lambda k: kern[k]["us_per_launch"] * kern[k]["launches_per_token"])
+    achieved = kern[dom]["GBps"]
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"k_decode<float,{dom}> (370M)", "bytes_per_launch": kern[dom]["bytes_per_launch"],
+                "us_per_launch": kern[dom]["us_per_launch"]}
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        ref_ids, cpu = cpu_reference(blob_path(args.blob_dir, "s0"), ids, 128, threads)
+        if ref_ids is not None:
+            parity = {"against": "reference mmfree-cli (oracle/_ref)", "tokens": 128,
+                      "ids_identical": bool(np.array_equal(ref_ids, gpu_ids))}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(head["step_us"] / 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded ternary weights ~N(0,0.02) -> {-1,0,1}, embeddings ~N(0,0.02), norms 1)",
+        "config": {"workload": "HGRN-Bit 370M (H1024 I2816 L24 V32000) greedy decode, batch 1, float mode, "
+                               "16-token random prompt", "batch": 1, "prompt_tokens": 16, "mode": "float"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "decode_tok_s": {n: round(1e6 / r["step_us"], 1) for n, r in results.items()},
+        "step_GBps": {n: round(r["tok_bytes"] / r["step_us"] / 1e3, 1) for n, r in results.items()},
+        "kernels": {n: r["kernels"] for n, r in results.items()},
+        "parity": parity,
+        "device": f"{devname}, {cus} CUs",
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

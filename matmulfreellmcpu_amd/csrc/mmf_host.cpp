@@ -81,6 +81,7 @@ struct DevTensor {
 struct LayerDev {
   int proj[6];
   const float *attn = nullptr, *mlp = nullptr, *gn = nullptr, *lb = nullptr;
+  const float *attnT = nullptr, *mlpT = nullptr, *gnT = nullptr;  // chain-transposed
 };
 
 // Scratch for row (multi-token) passes.
@@ -97,9 +98,12 @@ struct Model {
   std::unordered_map<std::string, DevTensor> tensors;
   const float* emb = nullptr;
   const float* norm_w = nullptr;
+  const float* norm_wT = nullptr;
   int lm = -1;
   std::vector<LayerDev> layers;
-  // decode buffers (single row)
+  Geom gH{}, gI{};  // chain geometry of H- and I-long vectors
+  DBuf embT, normT;  // chain-transposed embedding table and norm weights
+  // decode buffers (single row, chain-transposed)
   DBuf h, resid, g, recur, z, logits, key, hist, hist_pos;
   size_t hist_cap = 0;
   DBuf state;  // [L][B][H]
@@ -252,15 +256,18 @@ void check_ids(const Model& m, const int64_t* ids, size_t n) {
       fail(MMF_ERR_ARG, "token id " + std::to_string(ids[i]) + " outside the vocabulary");
 }
 
-void alloc_decode(Model& m) {
-  const size_t H = m.cfg.hidden_size, I = m.cfg.intermediate_size, V = m.cfg.vocab_size;
-  m.h.as<float>(H);
-  m.resid.as<float>(H);
-  m.g.as<float>(H);
-  m.recur.as<float>(H);
-  m.z.as<float>(I);
+size_t chain_len(const Geom& g) { return static_cast<size_t>(8 * g.Lc + 8); }
+
+void alloc_decode(mmf_ctx* c, Model& m) {
+  const size_t WH = chain_len(m.gH), WI = chain_len(m.gI), V = m.cfg.vocab_size;
+  for (DBuf* b : {&m.h, &m.resid, &m.g, &m.recur}) {
+    b->as<float>(WH);
+    MMF_HIP(hipMemsetAsync(b->p, 0, WH * sizeof(float), c->stream));  // zero padding
+  }
+  m.z.as<float>(WI);
+  MMF_HIP(hipMemsetAsync(m.z.p, 0, WI * sizeof(float), c->stream));
   m.logits.as<float>(V);
-  m.key.as<unsigned long long>(1);
+  m.key.as<unsigned long long>(kLMBlocks);
   m.hist_pos.as<int32_t>(1);
 }
 
@@ -390,6 +397,11 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   MMF_HIP(launch_gemm(ga, act, c->stream));
 }
 
+int lm_grid(const Model& m) {
+  const int g = static_cast<int>((m.cfg.vocab_size + kGroup - 1) / kGroup);
+  return g < kLMBlocks ? g : kLMBlocks;
+}
+
 DecArgs dec_base(Model& m) {
   DecArgs a{};
   a.H = static_cast<int>(m.cfg.hidden_size);
@@ -397,8 +409,11 @@ DecArgs dec_base(Model& m) {
   a.vocab = static_cast<int>(m.cfg.vocab_size);
   a.eps = m.cfg.rms_norm_eps;
   a.qs = m.qs;
-  a.emb = m.emb;
-  a.key = m.key.as<unsigned long long>(1);
+  a.embT = static_cast<const float*>(m.embT.p);
+  a.oLc = m.gH.Lc;
+  a.oK8 = m.gH.K8;
+  a.keys = static_cast<unsigned long long*>(m.key.p);
+  a.nkeys = lm_grid(m);
   return a;
 }
 
@@ -407,79 +422,84 @@ void set_proj(mmf_ctx* c, Model& m, DecArgs& a, int slot, int id) {
   a.inv_fixed[slot] = inv_fixed_of(a.p[slot].scale_w, m.frac);
 }
 
-// Single-row lm_head on device row x: logits (may be null) and, if want_key, the argmax
-// key (atomicMax into a cleared key).
+// Single-row lm_head on the chain-transposed device row x: logits (may be null) and, if
+// want_key, the argmax key (atomicMax into a cleared key).
 void lm_single(mmf_ctx* c, Model& m, const float* x, float* logits, bool want_key) {
   DecArgs a = dec_base(m);
   set_proj(c, m, a, 0, m.lm);
   a.x = x;
-  a.pre_w = m.norm_w;
+  a.pre_w = m.norm_wT;
   a.out = logits;
-  if (!want_key) a.key = nullptr;
+  if (!want_key) a.keys = nullptr;
   MMF_HIP(launch_decode(kLM, static_cast<Mode>(m.mode), a, c->stream));
 }
 
-// One single-row decode step for stream 0: reads the token from the argmax key, writes the
-// next key. `kinds` masks which kernel kinds run (timing), `first_from_key` selects the
-// embedding gather of layer 0.
-void decode_launches(mmf_ctx* c, Model& m, unsigned kinds = 0x1F) {
+// One kernel of the single-row decode step for stream 0. `full` = part of a real step:
+// layer 0 then gathers the embedding row of the argmax key (recording it in the token
+// history) and its kO clears the key for this step's lm_head. Timing runs use full =
+// false (layer 0 reads h like the others).
+void decode_one(mmf_ctx* c, Model& m, DecKind kind, size_t l, bool full = false) {
   const Mode mode = static_cast<Mode>(m.mode);
   const size_t H = m.cfg.hidden_size;
-  float* h = m.h.as<float>(H);
-  float* resid = m.resid.as<float>(H);
-  float* g = m.g.as<float>(H);
-  float* recur = m.recur.as<float>(H);
-  float* z = m.z.as<float>(m.cfg.intermediate_size);
+  float* h = static_cast<float*>(m.h.p);
+  float* resid = static_cast<float*>(m.resid.p);
+  float* g = static_cast<float*>(m.g.p);
+  float* recur = static_cast<float*>(m.recur.p);
+  float* z = static_cast<float*>(m.z.p);
   float* state = static_cast<float*>(m.state.p);
-  for (size_t l = 0; l < m.layers.size(); ++l) {
-    const LayerDev& L = m.layers[l];
-    if (kinds & 1) {
-      DecArgs a = dec_base(m);
+  if (kind == kLM) {
+    lm_single(c, m, h, nullptr, true);
+    return;
+  }
+  const LayerDev& L = m.layers[l];
+  DecArgs a = dec_base(m);
+  a.layer = static_cast<int>(l);
+  switch (kind) {
+    case kIFG:
       for (int k = 0; k < 3; ++k) set_proj(c, m, a, k, L.proj[k]);
-      a.layer = static_cast<int>(l);
-      a.x = (l == 0 && kinds == 0x1F) ? nullptr : h;
+      a.x = (l == 0 && full) ? nullptr : h;
       if (a.x == nullptr) {
         a.out = h;  // layer 0: the embedding row becomes h
         a.hist = m.hist.as<int64_t>(1);
         a.hist_pos = m.hist_pos.as<int32_t>(1);
         a.hist_cap = static_cast<int>(m.hist_cap);
       }
-      a.pre_w = L.attn;
+      a.pre_w = L.attnT;
       a.lb = L.lb;
       a.state = state + l * H;
       a.recur = recur;
       a.gout = g;
-      MMF_HIP(launch_decode(kIFG, mode, a, c->stream));
-    }
-    if (kinds & 2) {
-      DecArgs a = dec_base(m);
+      break;
+    case kO:
       set_proj(c, m, a, 0, L.proj[3]);
       a.x = g;
       a.x2 = recur;
-      a.pre_w = L.gn;
+      a.pre_w = L.gnT;
       a.hin = h;
       a.out = resid;
-      if (l == 0 && kinds == 0x1F) a.key_reset = a.key;
-      MMF_HIP(launch_decode(kO, mode, a, c->stream));
-    }
-    if (kinds & 4) {
-      DecArgs a = dec_base(m);
+      break;
+    case kGate:
       set_proj(c, m, a, 0, L.proj[4]);
       a.x = resid;
-      a.pre_w = L.mlp;
+      a.pre_w = L.mlpT;
       a.out = z;
-      MMF_HIP(launch_decode(kGate, mode, a, c->stream));
-    }
-    if (kinds & 8) {
-      DecArgs a = dec_base(m);
+      a.oLc = m.gI.Lc;  // z is I long
+      a.oK8 = m.gI.K8;
+      break;
+    default:  // kDown
       set_proj(c, m, a, 0, L.proj[5]);
       a.x = z;
       a.hin = resid;
       a.out = h;
-      MMF_HIP(launch_decode(kDown, mode, a, c->stream));
-    }
+      break;
   }
-  if (kinds & 16) lm_single(c, m, h, nullptr, true);
+  MMF_HIP(launch_decode(kind, mode, a, c->stream));
+}
+
+void decode_launches(mmf_ctx* c, Model& m) {
+  for (size_t l = 0; l < m.layers.size(); ++l)
+    for (DecKind k : {kIFG, kO, kGate, kDown}) decode_one(c, m, k, l, true);
+  decode_one(c, m, kLM, 0, true);
 }
 
 void decode_step(mmf_ctx* c, Model& m) {
@@ -558,15 +578,19 @@ float* prefill_rows(mmf_ctx* c, Model& m, size_t b, const int64_t* ids, size_t T
   return h;
 }
 
+// The token of the last lm_head: the max over its per-block argmax keys.
 int64_t read_key(mmf_ctx* c, Model& m) {
-  unsigned long long k = 0;
-  MMF_HIP(hipMemcpyAsync(&k, m.key.p, sizeof(k), hipMemcpyDeviceToHost, c->stream));
+  const int n = lm_grid(m);
+  std::vector<unsigned long long> k(n);
+  MMF_HIP(hipMemcpyAsync(k.data(), m.key.p, n * sizeof(unsigned long long), hipMemcpyDeviceToHost, c->stream));
   MMF_HIP(hipStreamSynchronize(c->stream));
-  return key_index(k);
+  unsigned long long best = 0;
+  for (auto v : k) best = v > best ? v : best;
+  return key_index(best);
 }
 
 void clear_key(mmf_ctx* c, Model& m) {
-  MMF_HIP(hipMemsetAsync(m.key.p, 0, sizeof(unsigned long long), c->stream));
+  MMF_HIP(hipMemsetAsync(m.key.p, 0, kLMBlocks * sizeof(unsigned long long), c->stream));
   MMF_HIP(hipMemsetAsync(m.hist_pos.p, 0, sizeof(int32_t), c->stream));
 }
 
@@ -857,10 +881,34 @@ int mmf_model_finalize(mmf_ctx* c, int mode, int frac) {
       }
       Ld.lb = (lb && l > 0) ? lb + l * H : nullptr;  // hgrn_model.cpp:116-117
     }
+    // chain-transposed copies for the single-row decode kernels
+    m.gH = make_geom(static_cast<int>(H), static_cast<int>(H));
+    m.gI = make_geom(static_cast<int>(H), static_cast<int>(I));
+    const size_t WH = chain_len(m.gH), WI = chain_len(m.gI);
+    float* et = m.embT.as<float>(V * WH);
+    MMF_HIP(launch_to_chain(m.emb, et, static_cast<int>(V), static_cast<int>(H), m.gH.Lc, c->stream));
+    const size_t nvec = 2 + L * 8;  // final norm, lm normw; per layer 3 norms + 5 H-long normw (+ down)
+    float* nt = m.normT.as<float>(nvec * WH + L * WI);
+    size_t off = 0;
+    auto tr = [&](const float* src, bool ilong) -> const float* {
+      float* dst = nt + off;
+      off += ilong ? WI : WH;
+      MMF_HIP(launch_to_chain(src, dst, 1, static_cast<int>(ilong ? I : H), ilong ? m.gI.Lc : m.gH.Lc, c->stream));
+      return dst;
+    };
+    m.norm_wT = tr(m.norm_w, false);
+    c->projs[m.lm].d.normwT = tr(c->projs[m.lm].d.normw, false);
+    for (size_t l = 0; l < L; ++l) {
+      LayerDev& Ld = m.layers[l];
+      Ld.attnT = tr(Ld.attn, false);
+      Ld.mlpT = tr(Ld.mlp, false);
+      Ld.gnT = tr(Ld.gn, false);
+      for (int j = 0; j < 6; ++j) c->projs[Ld.proj[j]].d.normwT = tr(c->projs[Ld.proj[j]].d.normw, j == 5);
+    }
     m.mode = mode;
     m.frac = frac;
     m.qs = static_cast<float>(1u << frac);
-    alloc_decode(m);
+    alloc_decode(c, m);
     m.finalized = true;
     drop_graph(m);
     reset_state(c, m, 1);
@@ -895,7 +943,9 @@ int mmf_model_generate(mmf_ctx* c, const int64_t* ids, size_t n, size_t new_toke
       if (out_len) *out_len = len;
       return;
     }
-    lm_single(c, m, h + (n - 1) * m.cfg.hidden_size, nullptr, true);
+    MMF_HIP(launch_to_chain(h + (n - 1) * m.cfg.hidden_size, static_cast<float*>(m.h.p), 1,
+                            static_cast<int>(m.cfg.hidden_size), m.gH.Lc, c->stream));
+    lm_single(c, m, static_cast<float*>(m.h.p), nullptr, true);
     int64_t t = read_key(c, m);
     out[len++] = t;
     if (cb) cb(user, t);
@@ -972,7 +1022,9 @@ int mmf_model_prefill(mmf_ctx* c, size_t stream, const int64_t* ids, size_t n, f
     if (!ids || n == 0) fail(MMF_ERR_ARG, "empty prompt");
     float* h = prefill_rows(c, m, stream, ids, n, nullptr, nullptr, nullptr);
     float* lg = m.logits.as<float>(m.cfg.vocab_size);
-    lm_single(c, m, h + (n - 1) * m.cfg.hidden_size, lg, false);
+    MMF_HIP(launch_to_chain(h + (n - 1) * m.cfg.hidden_size, static_cast<float*>(m.h.p), 1,
+                            static_cast<int>(m.cfg.hidden_size), m.gH.Lc, c->stream));
+    lm_single(c, m, static_cast<float*>(m.h.p), lg, false);
     deliver_rows(c, m, lg, 1, logits, argmax);
   });
 }
@@ -1049,6 +1101,7 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
       drop_graph(m);
     }
     clear_key(c, m);
+    MMF_HIP(hipMemsetAsync(m.hist_pos.p, 0, sizeof(int32_t), c->stream));
     hipEvent_t e0, e1;
     MMF_HIP(hipEventCreate(&e0));
     MMF_HIP(hipEventCreate(&e1));
@@ -1061,17 +1114,30 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
     MMF_HIP(hipEventElapsedTime(&ms, e0, e1));
     if (step_us) *step_us = 1000.0 * ms / reps;
     if (kind_us) {
-      const double launches[5] = {static_cast<double>(m.layers.size()), static_cast<double>(m.layers.size()),
-                                  static_cast<double>(m.layers.size()), static_cast<double>(m.layers.size()), 1.0};
+      // An event pair around every launch: the elapsed time of each pair is that kernel's
+      // execution on the stream, independent of host submission gaps.
+      const size_t L = m.layers.size();
+      std::vector<hipEvent_t> ev(2 * L);
+      for (auto& e : ev) MMF_HIP(hipEventCreate(&e));
       for (int k = 0; k < 5; ++k) {
-        decode_launches(c, m, 1u << k);  // warm
-        MMF_HIP(hipEventRecord(e0, c->stream));
-        for (int i = 0; i < reps; ++i) decode_launches(c, m, 1u << k);
-        MMF_HIP(hipEventRecord(e1, c->stream));
-        MMF_HIP(hipEventSynchronize(e1));
-        MMF_HIP(hipEventElapsedTime(&ms, e0, e1));
-        kind_us[k] = 1000.0 * ms / (reps * launches[k]);
+        const size_t nl = (k == 4) ? 1 : L;
+        double total = 0.0;
+        for (int r = 0; r < reps + 1; ++r) {
+          for (size_t l = 0; l < nl; ++l) {
+            MMF_HIP(hipEventRecord(ev[2 * l], c->stream));
+            decode_one(c, m, static_cast<DecKind>(k), l);
+            MMF_HIP(hipEventRecord(ev[2 * l + 1], c->stream));
+          }
+          MMF_HIP(hipEventSynchronize(ev[2 * nl - 1]));
+          if (r == 0) continue;  // warm-up pass
+          for (size_t l = 0; l < nl; ++l) {
+            MMF_HIP(hipEventElapsedTime(&ms, ev[2 * l], ev[2 * l + 1]));
+            total += ms;
+          }
+        }
+        kind_us[k] = 1000.0 * total / (static_cast<double>(reps) * nl);
       }
+      for (auto& e : ev) (void)hipEventDestroy(e);
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);

@@ -49,7 +49,8 @@ struct ProjDev {
   const uint32_t* pk = nullptr;
   const int8_t* tail = nullptr;
   const int32_t* rowsum = nullptr;
-  const float* normw = nullptr;
+  const float* normw = nullptr;   // BitLinear norm weight [K]
+  const float* normwT = nullptr;  // the same, chain-transposed [8*Lc + 8] (decode kernels)
   Geom g{};
   float scale_w = 1.0f;
   float inv_scale_w = 1.0f;  // 1.0f / scale_w (bitlinear.cpp:28)
@@ -63,26 +64,31 @@ struct DecArgs {
   ProjDev p[3];
   int H, I, vocab, layer, use_lb;
   float eps, qs, inv_fixed[3];
+  // Vectors below are chain-transposed ([8*Lc + 8], zero padding) unless noted.
   const float* x;         // input vector; nullptr for layer 0 (embedding row of *key,
                           // a cleared key or one outside [0, vocab) reads row 0)
-  const float* emb;
+  const float* embT;      // chain-transposed embedding rows [V][8*Lc_H + 8]
   const float* x2;        // kO: recurrence output (silu-gated)
   const float* pre_w;     // stage-1 norm weight (attn / g / mlp / final norm), or nullptr
-  const float* lb;        // lower bound row of this layer (kIFG), or nullptr
+  const float* lb;        // lower bound row of this layer (kIFG; natural order), or nullptr
   const float* hin;       // kO: layer input h; kDown: resid
-  float* state;           // kIFG: this layer's recurrent state [H]
+  int oLc, oK8;           // chain geometry of the output vector
+  float* state;           // kIFG: this layer's recurrent state [H] (natural order)
   float* recur;           // kIFG out
   float* gout;            // kIFG out
   float* out;             // kIFG layer 0: copy of the embedding row (h); kO: resid;
-                          // kGate: z; kDown: next h; kLM: logits (may be null)
-  unsigned long long* key;  // argmax key: written by kLM, read by layer-0 kIFG
-  unsigned long long* key_reset;  // kO of layer 0 clears it
+                          // kGate: z; kDown: next h; kLM: logits (natural, may be null)
+  unsigned long long* keys;  // argmax keys: one per kLM block; reduced by layer-0 kIFG
+  int nkeys;
   int64_t* hist;          // kIFG layer 0: token history, hist[*hist_pos]++ (below hist_cap)
   int32_t* hist_pos;
   int hist_cap;
 };
 
+constexpr int kLMBlocks = 512;  // lm_head grid (grid-stride over the vocabulary)
 hipError_t launch_decode(DecKind kind, Mode mode, const DecArgs& a, hipStream_t s);
+// rows of x [rows, K] -> chain-transposed rows out [rows, 8*Lc + 8]
+hipError_t launch_to_chain(const float* x, float* out, int rows, int K, int Lc, hipStream_t s);
 
 // Argmax key: (orderable float bits << 32) | (0xFFFFFFFF - index): the max key is the first
 // index of the largest value (the reference's strict `>` scan, hgrn_model.cpp:270-273).
