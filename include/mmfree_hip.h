@@ -87,6 +87,11 @@ int mmf_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps,
  * equal shapes sharing the input x; bit-identical to k mmf_bitlinear calls. */
 int mmf_bitlinear_cluster(mmf_ctx* ctx, const int* proj_ids, int k, int mode, int frac_bits,
                           float eps, const float* x, float* const* outs, size_t rows);
+/* The integer input of a FixedQ510 BitLinear, for an external TernaryBackend: the RMSNorm
+ * y = (x * rstd) * normw (bitlinear.cpp:62-70) and its Q5.10 codes (simd.hpp:162-187) as int32
+ * codes [rows, K] (frac_bits fractional bits). dev pointers. */
+int mmf_bitlinear_codes(mmf_ctx* ctx, const float* x, const float* normw, int32_t* codes, size_t rows,
+                        size_t K, float eps, int frac_bits);
 /* rmsnorm (kernels.hpp:29-31, rmsnorm.cpp:11-22) */
 int mmf_rmsnorm(mmf_ctx* ctx, float* y, const float* x, const float* w, size_t rows, size_t cols,
                 float eps);

@@ -764,6 +764,18 @@ int mmf_bitlinear_cluster(mmf_ctx* c, const int* ids, int k, int mode, int frac,
   });
 }
 
+int mmf_bitlinear_codes(mmf_ctx* c, const float* x, const float* normw, int32_t* codes, size_t rows, size_t K,
+                        float eps, int frac) {
+  return guard(c, [&] {
+    if (frac < 0 || frac > 30) fail(MMF_ERR_ARG, "invalid frac_bits");
+    if (!rows || !K) return;
+    float* y = c->opy.as<float>(rows * K);
+    MMF_HIP(launch_rmsnorm(x, normw, y, static_cast<int>(rows), static_cast<int>(K), eps, c->stream));
+    MMF_HIP(launch_quant_rows(y, codes, static_cast<int>(rows), static_cast<int>(K), static_cast<float>(1u << frac),
+                              c->stream));
+  });
+}
+
 int mmf_rmsnorm(mmf_ctx* c, float* y, const float* x, const float* w, size_t rows, size_t cols, float eps) {
   return guard(c, [&] {
     if (rows && cols) MMF_HIP(launch_rmsnorm(x, w, y, static_cast<int>(rows), static_cast<int>(cols), eps, c->stream));

@@ -157,6 +157,8 @@ hipError_t launch_embed(const float* emb, const int64_t* ids, float* h, int rows
 // Final RMSNorm rows (hgrn_model.cpp:235,440): plain rmsnorm kernel.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps,
                           hipStream_t s);
+// Q5.10 codes of rows y [rows, K] (SIMD body / scalar tail per row).
+hipError_t launch_quant_rows(const float* y, int32_t* q, int rows, int K, float qs, hipStream_t s);
 // Row argmax over [rows, V] logits -> ids.
 hipError_t launch_argmax_rows(const float* logits, int rows, int V, int64_t* ids, hipStream_t s);
 // Elementwise ops for the op-level API (kernels.hpp:54-68).

@@ -506,6 +506,15 @@ __global__ void k_argmax_rows(const float* __restrict__ lg, int V, int64_t* __re
   }
 }
 
+__global__ void k_quant_rows(const float* __restrict__ y, int32_t* __restrict__ q, int rows, int K, float qs) {
+  const size_t n = static_cast<size_t>(rows) * K;
+  for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int k = static_cast<int>(e % K);
+    q[e] = (k < (K & ~7)) ? q510_body(y[e], qs) : q510_tail(y[e], qs);
+  }
+}
+
 __global__ void k_swiglu(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
                          size_t n) {
   const size_t body = n & ~static_cast<size_t>(7);
@@ -627,6 +636,13 @@ hipError_t launch_swishgate(const float* g, const float* o, const float* w, floa
 
 hipError_t launch_argmax_rows(const float* logits, int rows, int V, int64_t* ids, hipStream_t s) {
   k_argmax_rows<<<rows, 1024, 0, s>>>(logits, V, ids);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const float* y, int32_t* q, int rows, int K, float qs, hipStream_t s) {
+  const size_t n = static_cast<size_t>(rows) * K;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
+  k_quant_rows<<<blocks > 0 ? blocks : 1, 256, 0, s>>>(y, q, rows, K, qs);
   return hipGetLastError();
 }
 

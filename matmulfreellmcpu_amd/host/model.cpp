@@ -1,0 +1,223 @@
+// model.cpp -- mmfree::Model on the MI355X through the mmfree_hip.h C ABI.
+//
+// The model compute (prefill time scan, single-row decode kernels, batched serving steps,
+// lm_head) runs on the GPU. Greedy generation stays on the device between tokens
+// (mmf_model_generate); sampled generation brings each step's logits back and samples on the
+// host with the reference's procedure (hgrn_model.cpp:263-303, 368-406): std::mt19937_64,
+// uniform_real_distribution<double>, nth_element top-k, max-shifted exp of float differences
+// divided by the temperature, cumulative search -- so equal logits give equal samples.
+#include "mmfree/model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <random>
+#include <stdexcept>
+#include <string>
+
+#include "mmfree/hip_backend.hpp"
+#include "mmfree/profile.hpp"
+#include "mmfree_hip.h"
+
+namespace mmfree {
+namespace {
+
+void check(mmf_ctx* c, int rc, const char* what) {
+  if (rc != MMF_OK) throw std::runtime_error(std::string(what) + ": " + mmf_last_error(c));
+}
+
+int device_index() {
+  const char* e = std::getenv("MMFREE_DEVICE");
+  return e ? std::atoi(e) : 0;
+}
+
+int mode_of(ActQuant aq) {
+  switch (aq) {
+    case ActQuant::FixedQ510: return MMF_FIXED_Q510;
+    case ActQuant::Int8Absmax: return MMF_INT8_ABSMAX;
+    default: return MMF_FLOAT;
+  }
+}
+
+// One sampling decision over logits [V] (greedy: first index of the maximum).
+std::int64_t pick(const float* lg, std::size_t V, const Sampling& s, std::mt19937_64& rng,
+                  std::vector<std::size_t>& cand) {
+  if (s.temperature <= 0.0f) {
+    std::size_t best = 0;
+    for (std::size_t v = 1; v < V; ++v)
+      if (lg[v] > lg[best]) best = v;
+    return static_cast<std::int64_t>(best);
+  }
+  cand.resize(V);
+  for (std::size_t v = 0; v < V; ++v) cand[v] = v;
+  const std::size_t k = (s.top_k > 0 && static_cast<std::size_t>(s.top_k) < V) ? static_cast<std::size_t>(s.top_k) : V;
+  if (k < V) {
+    std::nth_element(cand.begin(), cand.begin() + k, cand.end(),
+                     [&](std::size_t a, std::size_t b) { return lg[a] > lg[b]; });
+    cand.resize(k);
+  }
+  float top = lg[cand[0]];
+  for (std::size_t j = 1; j < cand.size(); ++j) top = std::max(top, lg[cand[j]]);
+  std::vector<double> w(cand.size());
+  double total = 0.0;
+  for (std::size_t j = 0; j < cand.size(); ++j) {
+    w[j] = std::exp((lg[cand[j]] - top) / s.temperature);  // float expression, as the reference
+    total += w[j];
+  }
+  std::uniform_real_distribution<double> uni(0.0, 1.0);
+  const double r = uni(rng) * total;
+  double acc = 0.0;
+  for (std::size_t j = 0; j < cand.size(); ++j) {
+    acc += w[j];
+    if (r <= acc) return static_cast<std::int64_t>(cand[j]);
+  }
+  return static_cast<std::int64_t>(cand.back());
+}
+
+void trampoline(void* user, std::int64_t id) { (*static_cast<const std::function<void(std::int64_t)>*>(user))(id); }
+
+}  // namespace
+
+Model::Model(const Weights& w, ActQuant aq, int frac_bits) : cfg_(w.config()), aq_(aq), frac_bits_(frac_bits) {
+  const int rc = mmf_create(&ctx_, device_index());
+  if (rc != MMF_OK) throw std::runtime_error(std::string("mmfree: ") + mmf_last_error(nullptr));
+  try {
+    mmf_config c{cfg_.vocab_size, cfg_.hidden_size, cfg_.num_hidden_layers, cfg_.intermediate_size,
+                 cfg_.use_lower_bound ? 1 : 0, cfg_.rms_norm_eps};
+    check(ctx_, mmf_model_begin(ctx_, &c), "mmf_model_begin");
+    for (const std::string& name : w.names()) {
+      const TensorRef& t = w.get(name);
+      check(ctx_, mmf_model_tensor(ctx_, name.c_str(), t.is_int8 ? 1 : 0, t.shape.data(), static_cast<int>(t.shape.size()),
+                                   t.data),
+            "mmf_model_tensor");
+    }
+    check(ctx_, mmf_model_finalize(ctx_, mode_of(aq), frac_bits), "mmf_model_finalize");
+  } catch (...) {
+    mmf_destroy(ctx_);
+    ctx_ = nullptr;
+    throw;
+  }
+}
+
+Model::~Model() { mmf_destroy(ctx_); }
+
+void Model::set_backend(TernaryBackend* be, std::unordered_map<std::string, int> proj_ids) {
+  (void)proj_ids;
+  if (be && !dynamic_cast<HipTernaryBackend*>(be))
+    throw std::runtime_error(
+        "mmfree: this Model runs the ternary projections on the GPU; a CPU/FPGA TernaryBackend "
+        "can be used with the operator functions (bitlinear) instead");
+}
+
+void Model::forward(const std::int64_t* ids, std::size_t T, std::vector<float>& logits) {
+  MMFREE_PROFILE("forward");
+  logits.assign(T * cfg_.vocab_size, 0.0f);
+  check(ctx_, mmf_model_forward(ctx_, ids, T, logits.data()), "mmf_model_forward");
+}
+
+std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, std::size_t new_tokens,
+                                          std::int64_t eos_id, const Sampling& samp,
+                                          const std::function<void(std::int64_t)>& on_token) {
+  if (ids.empty()) throw std::runtime_error("mmfree: generate needs at least one prompt token");
+  streams_ = 1;
+  if (samp.temperature <= 0.0f) {  // greedy: the decode loop stays on the device
+    MMFREE_PROFILE("generate");
+    std::vector<std::int64_t> out(ids.size() + new_tokens);
+    std::size_t len = 0;
+    check(ctx_,
+          mmf_model_generate(ctx_, ids.data(), ids.size(), new_tokens, eos_id, out.data(), out.size(), &len,
+                             on_token ? &trampoline : nullptr,
+                             on_token ? const_cast<void*>(static_cast<const void*>(&on_token)) : nullptr),
+          "mmf_model_generate");
+    out.resize(len);
+    return out;
+  }
+  const std::size_t V = cfg_.vocab_size;
+  std::vector<std::int64_t> stream = ids;
+  std::vector<float> lg(V);
+  std::vector<std::size_t> cand;
+  std::mt19937_64 rng(samp.seed);
+  check(ctx_, mmf_model_reset(ctx_, 1), "mmf_model_reset");
+  {
+    MMFREE_PROFILE("prefill");
+    check(ctx_, mmf_model_prefill(ctx_, 0, ids.data(), ids.size(), lg.data(), nullptr), "mmf_model_prefill");
+  }
+  if (new_tokens == 0) return stream;
+  for (std::size_t step = 0; step < new_tokens; ++step) {
+    if (step > 0) {
+      MMFREE_PROFILE("decode");
+      const std::int64_t t = stream.back();
+      check(ctx_, mmf_model_step(ctx_, &t, lg.data(), nullptr), "mmf_model_step");
+    }
+    std::int64_t t;
+    {
+      MMFREE_PROFILE("sample");
+      t = pick(lg.data(), V, samp, rng, cand);
+    }
+    stream.push_back(t);
+    if (on_token) on_token(t);
+    if (t == eos_id) break;
+  }
+  return stream;
+}
+
+std::vector<std::vector<std::int64_t>> Model::generate_serve(
+    const std::vector<std::vector<std::int64_t>>& prompts, std::size_t new_tokens, std::int64_t eos_id,
+    const Sampling& samp, const std::function<void(std::size_t, std::int64_t)>& on_token) {
+  const std::size_t B = prompts.size(), V = cfg_.vocab_size;
+  std::vector<std::vector<std::int64_t>> streams = prompts;
+  if (B == 0) return streams;
+  for (const auto& p : prompts)
+    if (p.empty()) throw std::runtime_error("mmfree: generate_serve needs a token in every prompt");
+  const bool greedy = samp.temperature <= 0.0f;
+  std::vector<std::mt19937_64> rng;
+  rng.reserve(B);
+  for (std::size_t b = 0; b < B; ++b) rng.emplace_back(samp.seed + b);
+  std::vector<std::size_t> cand;
+  std::vector<char> done(B, 0);
+  std::vector<float> lg(greedy ? 0 : B * V);
+  std::vector<std::int64_t> am(B);
+  check(ctx_, mmf_model_reset(ctx_, B), "mmf_model_reset");
+  streams_ = B;
+  // per-stream prefill, staggered first-token callbacks (model.hpp:60-66 of the reference)
+  for (std::size_t b = 0; b < B; ++b) {
+    {
+      MMFREE_PROFILE("prefill");
+      check(ctx_, mmf_model_prefill(ctx_, b, prompts[b].data(), prompts[b].size(), greedy ? nullptr : lg.data(),
+                                    &am[b]),
+            "mmf_model_prefill");
+    }
+    const std::int64_t t0 = greedy ? am[b] : pick(lg.data(), V, samp, rng[b], cand);
+    streams[b].push_back(t0);
+    if (on_token) on_token(b, t0);
+    if (t0 == eos_id) done[b] = 1;
+  }
+  if (new_tokens <= 1) return streams;
+  std::vector<std::int64_t> tok(B);
+  for (std::size_t step = 1; step < new_tokens; ++step) {
+    for (std::size_t b = 0; b < B; ++b) tok[b] = streams[b].back();
+    {
+      MMFREE_PROFILE("decode");
+      check(ctx_, mmf_model_step(ctx_, tok.data(), greedy ? nullptr : lg.data(), am.data()), "mmf_model_step");
+    }
+    bool all_done = true;
+    for (std::size_t b = 0; b < B; ++b) {
+      if (done[b]) continue;
+      const std::int64_t t = greedy ? am[b] : pick(lg.data() + b * V, V, samp, rng[b], cand);
+      streams[b].push_back(t);
+      if (on_token) on_token(b, t);
+      if (t == eos_id) done[b] = 1;
+      else all_done = false;
+    }
+    if (all_done) break;
+  }
+  return streams;
+}
+
+std::vector<float> Model::state() const {
+  std::vector<float> st(cfg_.num_hidden_layers * streams_ * cfg_.hidden_size);
+  check(ctx_, mmf_model_state(ctx_, st.data()), "mmf_model_state");
+  return st;
+}
+
+}  // namespace mmfree

@@ -117,6 +117,9 @@ void* ref_model_open(const char* blob, int mode, int frac_bits) {
 
 void ref_model_close(void* h) { delete static_cast<RefModel*>(h); }
 
+// The reference Model object itself (for attaching a TernaryBackend, ref_hipbe.cpp).
+void* ref_model_ptr(void* h) { return static_cast<RefModel*>(h)->m.get(); }
+
 // Model::generate; writes the full id stream into out_ids (capacity cap) and returns its
 // length. Sampling per model.hpp:27-31.
 long ref_model_generate(void* h, const std::int64_t* ids, std::size_t n, std::size_t new_tokens,
