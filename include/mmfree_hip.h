@@ -160,6 +160,23 @@ int mmf_model_trace(mmf_ctx* ctx, const int64_t* ids, size_t T, float* h, float*
  * per launch of the kernel kinds {IFG, O, GATE, DOWN, LM} (kind_us[5], may be NULL). */
 int mmf_model_time_decode(mmf_ctx* ctx, int warmup, int reps, double* step_us, double* kind_us);
 
+/* Timing of the prefill (prompt of T ids through all layers, then the final norm, lm_head
+ * and argmax of the last position -- the reference bench's time to the first token,
+ * bench.cpp:47-63) on the context's stream: average microseconds per prefill over `reps`
+ * runs after `warmup` (one HIP event pair around the runs), and, if kind_us (8 doubles) is
+ * not NULL, the microseconds per prefill spent in each launch kind {BitLinear prologues,
+ * i/f/g GEMM, mixer/recurrence, o GEMM, gate GEMM (+swiglu), down GEMM, final norm +
+ * lm_head, embedding} from an event pair around every launch (a second set of runs).
+ * No counterpart in the reference engine: measurement only. */
+int mmf_model_time_prefill(mmf_ctx* ctx, const int64_t* ids, size_t T, int warmup, int reps,
+                           double* total_us, double* kind_us);
+
+/* Timing of mmf_bitlinear on device buffers (same arguments): average microseconds per call,
+ * and of its two launches (prologue: RMSNorm + activation codes; GEMM). Measurement only. */
+int mmf_time_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps, const float* x,
+                       float* out, size_t rows, int warmup, int reps, double* total_us,
+                       double* prologue_us, double* gemm_us);
+
 #ifdef __cplusplus
 }
 #endif

@@ -80,6 +80,9 @@ def load_library(path: str = LIB_PATH):
         "mmf_model_forward": (i, [_vp, _i64p, _sz, _fp]),
         "mmf_model_trace": (i, [_vp, _i64p, _sz, _fp, _fp, _fp]),
         "mmf_model_time_decode": (i, [_vp, i, i, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "mmf_model_time_prefill": (i, [_vp, _i64p, _sz, i, i, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "mmf_time_bitlinear": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, i, i, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -270,6 +273,25 @@ class Engine:
         kinds = (C.c_double * 5)()
         self._chk(self.lib.mmf_model_time_decode(self.h, warmup, reps, C.byref(step), kinds))
         return step.value, dict(zip(("ifg", "o", "gate", "down", "lm"), list(kinds)))
+
+    PREFILL_KINDS = ("prologue", "gemm_ifg", "mixer", "gemm_o", "gemm_gate", "gemm_down", "lm", "embed")
+
+    def time_prefill(self, ids, warmup=1, reps=3, kinds=True):
+        """Microseconds per prefill (prompt through all layers + final norm/lm_head/argmax of
+        the last position) and, with kinds, the microseconds per prefill of each launch kind."""
+        ids, _ = _np(ids, np.int64)
+        total = C.c_double()
+        k = (C.c_double * 8)()
+        self._chk(self.lib.mmf_model_time_prefill(self.h, ids.ctypes.data_as(_i64p), ids.size, warmup, reps,
+                                                  C.byref(total), k if kinds else None))
+        return total.value, (dict(zip(self.PREFILL_KINDS, list(k))) if kinds else None)
+
+    def time_bitlinear(self, proj_id, x, out, rows, mode=FLOAT, frac_bits=10, eps=1e-6, warmup=3, reps=20):
+        """(total, prologue, gemm) microseconds per mmf_bitlinear call on device buffers."""
+        t, p, g = C.c_double(), C.c_double(), C.c_double()
+        self._chk(self.lib.mmf_time_bitlinear(self.h, proj_id, mode, frac_bits, eps, _ptr(x), _ptr(out), rows,
+                                              warmup, reps, C.byref(t), C.byref(p), C.byref(g)))
+        return t.value, p.value, g.value
 
 
 def make_blob(path: str, preset: str | None = None, seed: int = 1234, vocab=None, hidden=None, layers=None,

@@ -114,6 +114,30 @@ struct Model {
   bool graph_tried = false;
 };
 
+// Optional per-launch timing of the row path: an event pair around each launch, summed
+// per kind after the run (the elapsed time of a pair is that kernel's execution on the
+// stream, independent of host submission gaps).
+enum RowKind : int { kRkPrologue, kRkGemmIFG, kRkMixer, kRkGemmO, kRkGemmGate, kRkGemmDown, kRkLM, kRkOther,
+                     kRkCount };
+
+struct RowTimer {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<int> kinds;  // kind of event pair i (events 2i, 2i+1)
+  size_t used = 0;
+  hipEvent_t take() {
+    if (used == pool.size()) {
+      hipEvent_t e;
+      MMF_HIP(hipEventCreate(&e));
+      pool.push_back(e);
+    }
+    return pool[used++];
+  }
+  ~RowTimer() {
+    for (auto e : pool) (void)hipEventDestroy(e);
+  }
+};
+
 }  // namespace
 
 struct mmf_ctx {
@@ -125,6 +149,7 @@ struct mmf_ctx {
   DBuf raw;  // staging for int8 weights before the repack
   DBuf opy, opq, opct, opsa, opstate;
   hipDeviceProp_t prop{};
+  RowTimer timer;
 };
 
 namespace {
@@ -170,9 +195,12 @@ int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float sc
   const size_t npad = static_cast<size_t>(g.ngroups) * kGroup;
   const size_t b_pk = words * 4, b_tail = npad * 8, b_rs = npad * 4, b_nw = normw_host ? K * 4 : 0;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-  MMF_HIP(hipMalloc(&P.mem, al(b_pk) + al(b_tail) + al(b_rs) + al(b_nw) + 256));
+  const size_t b_pkm = pkm_words(g) * 4;
+  MMF_HIP(hipMalloc(&P.mem, al(b_pk) + al(b_pkm) + al(b_tail) + al(b_rs) + al(b_nw) + 256));
   char* base = static_cast<char*>(P.mem);
   P.d.pk = reinterpret_cast<uint32_t*>(base);
+  P.d.pkm = reinterpret_cast<uint32_t*>(base + al(b_pk));
+  base += al(b_pkm);
   P.d.tail = reinterpret_cast<int8_t*>(base + al(b_pk));
   P.d.rowsum = reinterpret_cast<int32_t*>(base + al(b_pk) + al(b_tail));
   float* nw = reinterpret_cast<float*>(base + al(b_pk) + al(b_tail) + al(b_rs));
@@ -192,8 +220,18 @@ int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float sc
     fail(MMF_ERR_ARG, "projection weights must be ternary (-1, 0, +1)");
   }
   MMF_HIP(e);
+  MMF_HIP(launch_pack_mfma(P.d.pk, g, false, const_cast<uint32_t*>(P.d.pkm), c->stream));
   c->projs.push_back(P);
   return static_cast<int>(c->projs.size() - 1);
+}
+
+void tbeg(mmf_ctx* c, int kind) {
+  if (!c->timer.on) return;
+  c->timer.kinds.push_back(kind);
+  MMF_HIP(hipEventRecord(c->timer.take(), c->stream));
+}
+void tend(mmf_ctx* c) {
+  if (c->timer.on) MMF_HIP(hipEventRecord(c->timer.take(), c->stream));
 }
 
 // ---- activation buffers ---------------------------------------------------------------
@@ -287,7 +325,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
   float* rb = s.recur.as<float>(static_cast<size_t>(rows) * H);
   float* resid = s.resid.as<float>(static_cast<size_t>(rows) * H);
   float* zb = s.z.as<float>(static_cast<size_t>(rows) * I * 2);
-  float* scan = trace_dev ? s.scan.as<float>(static_cast<size_t>(rows) * H) : nullptr;
+  float* scan = (trace_dev || (!stream_state && rows > 1)) ? s.scan.as<float>(static_cast<size_t>(rows) * H) : nullptr;
 
   // attention: attn_norm -> i/f/g BitLinears (hgrn_model.cpp:95-107)
   {
@@ -301,15 +339,21 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     for (int k = 0; k < 3; ++k) pa.normw[k] = proj_of(c, L.proj[k]).d.normw;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
+    tbeg(c, kRkPrologue);
     MMF_HIP(launch_prologue(mode, pa, act, st));
+    tend(c);
     GemmArgs ga = gemm_args(c, L.proj, 3, rows, mode, m.frac);
     ga.out[0] = ib;
     ga.out[1] = fb;
     ga.out[2] = gb;
+    tbeg(c, kRkGemmIFG);
     MMF_HIP(launch_gemm(ga, act, st));
+    tend(c);
   }
   // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
+  tbeg(c, kRkMixer);
   MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, st));
+  tend(c);
   if (trace_dev) {
     const size_t n = static_cast<size_t>(rows) * H * sizeof(float);
     MMF_HIP(hipMemcpyAsync(trace_dev + 0 * rows * H, ib, n, hipMemcpyDeviceToDevice, st));
@@ -331,12 +375,16 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.normw[0] = proj_of(c, L.proj[3]).d.normw;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
+    tbeg(c, kRkPrologue);
     MMF_HIP(launch_prologue(mode, pa, act, st));
+    tend(c);
     GemmArgs ga = gemm_args(c, &L.proj[3], 1, rows, mode, m.frac);
     ga.epi = kEpiAdd;
     ga.add = h;
     ga.out[0] = resid;
+    tbeg(c, kRkGemmO);
     MMF_HIP(launch_gemm(ga, act, st));
+    tend(c);
   }
   // mlp_norm -> gate_proj -> swiglu (hgrn_model.cpp:167-185)
   {
@@ -350,12 +398,16 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.normw[0] = proj_of(c, L.proj[4]).d.normw;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
+    tbeg(c, kRkPrologue);
     MMF_HIP(launch_prologue(mode, pa, act, st));
+    tend(c);
     GemmArgs ga = gemm_args(c, &L.proj[4], 1, rows, mode, m.frac);
     ga.epi = kEpiSwigluPair;
     ga.out[0] = zb;
     ga.swiglu_n = rows * I;
+    tbeg(c, kRkGemmGate);
     MMF_HIP(launch_gemm(ga, act, st));
+    tend(c);
   }
   // down_proj -> h = resid + d (hgrn_model.cpp:187-194)
   {
@@ -368,12 +420,16 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.normw[0] = proj_of(c, L.proj[5]).d.normw;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
+    tbeg(c, kRkPrologue);
     MMF_HIP(launch_prologue(mode, pa, act, st));
+    tend(c);
     GemmArgs ga = gemm_args(c, &L.proj[5], 1, rows, mode, m.frac);
     ga.epi = kEpiAdd;
     ga.add = resid;
     ga.out[0] = h;
+    tbeg(c, kRkGemmDown);
     MMF_HIP(launch_gemm(ga, act, st));
+    tend(c);
   }
 }
 
@@ -556,7 +612,9 @@ float* prefill_rows(mmf_ctx* c, Model& m, size_t b, const int64_t* ids, size_t T
   int64_t* dids = s.ids.as<int64_t>(T);
   MMF_HIP(hipMemcpyAsync(dids, ids, T * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
   float* h = s.h.as<float>(T * H);
+  tbeg(c, kRkOther);
   MMF_HIP(launch_embed(m.emb, dids, h, static_cast<int>(T), static_cast<int>(H), c->stream));
+  tend(c);
   float* tint = nullptr;
   DBuf tbuf;
   if (trace_int) tint = tbuf.as<float>(5 * T * H);
@@ -744,12 +802,64 @@ static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac
   for (int z = 0; z < k; ++z) pa.normw[z] = proj_of(c, ids[z]).d.normw;
   pa.eps = eps;
   pa.qs = static_cast<float>(1u << frac);
+  tbeg(c, kRkPrologue);
   MMF_HIP(launch_prologue(static_cast<Mode>(mode), pa, act, c->stream));
+  tend(c);
   GemmArgs ga = gemm_args(c, ids, k, static_cast<int>(rows), static_cast<Mode>(mode), frac);
   for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
   ga.acc[0] = acc;
+  tbeg(c, kRkGemmIFG);
   MMF_HIP(launch_gemm(ga, act, c->stream));
+  tend(c);
 }
+
+extern "C++" {
+// Runs f() `reps` times with the row timer on and adds each kind's average microseconds
+// per run to kind_us[kRkCount].
+template <class F>
+void time_kinds(mmf_ctx* c, int reps, F&& f, double* kind_us) {
+  RowTimer& t = c->timer;
+  t.used = 0;
+  t.kinds.clear();
+  t.on = true;
+  try {
+    for (int r = 0; r < reps; ++r) f();
+  } catch (...) {
+    t.on = false;
+    throw;
+  }
+  t.on = false;
+  MMF_HIP(hipStreamSynchronize(c->stream));
+  for (int k = 0; k < kRkCount; ++k) kind_us[k] = 0.0;
+  for (size_t i = 0; i < t.kinds.size(); ++i) {
+    float ms = 0.0f;
+    MMF_HIP(hipEventElapsedTime(&ms, t.pool[2 * i], t.pool[2 * i + 1]));
+    kind_us[t.kinds[i]] += 1000.0 * ms / reps;
+  }
+}
+
+// Average microseconds per run of f() over `reps` runs after `warmup`, one event pair
+// around the whole batch of runs.
+template <class F>
+double time_runs(mmf_ctx* c, int warmup, int reps, F&& f) {
+  for (int i = 0; i < warmup; ++i) f();
+  hipEvent_t e0, e1;
+  MMF_HIP(hipEventCreate(&e0));
+  MMF_HIP(hipEventCreate(&e1));
+  float ms = 0.0f;
+  hipError_t err = hipEventRecord(e0, c->stream);
+  if (err == hipSuccess) {
+    for (int i = 0; i < reps; ++i) f();
+    err = hipEventRecord(e1, c->stream);
+  }
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  MMF_HIP(err);
+  return 1000.0 * ms / reps;
+}
+}  // extern "C++"
 
 int mmf_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out, size_t rows,
                   int32_t* acc) {
@@ -890,6 +1000,12 @@ int mmf_model_finalize(mmf_ctx* c, int mode, int frac) {
       for (int j = 0; j < 6; ++j) {
         const size_t N = j == 4 ? 2 * I : H, K = j == 5 ? I : H;
         Ld.proj[j] = proj(p + "." + names[j], N, K);
+      }
+      // the gate matrix feeds swiglu(gate, up): interleave its halves in the tile order
+      ProjDev& gd = c->projs[Ld.proj[4]].d;
+      if (!gd.pair && pkm_pairable(gd.g)) {
+        MMF_HIP(launch_pack_mfma(gd.pk, gd.g, true, const_cast<uint32_t*>(gd.pkm), c->stream));
+        gd.pair = 1;
       }
       Ld.lb = (lb && l > 0) ? lb + l * H : nullptr;  // hgrn_model.cpp:116-117
     }
@@ -1153,6 +1269,43 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+  });
+}
+
+int mmf_time_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out, size_t rows,
+                       int warmup, int reps, double* total_us, double* prologue_us, double* gemm_us) {
+  return guard(c, [&] {
+    if (reps < 1 || warmup < 0 || rows == 0) fail(MMF_ERR_ARG, "invalid reps/rows");
+    auto f = [&] { bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, nullptr); };
+    const double t = time_runs(c, warmup, reps, f);
+    if (total_us) *total_us = t;
+    if (prologue_us || gemm_us) {
+      double k[kRkCount];
+      time_kinds(c, reps, f, k);
+      if (prologue_us) *prologue_us = k[kRkPrologue];
+      if (gemm_us) *gemm_us = k[kRkGemmIFG];
+    }
+  });
+}
+
+int mmf_model_time_prefill(mmf_ctx* c, const int64_t* ids, size_t T, int warmup, int reps, double* total_us,
+                           double* kind_us) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (!ids || T == 0 || reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid prompt/reps");
+    if (m.streams != 1) reset_state(c, m, 1);
+    const int H = static_cast<int>(m.cfg.hidden_size);
+    auto f = [&] {
+      float* h = prefill_rows(c, m, 0, ids, T, nullptr, nullptr, nullptr);
+      tbeg(c, kRkLM);
+      MMF_HIP(launch_to_chain(h + (T - 1) * static_cast<size_t>(H), static_cast<float*>(m.h.p), 1, H, m.gH.Lc,
+                              c->stream));
+      lm_single(c, m, static_cast<float*>(m.h.p), nullptr, true);
+      tend(c);
+    };
+    const double t = time_runs(c, warmup, reps, f);
+    if (total_us) *total_us = t;
+    if (kind_us) time_kinds(c, reps, f, kind_us);
   });
 }
 

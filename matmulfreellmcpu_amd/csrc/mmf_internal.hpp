@@ -47,6 +47,8 @@ __host__ __device__ inline Geom make_geom(int N, int K) {
 // Device view of one resident projection.
 struct ProjDev {
   const uint32_t* pk = nullptr;
+  const uint32_t* pkm = nullptr;  // the same words in the matrix-core tile order (mmf_mfma.hip)
+  int pair = 0;                   // pkm interleaves the two halves (MLP gate/up) by 32-column group
   const int8_t* tail = nullptr;
   const int32_t* rowsum = nullptr;
   const float* normw = nullptr;   // BitLinear norm weight [K]
@@ -143,11 +145,19 @@ struct GemmArgs {
   int32_t* acc[3];     // optional int32 accumulators [rows, N]
   int swiglu_n;        // kEpiSwigluPair: rows * (N/2), for the tail rule
 };
+// Dispatches the integer modes to the matrix-core kernel (mmf_mfma.hip) from
+// mfma_min_rows() rows on, everything else to the dot-product kernel.
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+// Rows from which the integer modes use the matrix cores (MMF_MFMA_MIN_ROWS, default 32;
+// 0 disables them).
+int mfma_min_rows();
 
 // HGRN gate + recurrence over rows (hgrn_model.cpp:109-150). i, f, g: [rows, H].
 // stream_state = false: rows are time steps of one sequence, state [H] carried in order.
 // stream_state = true: rows are independent streams, state [rows, H].
+// f is overwritten with the gated forget values; scan_out (the recurrence input, [rows, H])
+// is required scratch for a time scan of more than one row and may be null otherwise.
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
                         const float* lb, int rows, int H, bool stream_state, hipStream_t s);
 
@@ -171,5 +181,10 @@ hipError_t launch_scan(const float* i, const float* f, float* out, float* state,
 // ---- weight repack (mmf_ops.hip) ----------------------------------------------------------
 hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* tail, int32_t* rowsum,
                        hipStream_t s);
+// slab words -> matrix-core tile order (pair: interleave the two halves by 32-column group,
+// which needs N % 64 == 0); pkm holds pkm_words(g) words.
+size_t pkm_words(const Geom& g);
+bool pkm_pairable(const Geom& g);
+hipError_t launch_pack_mfma(const uint32_t* pk, const Geom& g, bool pair, uint32_t* pkm, hipStream_t s);
 
 }  // namespace mmf

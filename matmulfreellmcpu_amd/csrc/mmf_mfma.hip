@@ -1,0 +1,342 @@
+// mmf_mfma.hip -- the ternary GEMM of the integer modes on the CDNA4 matrix cores.
+//
+// C[row, o] = sum_p A[row, p] * W[o, p] over the chain-permuted positions p < 8*Lc, with
+// A the int8 activation planes (FixedQ510: hi and lo planes of the split Q5.10 code; Int8:
+// one plane) and W the ternary weights. Every product and sum is exact in int32, so the
+// order in which the matrix cores add them does not matter: the result equals the
+// reference's integer dot products (simd.hpp:125-154) bit for bit.
+//
+// Instruction: v_mfma_i32_32x32x32_i8 (on gfx950 it issues at about 1.6x the int8 rate of
+// the 16x16x64 form). Lane l supplies row (l % 32) of A and column (l % 32) of B, 16 int8
+// values each, for position group l / 32; the output tile puts C[8*(i/4) + 4*(l/32) + i%4]
+// [l % 32] in accumulator i of lane l. A and B use the same (lane group, byte) -> position
+// map, so any assignment of positions to bytes that is the same for both gives the exact
+// dot product.
+//
+// Weights ("pkm" layout): for physical 32-column group cg and 32-position block kb, the 64
+// words of lanes l = 32*kq + ol are contiguous: pkm[(cg * nK32 + kb) * 64 + l] holds the 16
+// codes of column 32*cg + ol at positions 32*kb + 16*kq + [0, 16) -- one word of the slab
+// layout, so a wave reads 256 contiguous bytes per fragment and expands each word to its
+// 16-byte B operand with four v_perm_b32. For the MLP gate matrix the groups are interleaved
+// (gate group c at cg = 2c, its up partner N/2 + 32c at cg = 2c + 1) so that one wave holds
+// both halves of swiglu(gate, up) (hgrn_model.cpp:171-185) in registers.
+//
+// Block: WM x WN waves (2 x 4 for long row ranges and wide matrices: 128 x 256 tiles, so
+// the activations are re-read once per 256 columns), each wave a 64 x 64 tile (2 x 2
+// fragments).
+// The operands of each 64-position stage travel from global memory to LDS by direct DMA
+// (global_load_lds: lane l's 16 or 4 bytes land at LDS base + 16l or 4l), laid out in the
+// matrix cores' own lane order, so every fragment read is one linear 1 KB (A) or 256 B (B)
+// LDS access. A ring of S stages keeps S - 1 stages in flight; each wave waits for its own
+// transfers (s_waitcnt vmcnt) and one barrier per stage publishes them to the block.
+#include "mmf_device.hpp"
+#include "mmf_internal.hpp"
+
+namespace mmf {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__global__ void k_pack_mfma(const uint32_t* __restrict__ pk, Geom g, int pair, uint32_t* __restrict__ pkm) {
+  const int nK32 = g.Lc / 4;
+  const int ng32 = (g.N + 31) / 32;
+  const size_t total = static_cast<size_t>(ng32) * nK32 * 64;
+  for (size_t w = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; w < total;
+       w += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int l = static_cast<int>(w & 63);
+    const size_t t = w >> 6;
+    const int kb = static_cast<int>(t % nK32);
+    const int cg = static_cast<int>(t / nK32);
+    const int lcg = pair ? ((cg & 1) ? ng32 / 2 + (cg >> 1) : (cg >> 1)) : cg;
+    const int col = lcg * 32 + (l & 31), kq = l >> 5;
+    const int p0 = kb * 32 + kq * 16;
+    const int j = p0 / g.Lc, m = (p0 % g.Lc) >> 4;
+    pkm[w] = col < g.N ? pk[(static_cast<size_t>((col >> 4) * g.Wc + m) * 16 + (col & 15)) * 8 + j] : 0u;
+  }
+}
+
+__device__ __forceinline__ v4i expand_w(uint32_t w) {
+  v4i b;
+  b[0] = static_cast<int>(w4_i8(w, 0));
+  b[1] = static_cast<int>(w4_i8(w, 1));
+  b[2] = static_cast<int>(w4_i8(w, 2));
+  b[3] = static_cast<int>(w4_i8(w, 3));
+  return b;
+}
+
+// s_waitcnt with only the vector-memory counter constrained (vmcnt <= N).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// DMA of one 64-position stage into a ring slot: this wave's A fragments (16 bytes per
+// lane) and B fragments (one word per lane). (A plain function: a lambda holding these
+// builtins keeps the kernel's host stub from being emitted.)
+template <int DA, int DB, int SA>
+__device__ __forceinline__ void issue_stage(const int8_t* const* asrc, const uint32_t* const* bsrc,
+                                            unsigned char* sb, int st, int wave) {
+#pragma unroll
+  for (int i = 0; i < DA; ++i)
+    __builtin_amdgcn_global_load_lds(asrc[i] + st * 64, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+    __builtin_amdgcn_global_load_lds(bsrc[i] + st * 128, (lds_void*)(sb + SA + (wave * DB + i) * 256), 4, 0, 0);
+}
+
+template <int MODE, int EPI, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
+  constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
+  constexpr int NW = WM * WN;                   // waves per block
+  constexpr int BM = 64 * WM;                   // rows per block
+  constexpr int BG = 2 * WN;                    // physical 32-column groups per block
+  constexpr int FR = BM / 32;                   // 32-row fragments
+  constexpr int SA = P * FR * 2 * 1024;         // A bytes per stage: [plane][frag][k-half]
+  constexpr int SS = SA + BG * 2 * 256;         // stage bytes (A, then B: [group][k-half])
+  constexpr int DA = P * FR * 2 / NW;           // A transfers per wave per stage
+  constexpr int DB = BG * 2 / NW;               // B transfers per wave per stage
+  static_assert(DA * NW == P * FR * 2 && DB * NW == BG * 2, "transfers must split evenly over the waves");
+  constexpr int D = DA + DB;
+  extern __shared__ __align__(16) unsigned char lds[];  // [S][SS]
+
+  const int z = blockIdx.z;
+  const ProjDev& W = a.p[z];
+  const int N = W.g.N, Lc = act.Lc;
+  const int ng32 = (N + 31) / 32;
+  // XCD-aware tile order: blocks are dealt to the 8 XCDs round-robin by block index, so
+  // block i runs on XCD i % 8; that XCD takes the i / 8-th tile of its own contiguous
+  // share of the row-major tile list. Concurrent blocks of one XCD then walk the column
+  // tiles of the same row tiles, and their activation rows stay in that XCD's L2.
+  const int nct = (ng32 + BG - 1) / BG, nrt = (act.rows + BM - 1) / BM;
+  const int ntile = nct * nrt, share = (ntile + 7) / 8;
+  const int tile = (blockIdx.x & 7) * share + (blockIdx.x >> 3);
+  if (tile >= ntile) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int row0 = (tile / nct) * BM;
+  const int cgb = (tile % nct) * BG;
+  const int am = (act.na > 1) ? z : 0;
+  const int nst = Lc / 8;  // 64-position stages
+  const size_t qstride = act.qstride(), plane = static_cast<size_t>(8 * Lc);
+  const int8_t* qbase = act.q + static_cast<size_t>(am) * act.rows * qstride;
+
+  // per-lane sources of this wave's transfers (advanced by 64 bytes / 128 words per stage)
+  const int8_t* asrc[DA];
+#pragma unroll
+  for (int i = 0; i < DA; ++i) {
+    const int f = wave * DA + i;  // = (plane * FR + frag) * 2 + k-half
+    const int kh = f & 1, pl = (f >> 1) / FR, rf = (f >> 1) % FR;
+    int row = row0 + rf * 32 + (lane & 31);
+    row = row < act.rows ? row : act.rows - 1;
+    asrc[i] = qbase + static_cast<size_t>(row) * qstride + pl * plane + kh * 32 + (lane >> 5) * 16;
+  }
+  const uint32_t* bsrc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) {
+    const int f = wave * DB + i;  // = group * 2 + k-half
+    int cg = cgb + (f >> 1);
+    cg = cg < ng32 ? cg : ng32 - 1;
+    bsrc[i] = W.pkm + (static_cast<size_t>(cg) * (Lc / 4) + (f & 1)) * 64 + lane;
+  }
+
+  v16i acc[P][2][2];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj) acc[pl][ai][bj] = v16i{};
+
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + st * SS, st, wave);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's transfers of stage st are complete once at most the later stages'
+    // transfers are outstanding
+    if (st + S - 2 < nst) wait_vm<(S - 2) * D>();
+    else wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // every wave has finished stage st - 1: its slot takes stage st + S - 1
+    if (st + S - 1 < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st + S - 1, wave);
+    const unsigned char* sb = lds + (st % S) * SS;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      v4i bop[2];
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj)
+        bop[bj] = expand_w(*reinterpret_cast<const uint32_t*>(sb + SA + ((wn * 2 + bj) * 2 + kh) * 256 + lane * 4));
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+        for (int ai = 0; ai < 2; ++ai) {
+          const v4i av =
+              *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * 2 + kh) * 1024 + lane * 16);
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj)
+            acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bop[bj], acc[pl][ai][bj], 0, 0, 0);
+        }
+    }
+    wait_lds();
+  }
+
+  // epilogue: exact integer totals, dequantisation, output stage. Per-column terms (the
+  // Q5.10 offset 128 * rowsum, tail weights) are loaded once per lane, per-row terms once
+  // per row, and the residual rows of a fragment in one batch before any store.
+  const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
+  const int ntail = W.g.ntail;
+  const int ol = lane & 31;
+  int col[2];
+  int32_t csum[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int cg = cgb + wn * 2 + (EPI == kEpiSwigluPair ? 0 : b);
+    col[b] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + (b ? Nout : 0) : cg * 32 + ol;
+    csum[b] = (MODE == kFixed && col[b] < N) ? 128 * W.rowsum[col[b]] : 0;
+  }
+  // stored columns of this lane: fragment b (non-pair) or the pair's gate column
+  constexpr int NB = (EPI == kEpiSwigluPair) ? 1 : 2;
+  bool cok[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) cok[b] = col[b] < Nout;
+#pragma unroll
+  for (int ai = 0; ai < 2; ++ai) {
+    const int rbase = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5);
+    float addv[16][NB];
+    float den[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int row = rbase + 8 * (i >> 2) + (i & 3);
+      row = row < act.rows ? row : act.rows - 1;
+      if (MODE == kInt8) den[i] = W.scale_w * act.sa[static_cast<size_t>(am) * act.rows + row];
+      if (EPI == kEpiAdd) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) addv[i][b] = cok[b] ? a.add[static_cast<size_t>(row) * N + col[b]] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = rbase + 8 * (i >> 2) + (i & 3);
+      if (row >= act.rows) continue;
+      const size_t grow = static_cast<size_t>(row);
+      const int32_t* ct = act.ct + (static_cast<size_t>(am) * act.rows + row) * 8;
+      int32_t tot[2];
+      float val[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        int32_t s = (MODE == kFixed) ? acc[0][ai][b][i] * 256 + acc[P - 1][ai][b][i] + csum[b] : acc[0][ai][b][i];
+        if (ntail && col[b] < N)
+          for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(W.tail[col[b] * 8 + t]) * ct[t];
+        tot[b] = s;
+        val[b] = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[z] : static_cast<float>(s) / den[i];
+      }
+      if (EPI == kEpiSwigluPair) {
+        if (!cok[0]) continue;
+        if (a.acc[z]) {
+          a.acc[z][grow * N + col[0]] = tot[0];
+          a.acc[z][grow * N + col[1]] = tot[1];
+        }
+        if (a.raw_acc) continue;
+        const size_t e = grow * Nout + col[0];
+        a.out[0][e] = swiglu_of(val[0], val[1], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+      } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          if (!cok[b]) continue;
+          const size_t e = grow * N + col[b];
+          if (a.acc[z]) a.acc[z][e] = tot[b];
+          if (a.raw_acc) continue;
+          a.out[z][e] = (EPI == kEpiAdd) ? addv[i][b] + val[b] : val[b];
+        }
+      }
+    }
+  }
+}
+
+// LDS bytes of a ring of S stages.
+template <int MODE, int WM, int WN>
+constexpr int ring_bytes(int S) {
+  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * 2 * 1024 + 2 * WN * 2 * 256);
+}
+
+// The device's LDS limit per block (160 KB on gfx950).
+int lds_limit() {
+  static int v = [] {
+    int dev = 0, lim = 65536;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      lim = 65536;
+    return lim;
+  }();
+  return v;
+}
+
+template <int WM, int WN>
+int tiles_of(const GemmArgs& a) {
+  const int ng32 = (a.p[0].g.N + 31) / 32;
+  return ((ng32 + 2 * WN - 1) / (2 * WN)) * ((a.rows + 64 * WM - 1) / (64 * WM));
+}
+
+// Ring depth 4 (3 stages in flight, up to 80 KB per block). Deeper rings measured slower
+// on the 1.3B shapes: 6 stages of 20 KB in flight on the 32 CUs of an XCD fill its 4 MB L2.
+// With a 64 KB LDS limit the ring falls back to 3 stages.
+template <int WM, int WN>
+constexpr int ring_stages() { return 4; }
+
+template <int MODE, int EPI, int WM, int WN>
+hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  constexpr int S = ring_stages<WM, WN>();
+  const int ntile = tiles_of<WM, WN>(a);
+  dim3 grid(8 * ((ntile + 7) / 8), 1, EPI == kEpiSwigluPair ? 1 : a.nmat);
+  const dim3 block(64 * WM * WN);
+  if (ring_bytes<MODE, WM, WN>(S) <= lds_limit())
+    k_mfma<MODE, EPI, WM, WN, S><<<grid, block, ring_bytes<MODE, WM, WN>(S), s>>>(a, act);
+  else
+    k_mfma<MODE, EPI, WM, WN, 3><<<grid, block, ring_bytes<MODE, WM, WN>(3), s>>>(a, act);
+  return hipGetLastError();
+}
+
+// Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
+// that still gives every CU a block (all blocks of all matrices), else 128.
+template <int MODE, int EPI>
+hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const int nz = (EPI == kEpiSwigluPair) ? 1 : a.nmat;
+  if (a.rows <= 64)
+    return tiles_of<1, 4>(a) * nz >= 256 ? mfma_inst<MODE, EPI, 1, 4>(a, act, s) : mfma_inst<MODE, EPI, 1, 2>(a, act, s);
+  return tiles_of<2, 4>(a) * nz >= 256 ? mfma_inst<MODE, EPI, 2, 4>(a, act, s) : mfma_inst<MODE, EPI, 2, 2>(a, act, s);
+}
+
+template <int MODE>
+hipError_t mfma_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  switch (a.epi) {
+    case kEpiSwigluPair: return mfma_epi<MODE, kEpiSwigluPair>(a, act, s);
+    case kEpiAdd: return mfma_epi<MODE, kEpiAdd>(a, act, s);
+    default: return mfma_epi<MODE, kEpiStore>(a, act, s);
+  }
+}
+
+}  // namespace
+
+size_t pkm_words(const Geom& g) { return static_cast<size_t>((g.N + 31) / 32) * 16 * g.Lc; }
+
+bool pkm_pairable(const Geom& g) { return g.N % 64 == 0; }
+
+hipError_t launch_pack_mfma(const uint32_t* pk, const Geom& g, bool pair, uint32_t* pkm, hipStream_t s) {
+  if (pair && !pkm_pairable(g)) return hipErrorInvalidValue;
+  const size_t total = pkm_words(g);
+  const int blocks = static_cast<int>(std::min<size_t>((total + 255) / 256, 65536));
+  k_pack_mfma<<<blocks, 256, 0, s>>>(pk, g, pair ? 1 : 0, pkm);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  return a.mode == kFixed ? mfma_mode<kFixed>(a, act, s) : mfma_mode<kInt8>(a, act, s);
+}
+
+}  // namespace mmf

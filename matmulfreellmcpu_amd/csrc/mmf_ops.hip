@@ -5,6 +5,8 @@
 //
 // Numerics follow the reference engine exactly (see mmf_device.hpp): every fp32
 // reduction keeps the 8-lane order of the AVX2 code, every int32 sum is exact.
+#include <cstdlib>
+
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
 
@@ -455,6 +457,65 @@ __global__ void k_mixer(const float* __restrict__ i, float* __restrict__ f, floa
   state[c] = s;
 }
 
+// Time-scan prefill split in two: the gate math of every element in parallel, then the
+// recurrence alone. k_gate: g = sigmoid(f) (then the lower bound), in = swiglu(i, 1 - g)
+// over the whole [rows, H] buffer, whose element count sets the tail rule
+// (hgrn_model.cpp:113-131). f is overwritten with g.
+__global__ void k_gate(const float* __restrict__ i, float* __restrict__ f, float* __restrict__ scan_in,
+                       const float* __restrict__ lb, int rows, int H) {
+  const size_t n = static_cast<size_t>(rows) * H;
+  const size_t body = n & ~static_cast<size_t>(7);
+  for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    float g = sigmoid_of(f[e], e >= body);
+    if (lb) {
+      const float l = lb[e % H];
+      g = __builtin_fmaf(1.0f - l, g, l);
+    }
+    scan_in[e] = swiglu_of(i[e], 1.0f - g, e >= body);
+    f[e] = g;
+  }
+}
+
+// The recurrence state = fma(g, state, in) (simd.hpp:335-357) down each column, in time
+// order. One thread per column; the g and in values of the next kScanU steps are loaded
+// while the current kScanU steps are computed.
+constexpr int kScanU = 64;
+
+__global__ __launch_bounds__(64) void k_scan_seq(const float* __restrict__ g, const float* __restrict__ in,
+                                                 float* __restrict__ recur, float* __restrict__ state, int rows,
+                                                 int H) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= H) return;
+  float s = state[c];
+  float gc[kScanU], ic[kScanU], gn[kScanU], inx[kScanU];
+  auto load = [&](int t0, float* gd, float* id) {
+#pragma unroll
+    for (int u = 0; u < kScanU; ++u) {
+      const int t = t0 + u < rows ? t0 + u : rows - 1;
+      gd[u] = g[static_cast<size_t>(t) * H + c];
+      id[u] = in[static_cast<size_t>(t) * H + c];
+    }
+  };
+  load(0, gc, ic);
+  for (int t0 = 0; t0 < rows; t0 += kScanU) {
+    if (t0 + kScanU < rows) load(t0 + kScanU, gn, inx);
+#pragma unroll
+    for (int u = 0; u < kScanU; ++u) {
+      if (t0 + u < rows) {
+        s = __builtin_fmaf(gc[u], s, ic[u]);
+        recur[static_cast<size_t>(t0 + u) * H + c] = s;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kScanU; ++u) {
+      gc[u] = gn[u];
+      ic[u] = inx[u];
+    }
+  }
+  state[c] = s;
+}
+
 __global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict__ ids,
                         float* __restrict__ h, int rows, int H) {
   const size_t n = static_cast<size_t>(rows) * H;
@@ -595,7 +656,21 @@ static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s)
   return pair ? gemm_inst<MODE, 8, true>(a, act, s) : gemm_inst<MODE, 8, false>(a, act, s);
 }
 
+int mfma_min_rows() {
+  static const int v = [] {
+    const char* e = std::getenv("MMF_MFMA_MIN_ROWS");
+    return e ? std::atoi(e) : 32;
+  }();
+  return v;
+}
+
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  if (a.mode != kFloat && mfma_min_rows() > 0 && a.rows >= mfma_min_rows()) {
+    bool ok = true;
+    for (int z = 0; z < (a.epi == kEpiSwigluPair ? 1 : a.nmat); ++z)
+      ok = ok && a.p[z].pkm && (a.p[z].pair != 0) == (a.epi == kEpiSwigluPair);
+    if (ok) return launch_gemm_mfma(a, act, s);
+  }
   switch (a.mode) {
     case kFloat: return gemm_mode<kFloat>(a, act, s);
     case kFixed: return gemm_mode<kFixed>(a, act, s);
@@ -605,6 +680,15 @@ hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
 
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
                         const float* lb, int rows, int H, bool stream_state, hipStream_t s) {
+  if (!stream_state && scan_out && rows > 1) {
+    const size_t n = static_cast<size_t>(rows) * H;
+    const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
+    k_gate<<<blocks, 256, 0, s>>>(i, f, scan_out, lb, rows, H);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_scan_seq<<<(H + 63) / 64, 64, 0, s>>>(f, scan_out, recur, state, rows, H);
+    return hipGetLastError();
+  }
   const int n = stream_state ? rows * H : H;
   k_mixer<<<(n + 255) / 256, 256, 0, s>>>(i, f, scan_out, recur, state, lb, rows, H, stream_state ? 1 : 0);
   return hipGetLastError();
