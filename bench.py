@@ -14,6 +14,19 @@ launch duration, measured with an event pair around each launch; peak = 8 TB/s H
 cpu_baseline: the reference engine compiled from its own sources (oracle/_ref/mmfree-cli,
 built by oracle/Makefile) timed on this host's cores with its own --bench harness on the
 same blob and prompt; its greedy id stream is also compared with the GPU's.
+
+Beside the headline (all on seeded synthetic weights of the named shapes):
+  op_sweep  BitLinear with int8-absmax activations: x ~N(0,1) [M, K], M in {1, 16, 256,
+            2048}, (K, N) in {(1024,1024), (1024,5632), (2816,1024), (2048,11264),
+            (5632,2048)}; microseconds per call (RMSNorm + quantisation + ternary GEMM),
+            algorithmic bytes N*K/4 + 4MK + 4MN + 4K against 8 TB/s, ops 2MNK against
+            the 5.0 POP/s int8 peak.
+  prefill   1.3B shape, 2048-token prompt, time to the first token (all layers + final
+            norm, lm_head, argmax) per mode; per-GEMM microseconds and TOP/s (event pair
+            around every launch); FixedQ510 runs two int8 passes (hi/lo code planes).
+  serve     batched decode of independent streams (2.7B x 64 streams x 128-token prompts,
+            float and FixedQ510; 1.3B x 32 x 512, FixedQ510): prompts prefilled per stream,
+            then lockstep decode steps timed on the host around each step.
 """
 from __future__ import annotations
 
@@ -77,6 +90,101 @@ def measure(eng, preset, steps, warmup):
     return step_us, kernels, tok_bytes
 
 
+INT8_PEAK_TOPS = 5000.0
+SWEEP_KN = [(1024, 1024), (1024, 5632), (2816, 1024), (2048, 11264), (5632, 2048)]
+SWEEP_M = [1, 16, 256, 2048]
+
+
+def measure_op_sweep(reps):
+    """BitLinear (int8 absmax) over the op-sweep shapes on device-resident inputs."""
+    import ctypes as C
+    from matmulfreellmcpu_amd import INT8_ABSMAX, Engine
+    e = Engine(0)
+    rng = np.random.default_rng(2024)
+    out = []
+
+    def dev(nbytes, arr=None):
+        p = C.c_void_p()
+        e._chk(e.lib.mmf_malloc(e.h, C.byref(p), nbytes))
+        if arr is not None:
+            e._chk(e.lib.mmf_upload(e.h, p, arr.ctypes.data_as(C.c_void_p), nbytes))
+        return p.value
+
+    for K, N in SWEEP_KN:
+        latent = rng.standard_normal((N, K)).astype(np.float32) * 0.02
+        scale = np.float32(1.0) / np.float32(np.abs(latent).mean())
+        wq = np.clip(np.rint(latent * scale), -1, 1).astype(np.int8)
+        pid = e.register_proj(wq, float(scale), np.ones(K, np.float32))
+        for M in SWEEP_M:
+            x = rng.standard_normal((M, K)).astype(np.float32)
+            dx, do = dev(x.nbytes, x), dev(M * N * 4)
+            total, _, gemm = e.time_bitlinear(pid, dx, do, M, mode=INT8_ABSMAX, warmup=3, reps=reps)
+            nbytes = N * K / 4 + 4 * M * K + 4 * M * N + 4 * K
+            ops = 2.0 * M * N * K
+            bound = "mfma" if ops / nbytes > INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+            out.append({"M": M, "K": K, "N": N, "us": round(total, 2), "GBps": round(nbytes / total / 1e3, 1),
+                        "hbm_frac": round(nbytes / total / 1e3 / HBM_PEAK_GBS, 4),
+                        "TOPS": round(ops / total / 1e6, 2), "mfma_frac": round(ops / total / 1e6 / INT8_PEAK_TOPS, 4),
+                        "bound": bound})
+            e.lib.mmf_free(e.h, dx)
+            e.lib.mmf_free(e.h, do)
+    e.close()
+    return out
+
+
+def measure_prefill(blob_dir, T=2048, modes=("fixed", "int8", "float")):
+    from matmulfreellmcpu_amd import MODES, Engine
+    V, H, L, I = DIMS["s2"]
+    p = blob_path(blob_dir, "s2")
+    ids = np.random.default_rng(77).integers(3, 32000, T)
+    res = {}
+    for name in modes:
+        mode = MODES[name]
+        e = Engine(0)
+        e.load_blob(p, mode)
+        total, kinds = e.time_prefill(ids, warmup=1, reps=3)
+        e.close()
+        r = {"ms": round(total / 1e3, 3), "tok_s": round(T / total * 1e6, 1),
+             "kinds_ms": {k: round(v / 1e3, 3) for k, v in kinds.items()}}
+        if name != "float":
+            planes = 2 if name == "fixed" else 1
+            ops = {"gemm_ifg": 2.0 * T * 3 * H * H * L, "gemm_o": 2.0 * T * H * H * L,
+                   "gemm_gate": 2.0 * T * 2 * I * H * L, "gemm_down": 2.0 * T * H * I * L}
+            r["gemm_TOPS"] = {k: round(ops[k] / kinds[k] / 1e6, 1) for k in ops}
+            r["mfma_TOPS"] = {k: round(planes * ops[k] / kinds[k] / 1e6, 1) for k in ops}
+            allops = sum(ops.values())
+            alltime = sum(kinds[k] for k in ops)
+            r["mfma_frac_all_gemms"] = round(planes * allops / alltime / 1e6 / INT8_PEAK_TOPS, 4)
+        res[name] = r
+        log(f"[bench] prefill 1.3B T={T} {name}: {r['ms']} ms ({r['tok_s']} tok/s)")
+    return res
+
+
+def measure_serve(blob_dir, preset, B, T, mode_name, steps):
+    from matmulfreellmcpu_amd import MODES, Engine
+    p = blob_path(blob_dir, preset)
+    e = Engine(0)
+    e.load_blob(p, MODES[mode_name])
+    rng = np.random.default_rng(B * 1000 + T)
+    prompts = rng.integers(3, 32000, (B, T))
+    e.reset(B)
+    t0 = time.perf_counter()
+    cur = np.array([e.prefill(b, prompts[b]) for b in range(B)], np.int64)
+    t_pre = time.perf_counter() - t0
+    for _ in range(2):
+        cur = e.step(cur)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cur = e.step(cur)
+    dt = time.perf_counter() - t0
+    e.close()
+    r = {"streams": B, "prompt_tokens": T, "mode": mode_name, "steps_timed": steps,
+         "ms_per_step": round(dt / steps * 1e3, 3), "decode_tok_s": round(B * steps / dt, 1),
+         "prefill_s": round(t_pre, 3)}
+    log(f"[bench] serve {preset} B={B} T={T} {mode_name}: {r['ms_per_step']} ms/step, {r['decode_tok_s']} tok/s")
+    return r
+
+
 def cpu_reference(blob, ids, gen, threads):
     cli = os.path.join(ROOT, "oracle", "_ref", "mmfree-cli")
     if not os.path.exists(cli):
@@ -105,6 +213,8 @@ def main():
     ap.add_argument("--shapes", default="370M,1.3B,2.7B")
     ap.add_argument("--blob-dir", default=os.environ.get("MMF_BLOB_DIR", "/tmp/mmf_bench_blobs"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
+    ap.add_argument("--sections", default="decode,op_sweep,prefill,serve",
+                    help="comma list of decode,op_sweep,prefill,serve (decode is always run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HGRN-Bit hot path here runs on a single MI355X and this "
@@ -143,6 +253,16 @@ def main():
         log(f"[bench] {name}: {1e6 / step_us:.1f} tok/s ({step_us:.1f} us/token), "
             + ", ".join(f"{k} {v['us_per_launch']:.2f}us {v['GBps']:.0f}GB/s" for k, v in kernels.items()))
     eng.close()
+    sections = {x.strip() for x in args.sections.split(",")}
+    extra = {}
+    if "op_sweep" in sections:
+        extra["op_sweep"] = measure_op_sweep(reps=20)
+    if "prefill" in sections:
+        extra["prefill"] = measure_prefill(args.blob_dir)
+    if "serve" in sections:
+        extra["serve"] = [measure_serve(args.blob_dir, "s3", 64, 128, "float", 32),
+                          measure_serve(args.blob_dir, "s3", 64, 128, "fixed", 32),
+                          measure_serve(args.blob_dir, "s2", 32, 512, "fixed", 32)]
 
     head = results["370M"]
     value = 1e6 / head["step_us"]
@@ -186,6 +306,7 @@ def main():
         "parity": parity,
         "device": f"{devname}, {cus} CUs",
     }
+    out.update(extra)
     print(json.dumps(out), flush=True)
 
 
