@@ -269,8 +269,16 @@ def main():
     kern = head["kernels"]
     dom = max(KINDS, key=lambda k: kern[k]["us_per_launch"] * kern[k]["launches_per_token"])
     achieved = kern[dom]["GBps"]
+    # HBM bytes per launch of that kernel from the committed PMC summary (FETCH_SIZE and
+    # WRITE_SIZE runs, calibrated on a copy kernel of known size), when it covers the kernel
+    traffic = None
+    try:
+        with open(os.path.join(ROOT, "profiles", "pmc_traffic.json")) as f:
+            traffic = json.load(f)["kernels"][dom]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        pass
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": f"k_decode<float,{dom}> (370M)", "bytes_per_launch": kern[dom]["bytes_per_launch"],
                 "us_per_launch": kern[dom]["us_per_launch"]}
 

@@ -157,7 +157,10 @@ int mmf_model_trace(mmf_ctx* ctx, const int64_t* ids, size_t T, float* h, float*
 
 /* Timing of the single-row decode kernels on the context's stream (HIP events around
  * `reps` decode steps, after `warmup` untimed ones): average microseconds per step and
- * per launch of the kernel kinds {IFG, O, GATE, DOWN, LM} (kind_us[5], may be NULL). */
+ * per launch of the kernel kinds {IFG, O, GATE, DOWN, LM} (kind_us[5], may be NULL; each
+ * kind's launches for all layers are replayed back to back from a captured HIP graph, so
+ * the figure is the kernels' execution time). No counterpart in the reference engine:
+ * measurement only. */
 int mmf_model_time_decode(mmf_ctx* ctx, int warmup, int reps, double* step_us, double* kind_us);
 
 /* Timing of the prefill (prompt of T ids through all layers, then the final norm, lm_head

@@ -558,28 +558,41 @@ void decode_launches(mmf_ctx* c, Model& m) {
   decode_one(c, m, kLM, 0, true);
 }
 
-void decode_step(mmf_ctx* c, Model& m) {
-  static const bool use_graph = [] {
+// HIP graphs for the launch-bound loops (MMF_GRAPH=0 turns them off, e.g. under a profiler
+// that cannot follow graph launches).
+bool graphs_enabled() {
+  static const bool on = [] {
     const char* e = std::getenv("MMF_GRAPH");
     return !(e && std::strcmp(e, "0") == 0);
   }();
-  if (use_graph && !m.graph_tried) {
-    m.graph_tried = true;
-    hipGraph_t gr = nullptr;
-    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-      bool ok = true;
-      try {
-        decode_launches(c, m);
-      } catch (const Err&) {
-        ok = false;
-      }
-      if (hipStreamEndCapture(c->stream, &gr) != hipSuccess) ok = false;
-      if (ok && gr && hipGraphInstantiate(&m.graph, gr, nullptr, nullptr, 0) != hipSuccess) {
-        m.graph = nullptr;
-      }
-      if (gr) (void)hipGraphDestroy(gr);
+  return on;
+}
+
+// Capture the launches that f() enqueues on the context's stream into an executable graph;
+// nullptr if capture or instantiation fails (the caller then launches directly).
+template <class F>
+hipGraphExec_t capture_graph(mmf_ctx* c, F&& f) {
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t gr = nullptr;
+  if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+    bool ok = true;
+    try {
+      f();
+    } catch (const Err&) {
+      ok = false;
     }
-    (void)hipGetLastError();
+    if (hipStreamEndCapture(c->stream, &gr) != hipSuccess) ok = false;
+    if (ok && gr && hipGraphInstantiate(&exec, gr, nullptr, nullptr, 0) != hipSuccess) exec = nullptr;
+    if (gr) (void)hipGraphDestroy(gr);
+  }
+  (void)hipGetLastError();
+  return exec;
+}
+
+void decode_step(mmf_ctx* c, Model& m) {
+  if (graphs_enabled() && !m.graph_tried) {
+    m.graph_tried = true;
+    m.graph = capture_graph(c, [&] { decode_launches(c, m); });
   }
   if (m.graph) {
     MMF_HIP(hipGraphLaunch(m.graph, c->stream));
@@ -1242,13 +1255,34 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
     MMF_HIP(hipEventElapsedTime(&ms, e0, e1));
     if (step_us) *step_us = 1000.0 * ms / reps;
     if (kind_us) {
-      // An event pair around every launch: the elapsed time of each pair is that kernel's
-      // execution on the stream, independent of host submission gaps.
+      // Per kind: the kernels of that kind for all layers, back to back, `reps` times. With
+      // graphs the launches are captured and replayed, so the average per launch is the
+      // kernel's execution time (graph nodes run without host submission gaps); without
+      // graphs an event pair around every launch measures each kernel on the stream.
       const size_t L = m.layers.size();
-      std::vector<hipEvent_t> ev(2 * L);
-      for (auto& e : ev) MMF_HIP(hipEventCreate(&e));
       for (int k = 0; k < 5; ++k) {
         const size_t nl = (k == 4) ? 1 : L;
+        const int per = std::max(1, std::min(reps, static_cast<int>(512 / nl)));
+        auto launches = [&] {
+          for (int r = 0; r < per; ++r)
+            for (size_t l = 0; l < nl; ++l) decode_one(c, m, static_cast<DecKind>(k), l);
+        };
+        hipGraphExec_t gx = graphs_enabled() ? capture_graph(c, launches) : nullptr;
+        if (gx) {
+          const int rounds = std::max(1, reps / per);
+          hipError_t err = hipGraphLaunch(gx, c->stream);  // warm-up replay
+          if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+          for (int r = 0; r < rounds && err == hipSuccess; ++r) err = hipGraphLaunch(gx, c->stream);
+          if (err == hipSuccess) err = hipEventRecord(e1, c->stream);
+          if (err == hipSuccess) err = hipEventSynchronize(e1);
+          if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+          (void)hipGraphExecDestroy(gx);
+          MMF_HIP(err);
+          kind_us[k] = 1000.0 * ms / (static_cast<double>(rounds) * per * nl);
+          continue;
+        }
+        std::vector<hipEvent_t> ev(2 * nl);
+        for (auto& e : ev) MMF_HIP(hipEventCreate(&e));
         double total = 0.0;
         for (int r = 0; r < reps + 1; ++r) {
           for (size_t l = 0; l < nl; ++l) {
@@ -1263,9 +1297,9 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
             total += ms;
           }
         }
+        for (auto& e : ev) (void)hipEventDestroy(e);
         kind_us[k] = 1000.0 * total / (static_cast<double>(reps) * nl);
       }
-      for (auto& e : ev) (void)hipEventDestroy(e);
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
