@@ -5,7 +5,8 @@
 //   kO    : g_norm (RMSNorm(g) * silu(recur)) -> BitLinear norm -> o GEMV -> resid = h + o
 //   kGate : mlp_norm -> BitLinear norm -> gate/up GEMV (rows c and I + c) -> swiglu
 //   kDown : BitLinear norm -> down GEMV -> h = resid + d
-//   kLM   : final norm -> BitLinear norm -> lm_head GEMV -> logits, argmax key (atomicMax)
+//   kLM   : final norm -> BitLinear norm -> lm_head GEMV -> logits, one argmax key per block
+//           (reduced by the next step's layer-0 kIFG or by the host)
 //
 // Latency is what bounds a batch-1 decode step, so each kernel is organised around it:
 //  * all vectors passed between these kernels, and all norm weights, are stored in the

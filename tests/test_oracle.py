@@ -172,6 +172,23 @@ def test_int8_absmax_closed_form(oracle):
     assert_bitexact(r["out"], want.astype(np.float32), "int8 out")
 
 
+def test_int8_absmax_known_answers(oracle):
+    """Hand-computed vectors for tools/reference.py:131-135,180-184: x = ones and eps = 0 give
+    rstd = 1 exactly, so y = normw; max|y| = 127/64 gives scale_a = 64 exactly. y*scale_a hits
+    +-2.5 (round half to even -> +-2, half away from zero would give +-3), 3.5 (-> 4) and
+    +-127; one-hot weight rows make acc = the codes, and acc / (scale_w * scale_a) with
+    scale_w = 2 gives exact eighths of a sixteenth."""
+    y = np.array([127 / 64, -127 / 64, 2.5 / 64, -2.5 / 64, 3.5 / 64, 0.0, 1 / 128, 40 / 64],
+                 np.float32)
+    x = np.ones((1, 8), np.float32)
+    wq = np.eye(8, dtype=np.int8)
+    r = oracle.bitlinear(x, y, wq, 2.0, 0.0, INT8)
+    assert r["scale_a"][0] == np.float32(64.0)
+    np.testing.assert_array_equal(r["codes"][0], [127, -127, 2, -2, 4, 0, 0, 40])
+    np.testing.assert_array_equal(r["acc"][0], [127, -127, 2, -2, 4, 0, 0, 40])
+    np.testing.assert_array_equal(r["out"][0], np.array([127, -127, 2, -2, 4, 0, 0, 40], np.float32) / 128)
+
+
 def test_fixed_codes_and_acc_closed_form(oracle):
     rng = np.random.default_rng(3)
     x = rng.standard_normal((2, 64)).astype(np.float32)
