@@ -45,57 +45,6 @@ namespace mmf {
 
 namespace {
 
-// Sequential reference lane sums (simd.hpp:69-89) over a zero-padded chain-transposed LDS
-// vector whose rows are LS floats apart and zero up to a multiple of 32, in two halves so
-// other waves can work while wave 0 runs the chains: chain_begin -- thread j < 8 sums row j
-// with FMAs in order, 32 values per batch, the next batch loading while the current one is
-// summed (the zeros add exact zeros); chain_end (after a barrier) -- hsum + the tail.
-__device__ void chain_begin(const float* X, int Lc, int LS, float* red) {
-  if (threadIdx.x < 8) {
-    const float4* c = reinterpret_cast<const float4*>(X + threadIdx.x * LS);
-    const int nbat = (Lc + 31) / 32;
-    float a = 0.0f;
-    float4 A[8], B[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) A[u] = c[u];
-    for (int b = 0; b < nbat; b += 2) {
-      const bool more = b + 1 < nbat;
-      if (more)
-#pragma unroll
-        for (int u = 0; u < 8; ++u) B[u] = c[8 * (b + 1) + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        a = __builtin_fmaf(A[u].x, A[u].x, a);
-        a = __builtin_fmaf(A[u].y, A[u].y, a);
-        a = __builtin_fmaf(A[u].z, A[u].z, a);
-        a = __builtin_fmaf(A[u].w, A[u].w, a);
-      }
-      if (more) {
-        if (b + 2 < nbat)
-#pragma unroll
-          for (int u = 0; u < 8; ++u) A[u] = c[8 * (b + 2) + u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          a = __builtin_fmaf(B[u].x, B[u].x, a);
-          a = __builtin_fmaf(B[u].y, B[u].y, a);
-          a = __builtin_fmaf(B[u].z, B[u].z, a);
-          a = __builtin_fmaf(B[u].w, B[u].w, a);
-        }
-      }
-    }
-    red[threadIdx.x] = a;
-  }
-}
-
-__device__ float chain_end(const float* X, int LS, int nt, const float* red) {
-  float s = hsum8(red);
-  for (int t = 0; t < nt; ++t) {
-    const float v = X[8 * LS + t];
-    s = __builtin_fmaf(v, v, s);
-  }
-  return s;
-}
-
 template <int KIND> struct KindTraits;
 // NM matrices (one wave pair each), NA activation vectors, NP prologue source vectors
 template <> struct KindTraits<kIFG> { static constexpr int NM = 3, NA = 3, NP = 5; };

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -38,7 +39,10 @@ struct Err {
 
 [[noreturn]] void fail(int code, const std::string& m) { throw Err{code, m}; }
 
-// Grow-only device buffer.
+// Grow-only device buffer. Every reallocation bumps dbuf_epoch, so a captured graph that
+// baked in buffer addresses can tell that it is stale.
+std::atomic<uint64_t> dbuf_epoch{0};
+
 struct DBuf {
   void* p = nullptr;
   size_t n = 0;
@@ -49,6 +53,7 @@ struct DBuf {
       n = 0;
       MMF_HIP(hipMalloc(&p, bytes));
       n = bytes;
+      ++dbuf_epoch;
     }
     return p;
   }
@@ -112,6 +117,10 @@ struct Model {
   // decode graph
   hipGraphExec_t graph = nullptr;
   bool graph_tried = false;
+  // batched serving step graph, valid for step_B streams while no buffer moved
+  hipGraphExec_t step_graph = nullptr;
+  size_t step_B = 0;
+  uint64_t step_epoch = 0;
 };
 
 // Optional per-launch timing of the row path: an event pair around each launch, summed
@@ -148,6 +157,7 @@ struct mmf_ctx {
   Model model;
   DBuf raw;  // staging for int8 weights before the repack
   DBuf opy, opq, opct, opsa, opstate;
+  DBuf gws;  // split-K workspace of the matrix-core GEMM
   hipDeviceProp_t prop{};
   RowTimer timer;
 };
@@ -255,6 +265,13 @@ ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, 
   return a;
 }
 
+// launch_gemm with the split-K workspace it asks for (grow-only, owned by the context).
+void run_gemm(mmf_ctx* c, GemmArgs& ga, const ActBuf& act, hipStream_t st) {
+  const size_t wsb = gemm_workspace_bytes(ga);
+  ga.ws = wsb ? static_cast<int32_t*>(c->gws.get(wsb)) : nullptr;
+  MMF_HIP(launch_gemm(ga, act, st));
+}
+
 GemmArgs gemm_args(mmf_ctx* c, const int* ids, int n, int rows, Mode mode, int frac) {
   GemmArgs a{};
   a.nmat = n;
@@ -347,7 +364,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.out[1] = fb;
     ga.out[2] = gb;
     tbeg(c, kRkGemmIFG);
-    MMF_HIP(launch_gemm(ga, act, st));
+    run_gemm(c, ga, act, st);
     tend(c);
   }
   // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
@@ -383,7 +400,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.add = h;
     ga.out[0] = resid;
     tbeg(c, kRkGemmO);
-    MMF_HIP(launch_gemm(ga, act, st));
+    run_gemm(c, ga, act, st);
     tend(c);
   }
   // mlp_norm -> gate_proj -> swiglu (hgrn_model.cpp:167-185)
@@ -406,7 +423,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.out[0] = zb;
     ga.swiglu_n = rows * I;
     tbeg(c, kRkGemmGate);
-    MMF_HIP(launch_gemm(ga, act, st));
+    run_gemm(c, ga, act, st);
     tend(c);
   }
   // down_proj -> h = resid + d (hgrn_model.cpp:187-194)
@@ -428,7 +445,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.add = resid;
     ga.out[0] = h;
     tbeg(c, kRkGemmDown);
-    MMF_HIP(launch_gemm(ga, act, st));
+    run_gemm(c, ga, act, st);
     tend(c);
   }
 }
@@ -450,7 +467,7 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   MMF_HIP(launch_prologue(mode, pa, act, c->stream));
   GemmArgs ga = gemm_args(c, &m.lm, 1, rows, mode, m.frac);
   ga.out[0] = logits;
-  MMF_HIP(launch_gemm(ga, act, c->stream));
+  run_gemm(c, ga, act, c->stream);
 }
 
 int lm_grid(const Model& m) {
@@ -605,6 +622,9 @@ void drop_graph(Model& m) {
   if (m.graph) (void)hipGraphExecDestroy(m.graph);
   m.graph = nullptr;
   m.graph_tried = false;
+  if (m.step_graph) (void)hipGraphExecDestroy(m.step_graph);
+  m.step_graph = nullptr;
+  m.step_B = 0;
 }
 
 void reset_state(mmf_ctx* c, Model& m, size_t B) {
@@ -791,7 +811,7 @@ int mmf_ternary_matmul(mmf_ctx* c, int id, const int32_t* x, int32_t* acc, size_
     GemmArgs ga = gemm_args(c, &id, 1, static_cast<int>(b), kFixed, 10);
     ga.raw_acc = true;
     ga.acc[0] = acc;
-    MMF_HIP(launch_gemm(ga, act, c->stream));
+    run_gemm(c, ga, act, c->stream);
   });
 }
 
@@ -822,7 +842,7 @@ static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac
   for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
   ga.acc[0] = acc;
   tbeg(c, kRkGemmIFG);
-  MMF_HIP(launch_gemm(ga, act, c->stream));
+  run_gemm(c, ga, act, c->stream);
   tend(c);
 }
 
@@ -1180,13 +1200,39 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
     int64_t* d = s.ids.as<int64_t>(B);
     MMF_HIP(hipMemcpyAsync(d, tokens, B * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
     float* h = s.h.as<float>(B * H);
-    MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
-    for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
-      layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H, true,
-                 nullptr);
     float* lg = s.logits.as<float>(B * V);
-    lm_rows(c, m, static_cast<int>(B), h, lg);
-    deliver_rows(c, m, lg, B, logits, argmax);
+    int64_t* am = s.am.as<int64_t>(B);
+    // embedding, all layers, final norm + lm_head, argmax: captured once per stream count
+    // and replayed while no scratch buffer has moved (the first step runs them directly)
+    auto work = [&] {
+      MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
+      for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
+        layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H,
+                   true, nullptr);
+      lm_rows(c, m, static_cast<int>(B), h, lg);
+      MMF_HIP(launch_argmax_rows(lg, static_cast<int>(B), static_cast<int>(V), am, c->stream));
+    };
+    if (m.step_graph && m.step_B == B && m.step_epoch == dbuf_epoch.load()) {
+      MMF_HIP(hipGraphLaunch(m.step_graph, c->stream));
+    } else {
+      work();
+      if (m.step_graph) (void)hipGraphExecDestroy(m.step_graph);
+      m.step_graph = nullptr;
+      if (graphs_enabled()) {
+        const uint64_t ep = dbuf_epoch.load();
+        hipGraphExec_t g = capture_graph(c, work);
+        if (g && dbuf_epoch.load() == ep) {
+          m.step_graph = g;
+          m.step_B = B;
+          m.step_epoch = ep;
+        } else if (g) {
+          (void)hipGraphExecDestroy(g);
+        }
+      }
+    }
+    if (logits) MMF_HIP(hipMemcpyAsync(logits, lg, B * V * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    if (argmax) MMF_HIP(hipMemcpyAsync(argmax, am, B * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
   });
 }
 

@@ -144,11 +144,18 @@ struct GemmArgs {
   float* out[3];       // [rows, N] per matrix (kEpiSwigluPair: out[0] = z [rows, N/2])
   int32_t* acc[3];     // optional int32 accumulators [rows, N]
   int swiglu_n;        // kEpiSwigluPair: rows * (N/2), for the tail rule
+  // matrix-core split-K (set by launch_gemm): ksplit partial tiles [ksplit][nmat][rows][N]
+  // of exact int32 sums in ws, reduced in split order by a second kernel
+  int ksplit;
+  int32_t* ws;
 };
 // Dispatches the integer modes to the matrix-core kernel (mmf_mfma.hip) from
 // mfma_min_rows() rows on, everything else to the dot-product kernel.
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+// Bytes of int32 workspace launch_gemm needs for `a` (0 when it will not split K); the
+// caller passes at least that much in a.ws.
+size_t gemm_workspace_bytes(const GemmArgs& a);
 // Rows from which the integer modes use the matrix cores (MMF_MFMA_MIN_ROWS, default 32;
 // 0 disables them).
 int mfma_min_rows();

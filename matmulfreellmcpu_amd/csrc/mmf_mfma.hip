@@ -29,6 +29,11 @@
 // matrix cores' own lane order, so every fragment read is one linear 1 KB (A) or 256 B (B)
 // LDS access. A ring of S stages keeps S - 1 stages in flight; each wave waits for its own
 // transfers (s_waitcnt vmcnt) and one barrier per stage publishes them to the block.
+//
+// Split-K: when a GEMM has too few tiles to occupy the chip (a few dozen rows, or narrow
+// matrices), blockIdx.y selects a contiguous range of stages; each block stores its exact
+// int32 partial tile, and k_splitk_epi adds the partials in split order and applies the
+// epilogue (integer sums: the order does not change the result).
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
 
@@ -122,7 +127,10 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int row0 = (tile / nct) * BM;
   const int cgb = (tile % nct) * BG;
   const int am = (act.na > 1) ? z : 0;
-  const int nst = Lc / 8;  // 64-position stages
+  // stage range of this block's split (all stages without split-K)
+  const int nall = Lc / 8, ksp = gridDim.y, ks = blockIdx.y;
+  const int st0 = static_cast<int>((static_cast<long>(nall) * ks) / ksp);
+  const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
   const size_t qstride = act.qstride(), plane = static_cast<size_t>(8 * Lc);
   const int8_t* qbase = act.q + static_cast<size_t>(am) * act.rows * qstride;
 
@@ -155,7 +163,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
-    if (st < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + st * SS, st, wave);
+    if (st < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + st * SS, st0 + st, wave);
   for (int st = 0; st < nst; ++st) {
     // this wave's transfers of stage st are complete once at most the later stages'
     // transfers are outstanding
@@ -164,7 +172,8 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // every wave has finished stage st - 1: its slot takes stage st + S - 1
-    if (st + S - 1 < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st + S - 1, wave);
+    if (st + S - 1 < nst)
+      issue_stage<DA, DB, SA>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st0 + st + S - 1, wave);
     const unsigned char* sb = lds + (st % S) * SS;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -184,6 +193,28 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
         }
     }
     wait_lds();
+  }
+
+  if (ksp > 1) {
+    // split-K: exact partial sums of this stage range, logical column order
+    int32_t* wp = a.ws + (static_cast<size_t>(ks) * a.nmat + z) * act.rows * static_cast<size_t>(N);
+    const int Nh = N / 2;
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const int cg = cgb + wn * 2 + bj;
+      const int o = (EPI == kEpiSwigluPair) ? ((cg & 1) ? Nh : 0) + (cg >> 1) * 32 + (lane & 31) : cg * 32 + (lane & 31);
+      if (cg >= ng32 || o >= N) continue;
+#pragma unroll
+      for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = row0 + wm * 64 + ai * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+          if (row >= act.rows) continue;
+          wp[static_cast<size_t>(row) * N + o] =
+              (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] : acc[0][ai][bj][i];
+        }
+    }
+    return;
   }
 
   // epilogue: exact integer totals, dequantisation, output stage. Per-column terms (the
@@ -259,6 +290,54 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   }
 }
 
+// Split-K epilogue: one thread per output element (per pair for swiglu), the partials of
+// every split added in split order, then the same bias / tail / dequantisation / output
+// stage as the single-pass epilogue.
+template <int MODE, int EPI>
+__global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
+  const int z = blockIdx.z;
+  const ProjDev& W = a.p[z];
+  const int N = W.g.N;
+  const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
+  const size_t n = static_cast<size_t>(act.rows) * Nout;
+  const size_t plane = static_cast<size_t>(act.rows) * N;  // one split of one matrix
+  const int am = (act.na > 1) ? z : 0;
+  constexpr int NM = (EPI == kEpiSwigluPair) ? 2 : 1;
+  for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int row = static_cast<int>(e / Nout), o0 = static_cast<int>(e % Nout);
+    const size_t ar = static_cast<size_t>(am) * act.rows + row;
+    float val[NM];
+    int32_t tot[NM];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int o = o0 + (mi ? Nout : 0);
+      int32_t s = 0;
+      for (int ks = 0; ks < a.ksplit; ++ks)
+        s += a.ws[(static_cast<size_t>(ks) * a.nmat + z) * plane + static_cast<size_t>(row) * N + o];
+      if (MODE == kFixed) s += 128 * W.rowsum[o];
+      const int32_t* ct = act.ct + ar * 8;
+      for (int t = 0; t < W.g.ntail; ++t) s += static_cast<int32_t>(W.tail[o * 8 + t]) * ct[t];
+      tot[mi] = s;
+      val[mi] = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[z]
+                                 : static_cast<float>(s) / (W.scale_w * act.sa[ar]);
+    }
+    const size_t grow = static_cast<size_t>(row);
+    if (a.acc[z]) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) a.acc[z][grow * N + o0 + (mi ? Nout : 0)] = tot[mi];
+    }
+    if (a.raw_acc) continue;
+    if (EPI == kEpiSwigluPair) {
+      a.out[0][e] = swiglu_of(val[0], val[NM - 1], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+    } else if (EPI == kEpiAdd) {
+      a.out[z][e] = a.add[e] + val[0];
+    } else {
+      a.out[z][e] = val[0];
+    }
+  }
+}
+
 // LDS bytes of a ring of S stages.
 template <int MODE, int WM, int WN>
 constexpr int ring_bytes(int S) {
@@ -289,27 +368,54 @@ int tiles_of(const GemmArgs& a) {
 template <int WM, int WN>
 constexpr int ring_stages() { return 4; }
 
+// Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
+// that still gives every CU a block (all blocks of all matrices), else 128. Then K is
+// split in powers of two until there is a block per CU (each split >= 4 stages).
+struct Plan {
+  int wm, wn, ksplit;
+};
+
+Plan plan_of(const GemmArgs& a) {
+  const int nz = (a.epi == kEpiSwigluPair) ? 1 : a.nmat;
+  Plan p{a.rows <= 64 ? 1 : 2, 4, 1};
+  if (p.wm == 1 ? tiles_of<1, 4>(a) * nz < 256 : tiles_of<2, 4>(a) * nz < 256) p.wn = 2;
+  const int tiles = (p.wm == 1 ? (p.wn == 4 ? tiles_of<1, 4>(a) : tiles_of<1, 2>(a))
+                               : (p.wn == 4 ? tiles_of<2, 4>(a) : tiles_of<2, 2>(a))) * nz;
+  // split K until there is a block per CU, keeping >= 4 stages per split
+  const int nst = a.p[0].g.Lc / 8;
+  while (tiles * p.ksplit < 256 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
+  return p;
+}
+
 template <int MODE, int EPI, int WM, int WN>
-hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream_t s) {
   constexpr int S = ring_stages<WM, WN>();
   const int ntile = tiles_of<WM, WN>(a);
-  dim3 grid(8 * ((ntile + 7) / 8), 1, EPI == kEpiSwigluPair ? 1 : a.nmat);
+  const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
+  dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
   const dim3 block(64 * WM * WN);
   if (ring_bytes<MODE, WM, WN>(S) <= lds_limit())
     k_mfma<MODE, EPI, WM, WN, S><<<grid, block, ring_bytes<MODE, WM, WN>(S), s>>>(a, act);
   else
     k_mfma<MODE, EPI, WM, WN, 3><<<grid, block, ring_bytes<MODE, WM, WN>(3), s>>>(a, act);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || ksplit == 1) return e;
+  GemmArgs b = a;
+  b.ksplit = ksplit;
+  const int Nout = EPI == kEpiSwigluPair ? a.p[0].g.N / 2 : a.p[0].g.N;
+  const size_t n = static_cast<size_t>(a.rows) * Nout;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 4096));
+  k_splitk_epi<MODE, EPI><<<dim3(blocks, 1, nz), 256, 0, s>>>(b, act);
   return hipGetLastError();
 }
 
-// Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
-// that still gives every CU a block (all blocks of all matrices), else 128.
 template <int MODE, int EPI>
 hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
-  const int nz = (EPI == kEpiSwigluPair) ? 1 : a.nmat;
-  if (a.rows <= 64)
-    return tiles_of<1, 4>(a) * nz >= 256 ? mfma_inst<MODE, EPI, 1, 4>(a, act, s) : mfma_inst<MODE, EPI, 1, 2>(a, act, s);
-  return tiles_of<2, 4>(a) * nz >= 256 ? mfma_inst<MODE, EPI, 2, 4>(a, act, s) : mfma_inst<MODE, EPI, 2, 2>(a, act, s);
+  const Plan p = plan_of(a);
+  const int ks = a.ws ? p.ksplit : 1;
+  if (p.wm == 1)
+    return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2>(a, act, ks, s);
+  return p.wn == 4 ? mfma_inst<MODE, EPI, 2, 4>(a, act, ks, s) : mfma_inst<MODE, EPI, 2, 2>(a, act, ks, s);
 }
 
 template <int MODE>
@@ -333,6 +439,13 @@ hipError_t launch_pack_mfma(const uint32_t* pk, const Geom& g, bool pair, uint32
   const int blocks = static_cast<int>(std::min<size_t>((total + 255) / 256, 65536));
   k_pack_mfma<<<blocks, 256, 0, s>>>(pk, g, pair ? 1 : 0, pkm);
   return hipGetLastError();
+}
+
+size_t gemm_workspace_bytes(const GemmArgs& a) {
+  if (a.mode == kFloat || mfma_min_rows() <= 0 || a.rows < mfma_min_rows()) return 0;
+  const Plan p = plan_of(a);
+  if (p.ksplit == 1) return 0;
+  return static_cast<size_t>(p.ksplit) * a.nmat * a.rows * static_cast<size_t>(a.p[0].g.N) * sizeof(int32_t);
 }
 
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s) {

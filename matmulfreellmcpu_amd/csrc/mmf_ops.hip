@@ -14,33 +14,21 @@ namespace mmf {
 
 namespace {
 
-__device__ __forceinline__ int act_pos(int k, int K8, int Lc) {
-  return k < K8 ? (k & 7) * Lc + (k >> 3) : 8 * Lc + (k - K8);
+// Chain-transposed LDS copy of one row for the order-exact row norms: chain j at
+// X[j * LS ...], LS = roundup(Lc, 32) + 4 (the +4 spreads the 8 chain rows over distinct
+// LDS banks), zeros from nb up to roundup(Lc, 32), the tail at X[8 * LS ...].
+__device__ __forceinline__ int lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
+
+__device__ __forceinline__ int act_pos(int k, int K8, int LS) {
+  return k < K8 ? (k & 7) * LS + (k >> 3) : 8 * LS + (k - K8);
 }
 
-// Reference sumsq (simd.hpp:69-89) of a chain-transposed vector in LDS; every thread gets
-// the result. `red` is 8 floats of LDS.
-__device__ float block_sumsq(const float* X, int Lc, int nb, int ntail, float* red) {
-  if (threadIdx.x < 8) {
-    const float* c = X + threadIdx.x * Lc;
-    float a = 0.0f;
-    int t = 0;
-    for (; t + 4 <= nb; t += 4) {
-      float4 v = *reinterpret_cast<const float4*>(c + t);
-      a = __builtin_fmaf(v.x, v.x, a);
-      a = __builtin_fmaf(v.y, v.y, a);
-      a = __builtin_fmaf(v.z, v.z, a);
-      a = __builtin_fmaf(v.w, v.w, a);
-    }
-    for (; t < nb; ++t) a = __builtin_fmaf(c[t], c[t], a);
-    red[threadIdx.x] = a;
-  }
+// Reference sumsq (simd.hpp:69-89) of a padded chain-transposed vector in LDS: every
+// thread gets the result. `red` is 8 floats of LDS.
+__device__ float block_sumsq(const float* X, int Lc, int LS, int ntail, float* red) {
+  chain_begin(X, Lc, LS, red);
   __syncthreads();
-  float s = hsum8(red);
-  for (int t = 0; t < ntail; ++t) {
-    float v = X[8 * Lc + t];
-    s = __builtin_fmaf(v, v, s);
-  }
+  const float s = chain_end(X, LS, ntail, red);
   __syncthreads();
   return s;
 }
@@ -56,12 +44,33 @@ __device__ float block_max(float v, float* red) {
   return m;
 }
 
-// Load row x[0..K) into chain-transposed LDS X (zero padding).
-__device__ void load_T(float* X, const float* x, int K, int K8, int Lc, int nb) {
-  for (int k = threadIdx.x; k < K; k += blockDim.x) X[act_pos(k, K8, Lc)] = x[k];
+// for k = threadIdx.x, + blockDim.x, ... < n: fetch(k) for kU elements first, then use(k,
+// value) -- kU global loads in flight per thread instead of one round trip per element.
+constexpr int kU = 8;
+template <class Fetch, class Use>
+__device__ __forceinline__ void batched_loop(int n, Fetch fetch, Use use) {
+  for (int k0 = threadIdx.x; k0 < n; k0 += kU * blockDim.x) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = k0 + u * blockDim.x;
+      v[u] = k < n ? fetch(k) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = k0 + u * blockDim.x;
+      if (k < n) use(k, v[u]);
+    }
+  }
+}
+
+// Load row x[0..K) into the padded chain-transposed LDS layout (zeros in the padding).
+__device__ void load_T(float* X, const float* x, int K, int K8, int Lc, int LS, int nb) {
+  batched_loop(K, [&](int k) { return x[k]; }, [&](int k, float v) { X[act_pos(k, K8, LS)] = v; });
+  const int L32 = (Lc + 31) / 32 * 32;
   for (int j = 0; j < 8; ++j)
-    for (int t = nb + threadIdx.x; t < Lc; t += blockDim.x) X[j * Lc + t] = 0.0f;
-  for (int t = (K - K8) + threadIdx.x; t < 8; t += blockDim.x) X[8 * Lc + t] = 0.0f;
+    for (int t = nb + threadIdx.x; t < L32; t += blockDim.x) X[j * LS + t] = 0.0f;
+  for (int t = (K - K8) + threadIdx.x; t < 8; t += blockDim.x) X[8 * LS + t] = 0.0f;
 }
 
 // ------------------------------------------------------------------------------------
@@ -118,78 +127,88 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
   const int row = blockIdx.x;
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail;
-  float* X = smem;                   // [8*Lc + 8]
-  float* S = X + 8 * Lc + 8;         // [8*Lc + 8] silu(x2) for kPreSwish
-  float* red = S + 8 * Lc + 8;       // [16]
-  load_T(X, a.x + static_cast<size_t>(row) * K, K, K8, Lc, nb);
+  const int LS = lds_stride(Lc);
+  float* X = smem;                   // [8*LS + 8]
+  float* S = X + 8 * LS + 8;         // [8*LS + 8] silu(x2) for kPreSwish
+  float* red = S + 8 * LS + 8;       // [16]
+  load_T(X, a.x + static_cast<size_t>(row) * K, K, K8, Lc, LS, nb);
   if (a.pre == kPreSwish) {
     // silu over one row of `cols` = K elements (rmsnorm_swishgate.cpp:24): tail k >= K & ~7
     const float* o = a.x2 + static_cast<size_t>(row) * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x)
-      S[act_pos(k, K8, Lc)] = silu_of(o[k], k >= (K & ~7));
+    batched_loop(K, [&](int k) { return o[k]; },
+                 [&](int k, float v) { S[act_pos(k, K8, LS)] = silu_of(v, k >= (K & ~7)); });
   }
   __syncthreads();
   if (a.pre != kPreNone) {
-    const float r1 = rstd_of(block_sumsq(X, Lc, nb, nt, red), K, a.eps);
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-      const int p = act_pos(k, K8, Lc);
-      float v = (X[p] * r1) * a.pre_w[k];
+    const float r1 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+    batched_loop(K, [&](int k) { return a.pre_w[k]; }, [&](int k, float w) {
+      const int p = act_pos(k, K8, LS);
+      float v = (X[p] * r1) * w;
       if (a.pre == kPreSwish) v = v * S[p];
       X[p] = v;
-    }
+    });
     __syncthreads();
   }
-  const float r2 = rstd_of(block_sumsq(X, Lc, nb, nt, red), K, a.eps);
+  const float r2 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+  // Per projection: y = (x * rstd) * normw (bitlinear.cpp:62-70) for every element in one
+  // parallel pass into LDS (S is free after stage 1), then the encoding reads only LDS.
+  float* Y = S;
   for (int ai = 0; ai < a.na; ++ai) {
-    const float* nw = a.normw[ai];
+    const float* __restrict__ nw = a.normw[ai];
     const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+    float m = 0.0f;
+    batched_loop(K, [&](int k) { return nw[k]; }, [&](int k, float w) {
+      const int p = act_pos(k, K8, LS);
+      const float y = (X[p] * r2) * w;
+      Y[p] = y;
+      if (MODE == kInt8) m = fmaxf(m, fabsf(y));
+    });
+    float sa = 0.0f;
+    if (MODE == kInt8) {
+      m = block_max(m, red);  // includes the barrier that publishes Y
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+      if (threadIdx.x == 0) act.sa[ar] = sa;
+    } else {
+      __syncthreads();
+    }
     if (MODE == kFloat) {
       float* yo = act.y + ar * act.ystride();
       for (int j = 0; j < 8; ++j)
-        for (int t = threadIdx.x; t < Lc; t += blockDim.x)
-          yo[j * Lc + t] = (t < nb) ? (X[j * Lc + t] * r2) * nw[j + 8 * t] : 0.0f;
-      for (int t = threadIdx.x; t < 8; t += blockDim.x)
-        yo[8 * Lc + t] = (t < nt) ? (X[8 * Lc + t] * r2) * nw[K8 + t] : 0.0f;
+        for (int t = threadIdx.x; t < Lc; t += blockDim.x) yo[j * Lc + t] = (t < nb) ? Y[j * LS + t] : 0.0f;
+      for (int t = threadIdx.x; t < 8; t += blockDim.x) yo[8 * Lc + t] = (t < nt) ? Y[8 * LS + t] : 0.0f;
     } else {
-      float sa = 0.0f;
-      if (MODE == kInt8) {
-        float m = 0.0f;
-        for (int k = threadIdx.x; k < K; k += blockDim.x)
-          m = fmaxf(m, fabsf((X[act_pos(k, K8, Lc)] * r2) * nw[k]));
-        m = block_max(m, red);
-        sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
-        if (threadIdx.x == 0) act.sa[ar] = sa;
-      }
       int8_t* q = act.q + ar * act.qstride();
       // 4 consecutive chain positions per thread -> one 32-bit store per plane
-      for (int j = 0; j < 8; ++j)
-        for (int t4 = threadIdx.x * 4; t4 < Lc; t4 += blockDim.x * 4) {
-          uint32_t hi = 0, lo = 0;
-          for (int u = 0; u < 4; ++u) {
-            const int t = t4 + u;
-            if (t < nb) {
-              const float y = (X[j * Lc + t] * r2) * nw[j + 8 * t];
-              if (MODE == kFixed) {
-                const int32_t c = q510_body(y, a.qs);
-                hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
-                lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
-              } else {
-                hi |= static_cast<uint32_t>(q8_of(y, sa) & 0xFF) << (8 * u);
-              }
+      const int n4 = Lc / 4;
+      for (int w = threadIdx.x; w < 8 * n4; w += blockDim.x) {
+        const int j = w / n4, t4 = (w - j * n4) * 4;
+        uint32_t hi = 0, lo = 0;
+        for (int u = 0; u < 4; ++u) {
+          const int t = t4 + u;
+          if (t < nb) {
+            const float y = Y[j * LS + t];
+            if (MODE == kFixed) {
+              const int32_t c = q510_body(y, a.qs);
+              hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
+              lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
+            } else {
+              hi |= static_cast<uint32_t>(q8_of(y, sa) & 0xFF) << (8 * u);
             }
           }
-          *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
-          if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
         }
+        *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
+        if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
+      }
       for (int t = threadIdx.x; t < 8; t += blockDim.x) {
         int32_t c = 0;
         if (t < nt) {
-          const float y = (X[8 * Lc + t] * r2) * nw[K8 + t];
+          const float y = Y[8 * LS + t];
           c = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
         }
         act.ct[ar * 8 + t] = c;
       }
     }
+    __syncthreads();  // Y is rewritten for the next projection
   }
 }
 
@@ -526,23 +545,38 @@ __global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict
   }
 }
 
-// rmsnorm / swishgate rows: one block per row, chain-transposed copy in LDS for the sumsq
+// rmsnorm / swishgate rows: one block per row, padded chain-transposed copy in LDS for the
+// order-exact sumsq
 __global__ void k_rownorm(const float* __restrict__ x, const float* __restrict__ o,
                           const float* __restrict__ w, float* __restrict__ y, int cols, float eps) {
   extern __shared__ float smem[];
-  const int K = cols, K8 = K & ~7, nb = K8 / 8, Lc = (nb + 15) / 16 * 16 + 16;
+  const int K = cols, K8 = K & ~7, nb = K8 / 8, Lc = nb > 0 ? (nb + 15) / 16 * 16 : 16;
+  const int LS = lds_stride(Lc);
   float* X = smem;
-  float* red = X + 8 * Lc + 8;
+  float* red = X + 8 * LS + 8;
   const float* xr = x + static_cast<size_t>(blockIdx.x) * K;
-  load_T(X, xr, K, K8, Lc, nb);
+  load_T(X, xr, K, K8, Lc, LS, nb);
   __syncthreads();
-  const float r = rstd_of(block_sumsq(X, Lc, nb, K - K8, red), K, eps);
+  const float r = rstd_of(block_sumsq(X, Lc, LS, K - K8, red), K, eps);
   float* yr = y + static_cast<size_t>(blockIdx.x) * K;
   const float* orow = o ? o + static_cast<size_t>(blockIdx.x) * K : nullptr;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    float v = (xr[k] * r) * w[k];
-    if (orow) v = v * silu_of(orow[k], k >= K8);
-    yr[k] = v;
+  for (int k0 = threadIdx.x; k0 < K; k0 += kU * blockDim.x) {
+    float xv[kU], wv[kU], ov[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = k0 + u * blockDim.x;
+      xv[u] = k < K ? xr[k] : 0.0f;
+      wv[u] = k < K ? w[k] : 0.0f;
+      ov[u] = (orow && k < K) ? orow[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = k0 + u * blockDim.x;
+      if (k >= K) continue;
+      float v = (xv[u] * r) * wv[u];
+      if (orow) v = v * silu_of(ov[u], k >= K8);
+      yr[k] = v;
+    }
   }
 }
 
@@ -621,8 +655,10 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
   return e;
 }
 
+static int host_lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
+
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
-  const size_t lds = (2 * static_cast<size_t>(8 * act.Lc + 8) + 16) * sizeof(float);
+  const size_t lds = (2 * static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8) + 16) * sizeof(float);
   const int threads = 256;
   switch (mode) {
     case kFloat: k_prologue<kFloat><<<act.rows, threads, lds, s>>>(a, act); break;
@@ -702,8 +738,8 @@ hipError_t launch_embed(const float* emb, const int64_t* ids, float* h, int rows
 }
 
 static size_t rownorm_lds(int cols) {
-  const int nb = (cols & ~7) / 8, Lc = (nb + 15) / 16 * 16 + 16;
-  return (static_cast<size_t>(8 * Lc + 8) + 16) * sizeof(float);
+  const int nb = (cols & ~7) / 8, Lc = nb > 0 ? (nb + 15) / 16 * 16 : 16;
+  return (static_cast<size_t>(8 * host_lds_stride(Lc) + 8) + 16) * sizeof(float);
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps,
