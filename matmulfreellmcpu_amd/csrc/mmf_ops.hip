@@ -5,6 +5,7 @@
 //
 // Numerics follow the reference engine exactly (see mmf_device.hpp): every fp32
 // reduction keeps the 8-lane order of the AVX2 code, every int32 sum is exact.
+#include <cstdint>
 #include <cstdlib>
 
 #include "mmf_device.hpp"
@@ -209,6 +210,135 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
       }
     }
     __syncthreads();  // Y is rewritten for the next projection
+  }
+}
+
+// The same prologue for K % 4 == 0 with 16-byte aligned inputs: every global input of the
+// row (x, the gate input x2, the stage-1 weight, the NA BitLinear norm weights) is loaded
+// as float4 at entry -- one memory round trip -- and each thread then works on exactly the
+// elements it loaded. Arithmetic and order are those of k_prologue.
+template <int MODE, int PRE, int NA, int MAXV>
+__global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
+  extern __shared__ float smem[];
+  constexpr int NV = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
+  constexpr int IX2 = 1, IPW = (PRE == kPreSwish) ? 2 : 1, INW = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
+  const int row = blockIdx.x;
+  const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
+  const int LS = lds_stride(Lc);
+  float* X = smem;
+  float* S = X + 8 * LS + 8;
+  float* red = S + 8 * LS + 8;
+  const float* src[NV];
+  src[0] = a.x + static_cast<size_t>(row) * K;
+  if (PRE == kPreSwish) src[IX2] = a.x2 + static_cast<size_t>(row) * K;
+  if (PRE != kPreNone) src[IPW] = a.pre_w;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) src[INW + i] = a.normw[i];
+  float4 v[NV][MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    const int k4 = threadIdx.x + j * blockDim.x;
+#pragma unroll
+    for (int vi = 0; vi < NV; ++vi)
+      v[vi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[vi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  auto el = [](const float4& f, int c) { return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w)); };
+  // x (and silu(x2)) into the padded chain-transposed LDS rows
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    const int k4 = threadIdx.x + j * blockDim.x;
+    if (k4 >= K4) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
+      X[p] = el(v[0][j], c);
+      if (PRE == kPreSwish) S[p] = silu_of(el(v[IX2][j], c), k >= K8);
+    }
+  }
+  const int L32 = (Lc + 31) / 32 * 32;
+  for (int jr = 0; jr < 8; ++jr)
+    for (int t = nb + threadIdx.x; t < L32; t += blockDim.x) X[jr * LS + t] = 0.0f;
+  for (int t = nt + threadIdx.x; t < 8; t += blockDim.x) X[8 * LS + t] = 0.0f;
+  __syncthreads();
+  if (PRE != kPreNone) {
+    const float r1 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int k4 = threadIdx.x + j * blockDim.x;
+      if (k4 >= K4) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int p = act_pos(4 * k4 + c, K8, LS);
+        float x = (X[p] * r1) * el(v[IPW][j], c);
+        if (PRE == kPreSwish) x = x * S[p];
+        X[p] = x;
+      }
+    }
+    __syncthreads();
+  }
+  const float r2 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+  float* Y = S;
+#pragma unroll
+  for (int ai = 0; ai < NA; ++ai) {
+    const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int k4 = threadIdx.x + j * blockDim.x;
+      if (k4 >= K4) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int p = act_pos(4 * k4 + c, K8, LS);
+        const float y = (X[p] * r2) * el(v[INW + ai][j], c);
+        Y[p] = y;
+        if (MODE == kInt8) m = fmaxf(m, fabsf(y));
+      }
+    }
+    float sa = 0.0f;
+    if (MODE == kInt8) {
+      m = block_max(m, red);
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+      if (threadIdx.x == 0) act.sa[ar] = sa;
+    } else {
+      __syncthreads();
+    }
+    if (MODE == kFloat) {
+      float* yo = act.y + ar * act.ystride();
+      for (int jr = 0; jr < 8; ++jr)
+        for (int t = threadIdx.x; t < Lc; t += blockDim.x) yo[jr * Lc + t] = (t < nb) ? Y[jr * LS + t] : 0.0f;
+      for (int t = threadIdx.x; t < 8; t += blockDim.x) yo[8 * Lc + t] = (t < nt) ? Y[8 * LS + t] : 0.0f;
+    } else {
+      int8_t* q = act.q + ar * act.qstride();
+      const int n4 = Lc / 4;
+      for (int w = threadIdx.x; w < 8 * n4; w += blockDim.x) {
+        const int jr = w / n4, t4 = (w - jr * n4) * 4;
+        uint32_t hi = 0, lo = 0;
+        for (int u = 0; u < 4; ++u) {
+          const int t = t4 + u;
+          if (t < nb) {
+            const float y = Y[jr * LS + t];
+            if (MODE == kFixed) {
+              const int32_t c = q510_body(y, a.qs);
+              hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
+              lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
+            } else {
+              hi |= static_cast<uint32_t>(q8_of(y, sa) & 0xFF) << (8 * u);
+            }
+          }
+        }
+        *reinterpret_cast<uint32_t*>(q + jr * Lc + t4) = hi;
+        if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + jr * Lc + t4) = lo;
+      }
+      for (int t = threadIdx.x; t < 8; t += blockDim.x) {
+        int32_t c = 0;
+        if (t < nt) {
+          const float y = Y[8 * LS + t];
+          c = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
+        }
+        act.ct[ar * 8 + t] = c;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -657,8 +787,42 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
 
 static int host_lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
 
+template <int MODE, int PRE, int NA>
+static hipError_t prologue4_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
+  if (act.K / 4 <= 3 * 256)
+    k_prologue4<MODE, PRE, NA, 3><<<act.rows, 256, lds, s>>>(a, act);
+  else
+    k_prologue4<MODE, PRE, NA, 7><<<act.rows, 256, lds, s>>>(a, act);
+  return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t prologue4_mode(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
+  if (a.pre == kPreNorm && a.na == 3) return prologue4_inst<MODE, kPreNorm, 3>(a, act, lds, s);
+  if (a.pre == kPreNorm && a.na == 1) return prologue4_inst<MODE, kPreNorm, 1>(a, act, lds, s);
+  if (a.pre == kPreSwish && a.na == 1) return prologue4_inst<MODE, kPreSwish, 1>(a, act, lds, s);
+  if (a.pre == kPreNone && a.na == 1) return prologue4_inst<MODE, kPreNone, 1>(a, act, lds, s);
+  if (a.pre == kPreNone && a.na == 3) return prologue4_inst<MODE, kPreNone, 3>(a, act, lds, s);
+  return hipErrorNotSupported;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   const size_t lds = (2 * static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8) + 16) * sizeof(float);
+  bool fast = act.K % 4 == 0 && act.K / 4 <= 7 * 256 && aligned16(a.x) && (a.na == 1 || a.na == 3);
+  if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
+  if (a.pre == kPreSwish) fast = fast && aligned16(a.x2);
+  for (int i = 0; i < a.na; ++i) fast = fast && aligned16(a.normw[i]);
+  if (fast) {
+    hipError_t e = hipErrorNotSupported;
+    switch (mode) {
+      case kFloat: e = prologue4_mode<kFloat>(a, act, lds, s); break;
+      case kFixed: e = prologue4_mode<kFixed>(a, act, lds, s); break;
+      default: e = prologue4_mode<kInt8>(a, act, lds, s); break;
+    }
+    if (e != hipErrorNotSupported) return e;
+  }
   const int threads = 256;
   switch (mode) {
     case kFloat: k_prologue<kFloat><<<act.rows, threads, lds, s>>>(a, act); break;
