@@ -665,6 +665,95 @@ __global__ __launch_bounds__(64) void k_scan_seq(const float* __restrict__ g, co
   state[c] = s;
 }
 
+// The recurrence for H % 16 == 0, staged through LDS so that enough bytes are in flight:
+// a block owns 16 columns (H/16 blocks spread over the CUs) and walks time in tiles of
+// kScTT steps. Waves by role: wave 0 runs the 16 column chains (state = fma(g, state, in),
+// in time order) from LDS; waves 1-4 fill a ring of kScNR tiles of g and in by direct
+// global-to-LDS DMA (lane l's 16 bytes land at LDS base + 16l: 16 steps x 16 columns per
+// transfer); waves 5-6 store the previous tile's results. One barrier per tile.
+constexpr int kScCols = 16, kScTT = 128, kScNR = 4;
+constexpr int kScWaves = 7;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void scan_issue(const float* g, const float* in, float* ring, int tile, int slot,
+                                           int T, int H, int c0, int lw, int lane) {
+  // loader wave lw (0..3) issues chunks lw*4 .. lw*4+3 of this tile (8 per array)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = lw * 4 + i, arr = idx >> 3, q = idx & 7;
+    int t = tile * kScTT + 16 * q + (lane >> 2);
+    t = t < T ? t : T - 1;
+    const float* src = (arr ? in : g) + static_cast<size_t>(t) * H + c0 + 4 * (lane & 3);
+    float* dst = ring + ((slot * 2 + arr) * kScTT + 16 * q) * kScCols;
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __restrict__ g, const float* __restrict__ in,
+                                                             float* __restrict__ recur, float* __restrict__ state,
+                                                             int T, int H) {
+  extern __shared__ __align__(16) float sm[];
+  float* ring = sm;                                      // [kScNR][2][kScTT][16]
+  float* R = sm + kScNR * 2 * kScTT * kScCols;           // [2][kScTT][16]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c0 = blockIdx.x * kScCols;
+  const int ntiles = (T + kScTT - 1) / kScTT;
+  const bool loader = wave >= 1 && wave <= 4;
+  float s = (wave == 0 && lane < kScCols) ? state[c0 + lane] : 0.0f;
+  if (loader)
+    for (int t = 0; t < kScNR - 1 && t < ntiles; ++t) scan_issue(g, in, ring, t, t, T, H, c0, wave - 1, lane);
+  for (int k = 0; k <= ntiles; ++k) {
+    // this wave's LDS writes (wave 0's results) have landed before the barrier publishes them
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    if (loader) {
+      // this wave's transfers of tile k are done once only later tiles' are outstanding
+      if (k + kScNR - 2 < ntiles) __builtin_amdgcn_s_waitcnt(((kScNR - 2) * 4 & 0xF) | (((kScNR - 2) * 4 >> 4) << 14) | 0x0F70);
+      else __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (loader && k + kScNR - 1 < ntiles)
+      scan_issue(g, in, ring, k + kScNR - 1, (k + kScNR - 1) % kScNR, T, H, c0, wave - 1, lane);
+    if (wave == 0 && k < ntiles && lane < kScCols) {
+      const float* G = ring + ((k % kScNR) * 2 + 0) * kScTT * kScCols;
+      const float* I = ring + ((k % kScNR) * 2 + 1) * kScTT * kScCols;
+      float* Rt = R + (k & 1) * kScTT * kScCols;
+      const int n = min(kScTT, T - k * kScTT);
+      int t = 0;
+      for (; t + 8 <= n; t += 8) {
+        float gv[8], iv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          gv[u] = G[(t + u) * kScCols + lane];
+          iv[u] = I[(t + u) * kScCols + lane];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          s = __builtin_fmaf(gv[u], s, iv[u]);
+          Rt[(t + u) * kScCols + lane] = s;
+        }
+      }
+      for (; t < n; ++t) {
+        s = __builtin_fmaf(G[t * kScCols + lane], s, I[t * kScCols + lane]);
+        Rt[t * kScCols + lane] = s;
+      }
+    }
+    if (wave >= 5 && k >= 1) {
+      // results of tile k - 1 to global memory, a float4 (4 columns of one step) per thread
+      const float* Rp = R + ((k - 1) & 1) * kScTT * kScCols;
+      const int n = min(kScTT, T - (k - 1) * kScTT);
+      for (int f = threadIdx.x - 320; f < kScTT * kScCols / 4; f += 128) {
+        const int row = f >> 2, c4 = f & 3;
+        if (row < n)
+          *reinterpret_cast<float4*>(recur + static_cast<size_t>((k - 1) * kScTT + row) * H + c0 + 4 * c4) =
+              *reinterpret_cast<const float4*>(Rp + row * kScCols + 4 * c4);
+      }
+    }
+  }
+  if (wave == 0 && lane < kScCols) state[c0 + lane] = s;
+}
+
 __global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict__ ids,
                         float* __restrict__ h, int rows, int H) {
   const size_t n = static_cast<size_t>(rows) * H;
@@ -886,7 +975,14 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
     k_gate<<<blocks, 256, 0, s>>>(i, f, scan_out, lb, rows, H);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_scan_seq<<<(H + 63) / 64, 64, 0, s>>>(f, scan_out, recur, state, rows, H);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(scan_out) |
+                           reinterpret_cast<uintptr_t>(recur)) & 15) == 0;
+    if (H % kScCols == 0 && aligned) {
+      const size_t lds = (static_cast<size_t>(kScNR) * 2 + 2) * kScTT * kScCols * sizeof(float);
+      k_scan_ring<<<H / kScCols, 64 * kScWaves, lds, s>>>(f, scan_out, recur, state, rows, H);
+    } else {
+      k_scan_seq<<<(H + 63) / 64, 64, 0, s>>>(f, scan_out, recur, state, rows, H);
+    }
     return hipGetLastError();
   }
   const int n = stream_state ? rows * H : H;
