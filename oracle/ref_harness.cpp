@@ -10,6 +10,7 @@
 //     cpp/include/mmfree/simd.hpp:69-357
 //   CpuBackend::matmul  cpp/include/mmfree/ternary_backend.hpp:96-103
 //   Model::{forward, generate, generate_serve}  cpp/include/mmfree/model.hpp:37-70
+//   Tokenizer::{encode, decode}  cpp/include/mmfree/tokenizer.hpp:15-37
 // Per-layer capture reads the Model's private scratch and recurrent state, so model.hpp
 // is included with `private` opened up (standard headers are included first so only the
 // reference's own headers see the define).
@@ -26,6 +27,7 @@
 #include "mmfree/kernels.hpp"
 #include "mmfree/simd.hpp"
 #include "mmfree/ternary_backend.hpp"
+#include "mmfree/tokenizer.hpp"
 #include "mmfree/weights.hpp"
 #define private public
 #include "mmfree/model.hpp"
@@ -207,6 +209,29 @@ void ref_model_trace(void* h, const std::int64_t* ids, std::size_t T, float* h_o
     if (scan_out) std::memcpy(scan_out + l * TH, m.scan_.data(), TH * sizeof(float));
     if (recur_out) std::memcpy(recur_out + l * TH, m.recur_.data(), TH * sizeof(float));
   }
+}
+
+// ---- tokenizer ----
+void* ref_tok_open(const char* path) {
+  try {
+    return new Tokenizer(path);
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+void ref_tok_close(void* h) { delete static_cast<Tokenizer*>(h); }
+// ids of `text` (n bytes) into out (capacity cap); returns the count (may exceed cap)
+long ref_tok_encode(void* h, const char* text, std::size_t n, int add_bos, std::int64_t* out, std::size_t cap) {
+  const auto ids = static_cast<Tokenizer*>(h)->encode(std::string(text, n), add_bos != 0);
+  for (std::size_t i = 0; i < ids.size() && i < cap; ++i) out[i] = ids[i];
+  return static_cast<long>(ids.size());
+}
+// bytes of decode(ids) into out (capacity cap); returns the length (may exceed cap)
+long ref_tok_decode(void* h, const std::int64_t* ids, std::size_t n, int skip_special, char* out, std::size_t cap) {
+  const std::string s = static_cast<Tokenizer*>(h)->decode(std::vector<std::int64_t>(ids, ids + n), skip_special != 0);
+  std::memcpy(out, s.data(), s.size() < cap ? s.size() : cap);
+  return static_cast<long>(s.size());
 }
 
 }  // extern "C"

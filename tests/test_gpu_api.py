@@ -114,6 +114,40 @@ def test_cli_ids_match_reference(blobs, tmp_path, mode, extra):
     assert_bitexact(np.fromfile(ours, np.float32), np.fromfile(theirs, np.float32), "--logits-out")
 
 
+def test_cli_text_generation_matches_reference(blobs, tmp_path):
+    """Text in, streamed text out (the reference CLI's main path): same bytes on stdout, with
+    BOS, --no-bos, sampling, and an EOS stop (the tokenizer's EOS set to the first greedy
+    token, so text generation stops right after it)."""
+    _need(CLI)
+    ref_cli = _ref_cli()
+    from tok_util import make_tokenizer, write_mmtok
+    blob = blobs("small")
+    tok = str(tmp_path / "t.mmtok")
+    pieces, merges = make_tokenizer(tok, seed=4)
+    cases = [["--gen", "12", "--mode", "fixed", "the quick brown fox"],
+             ["--gen", "12", "--mode", "float", "--no-bos", "café über"],
+             ["--gen", "10", "--mode", "fixed", "--temp", "0.9", "--seed", "5", "once upon a time"],
+             ["--gen", "6", "--mode", "float", "--show-ids", "hello world"]]
+    for extra in cases:
+        args = ["--blob", blob, "--tokenizer", tok] + extra
+        a = subprocess.run([CLI] + args, capture_output=True, timeout=120)
+        b = subprocess.run([ref_cli] + args, capture_output=True, timeout=120)
+        assert a.returncode == b.returncode == 0, (extra, a.stderr[-500:], b.stderr[-500:])
+        assert a.stdout == b.stdout, extra
+        if "--show-ids" in extra:
+            assert a.stderr == b.stderr
+    first = _run([ref_cli, "--blob", blob, "--tokenizer", tok, "--gen", "1", "--mode", "fixed", "--print-ids",
+                  "the quick brown fox"]).split()[-1]
+    eos_tok = str(tmp_path / "e.mmtok")
+    write_mmtok(eos_tok, pieces, merges, eos=int(first))
+    args = ["--blob", blob, "--tokenizer", eos_tok, "--gen", "12", "--mode", "fixed", "--show-ids", "the quick brown fox"]
+    a = subprocess.run([CLI] + args, capture_output=True, timeout=120)
+    b = subprocess.run([ref_cli] + args, capture_output=True, timeout=120)
+    assert a.returncode == b.returncode == 0
+    assert a.stdout == b.stdout and a.stderr == b.stderr
+    assert b"gen ids (1):" in a.stderr
+
+
 def test_cli_errors_like_reference(blobs):
     _need(CLI)
     r = subprocess.run([CLI, "--no-such-flag"], capture_output=True, text=True, timeout=60)
