@@ -547,6 +547,142 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a, ActBuf act) {
 }
 
 // ------------------------------------------------------------------------------------
+// Float-mode ternary GEMM over row tiles, register-blocked over outputs. Block = 128 threads
+// = 16 output lanes x 8 chains; thread (ol, j) runs chain j (the reference's AVX2 lane j,
+// simd.hpp:92-122: fma(y_k, w_k, a) over k = j + 8t in t order) of kFNO outputs from kFNO
+// slabs, for R rows. Activations of kFW words per chain are staged in LDS for the R rows,
+// chain rows padded by 4 floats so the 8 chains of a wave hit distinct banks; each value
+// read feeds kFNO FMAs and each weight word R x 16. PAIR: the first half of the slabs are
+// gate outputs, the second half their up partners N/2 later (swiglu epilogue).
+// ------------------------------------------------------------------------------------
+constexpr int kFNO = 4;               // outputs per thread
+constexpr int kFW = 4;                // words per chain per LDS chunk
+constexpr int kFCS = kFW * 16 + 4;    // floats per staged chain row
+
+template <int R, bool PAIR>
+__global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
+  extern __shared__ float smem[];
+  const int z = blockIdx.z;
+  const ProjDev& P = a.p[z];
+  const Geom& g = P.g;
+  const int Lc = act.Lc, Wc = g.Wc;
+  const int tid = threadIdx.x, ol = tid >> 3, j = tid & 7;
+  const int row0 = blockIdx.y * R;
+  const int nrows = min(R, a.rows - row0);
+  const int am = (act.na > 1) ? z : 0;
+  const int half = g.ngroups / 2;
+  int grp[kFNO];
+  bool gok[kFNO];
+#pragma unroll
+  for (int s = 0; s < kFNO; ++s) {
+    if (PAIR) {
+      const int gg = blockIdx.x * (kFNO / 2) + (s % (kFNO / 2));
+      gok[s] = gg < half;
+      grp[s] = (s < kFNO / 2) ? gg : half + gg;
+    } else {
+      grp[s] = blockIdx.x * kFNO + s;
+      gok[s] = grp[s] < g.ngroups;
+    }
+    if (!gok[s]) grp[s] = 0;
+  }
+  const uint32_t* slab[kFNO];
+#pragma unroll
+  for (int s = 0; s < kFNO; ++s) slab[s] = P.pk + static_cast<size_t>(grp[s]) * Wc * 128 + ol * 8 + j;
+  float acc[kFNO][R];
+#pragma unroll
+  for (int s = 0; s < kFNO; ++s)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[s][r] = 0.0f;
+  constexpr int PR = 8 * kFCS;  // LDS floats per staged row
+  const float* ybase = act.y + (static_cast<size_t>(am) * act.rows + row0) * act.ystride();
+  for (int m0 = 0; m0 < Wc; m0 += kFW) {
+    const int mw = min(kFW, Wc - m0);
+    uint32_t w[kFW][kFNO];
+#pragma unroll
+    for (int mm = 0; mm < kFW; ++mm)
+#pragma unroll
+      for (int s = 0; s < kFNO; ++s)
+        w[mm][s] = (mm < mw && gok[s]) ? slab[s][static_cast<size_t>(m0 + mm) * 128] : 0u;
+    __syncthreads();
+    const int n4 = mw * 4;
+    for (int e = tid; e < R * 8 * n4; e += 128) {
+      const int r = e / (8 * n4), rem = e - r * 8 * n4, jj = rem / n4, q = rem - jj * n4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r < nrows)
+        v = *reinterpret_cast<const float4*>(ybase + static_cast<size_t>(r) * act.ystride() + jj * Lc + m0 * 16 + q * 4);
+      *reinterpret_cast<float4*>(smem + r * PR + jj * kFCS + q * 4) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mm = 0; mm < kFW; ++mm) {
+      if (mm >= mw) break;
+      float wf[kFNO][16];
+#pragma unroll
+      for (int s = 0; s < kFNO; ++s)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) wf[s][t] = code_f(w[mm][s], t);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float* yl = smem + r * PR + j * kFCS + mm * 16;
+        float y[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 v = *reinterpret_cast<const float4*>(yl + 4 * q4);
+          y[4 * q4] = v.x;
+          y[4 * q4 + 1] = v.y;
+          y[4 * q4 + 2] = v.z;
+          y[4 * q4 + 3] = v.w;
+        }
+#pragma unroll
+        for (int s = 0; s < kFNO; ++s)
+#pragma unroll
+          for (int t = 0; t < 16; ++t) acc[s][r] = __builtin_fmaf(y[t], wf[s][t], acc[s][r]);
+      }
+    }
+  }
+  // reduce the 8 chains of each output (hsum_ps order), tails, scale, epilogue
+  const int Nout = PAIR ? g.N / 2 : g.N;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const size_t ar = static_cast<size_t>(am) * act.rows + row0 + r;
+    float val[kFNO];
+#pragma unroll
+    for (int s = 0; s < kFNO; ++s) {
+      float sum = hsum8_lanes(acc[s][r]);
+      const int o = grp[s] * 16 + ol;
+      if (j == 0 && r < nrows && gok[s] && o < g.N) {
+        const float* yt = act.y + ar * act.ystride() + 8 * Lc;
+        for (int t = 0; t < g.ntail; ++t) {
+          const int8_t wt = P.tail[o * 8 + t];
+          if (wt > 0) sum += yt[t];
+          else if (wt < 0) sum -= yt[t];
+        }
+      }
+      val[s] = sum * P.inv_scale_w;
+    }
+    if (j != 0 || r >= nrows) continue;
+    const size_t grow = static_cast<size_t>(row0 + r);
+    if (PAIR) {
+#pragma unroll
+      for (int s = 0; s < kFNO / 2; ++s) {
+        const int o = grp[s] * 16 + ol;
+        if (!gok[s] || o >= Nout) continue;
+        const size_t e = grow * Nout + o;
+        a.out[0][e] = swiglu_of(val[s], val[s + kFNO / 2], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < kFNO; ++s) {
+        const int o = grp[s] * 16 + ol;
+        if (!gok[s] || o >= g.N) continue;
+        const size_t e = grow * g.N + o;
+        a.out[z][e] = (a.epi == kEpiAdd) ? a.add[e] + val[s] : val[s];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // HGRN gate + recurrence (hgrn_model.cpp:109-150)
 // ------------------------------------------------------------------------------------
 __global__ void k_mixer(const float* __restrict__ i, float* __restrict__ f, float* __restrict__ scan_out,
@@ -937,8 +1073,23 @@ static hipError_t gemm_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s)
   return hipGetLastError();
 }
 
+template <int R, bool PAIR>
+static hipError_t gemm_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const Geom& g = a.p[0].g;
+  const size_t lds = static_cast<size_t>(R) * 8 * kFCS * sizeof(float);
+  const int gx = PAIR ? (g.ngroups / 2 + kFNO / 2 - 1) / (kFNO / 2) : (g.ngroups + kFNO - 1) / kFNO;
+  dim3 grid(gx, (a.rows + R - 1) / R, PAIR ? 1 : a.nmat);
+  k_gemm_f<R, PAIR><<<grid, 128, lds, s>>>(a, act);
+  return hipGetLastError();
+}
+
 template <int MODE>
 static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  if (MODE == kFloat && a.rows > 4) {
+    const bool pair = a.epi == kEpiSwigluPair;
+    if (a.rows <= 64) return pair ? gemm_f_inst<8, true>(a, act, s) : gemm_f_inst<8, false>(a, act, s);
+    return pair ? gemm_f_inst<16, true>(a, act, s) : gemm_f_inst<16, false>(a, act, s);
+  }
   const bool pair = a.epi == kEpiSwigluPair;
   if (a.rows <= 1) return pair ? gemm_inst<MODE, 1, true>(a, act, s) : gemm_inst<MODE, 1, false>(a, act, s);
   if (a.rows <= 4) return pair ? gemm_inst<MODE, 4, true>(a, act, s) : gemm_inst<MODE, 4, false>(a, act, s);
