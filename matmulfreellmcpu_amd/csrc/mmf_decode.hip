@@ -45,6 +45,10 @@ namespace mmf {
 
 namespace {
 
+// Makes the listed uniform values live in scalar registers at this point (no instruction is
+// emitted; the loads that produce them must complete before it).
+#define MMF_PIN(...) asm volatile("" ::__VA_ARGS__)
+
 template <int KIND> struct KindTraits;
 // NM matrices (one wave pair each), NA activation vectors, NP prologue source vectors
 template <> struct KindTraits<kIFG> { static constexpr int NM = 3, NA = 3, NP = 5; };
@@ -53,15 +57,61 @@ template <> struct KindTraits<kGate> { static constexpr int NM = 2, NA = 1, NP =
 template <> struct KindTraits<kDown> { static constexpr int NM = 1, NA = 1, NP = 2; };
 template <> struct KindTraits<kLM> { static constexpr int NM = 1, NA = 1, NP = 3; };
 
-constexpr int kPF = 16;  // weight words prefetched at entry
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int MODE, int KIND, int NV>
 __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArgs a) {
   constexpr int NM = KindTraits<KIND>::NM, NA = KindTraits<KIND>::NA, NP = KindTraits<KIND>::NP;
   constexpr int BS = kBlock * NM;
   extern __shared__ float smem[];
-  const Geom& g = a.p[0].g;
-  const int Lc = g.Lc, nt = g.ntail, Wc = g.Wc;
+  // ---- kernel arguments ---------------------------------------------------------------------
+  // Every field the launch uses is read here and pinned in scalar registers: the scalar loads
+  // then issue back to back at entry and cost one round trip, instead of one dependent round
+  // trip each where a field is first used (the compiler otherwise sinks them to their uses).
+  const int mis = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 7);  // wave's matrix
+  const ProjDev& Pa = a.p[KIND == kIFG ? mis : 0];
+  const Geom& g0 = a.p[0].g;
+  const int gN = g0.N, gK = g0.K, Lc = g0.Lc, nt = g0.ntail, Wc = g0.Wc, gng = g0.ngroups;
+  const uint32_t* const pk = Pa.pk;
+  const int8_t* const ptail = Pa.tail;
+  const int32_t* const prowsum = Pa.rowsum;
+  const float pscale = Pa.scale_w, pinv = Pa.inv_scale_w, invfx = a.inv_fixed[KIND == kIFG ? mis : 0];
+  const float* const nw0 = a.p[0].normwT;
+  const float* const nw1 = a.p[1].normwT;
+  const float* const nw2 = a.p[2].normwT;
+  const float* const ax = a.x;
+  const float* const aembT = a.embT;
+  const float* const ax2 = a.x2;
+  const float* const apre = a.pre_w;
+  const float* const alb = a.lb;
+  const float* const ahin = a.hin;
+  float* const astate = a.state;
+  float* const arecur = a.recur;
+  float* const agout = a.gout;
+  float* const aout = a.out;
+  unsigned long long* const akeys = a.keys;
+  int64_t* const ahist = a.hist;
+  int32_t* const ahist_pos = a.hist_pos;
+  const int awg = a.wgroups, aoLc = a.oLc, aoK8 = a.oK8, aH = a.H, avocab = a.vocab, ankeys = a.nkeys,
+            ahist_cap = a.hist_cap;
+  const float aeps = a.eps, aqs = a.qs;
+#define MMF_PIN_BASE                                                                           \
+  "s"(gN), "s"(gK), "s"(Lc), "s"(nt), "s"(Wc), "s"(pk), "s"(ptail), "s"(prowsum), "s"(pscale),  \
+      "s"(pinv), "s"(invfx), "s"(nw0), "s"(ax), "s"(aout), "s"(awg), "s"(aeps), "s"(aqs)
+  // one statement per kind, so that all the loads precede it (layer 0's token-gather fields
+  // are left to load where used)
+  if constexpr (KIND == kIFG)
+    MMF_PIN(MMF_PIN_BASE, "s"(nw1), "s"(nw2), "s"(alb), "s"(astate), "s"(arecur), "s"(agout), "s"(aH), "s"(apre),
+            "s"(aoLc), "s"(aoK8));
+  else if constexpr (KIND == kO)
+    MMF_PIN(MMF_PIN_BASE, "s"(apre), "s"(ax2), "s"(ahin), "s"(aoLc), "s"(aoK8));
+  else if constexpr (KIND == kGate)
+    MMF_PIN(MMF_PIN_BASE, "s"(gng), "s"(apre), "s"(aoLc), "s"(aoK8));
+  else if constexpr (KIND == kDown)
+    MMF_PIN(MMF_PIN_BASE, "s"(ahin), "s"(aoLc), "s"(aoK8));
+  else
+    MMF_PIN(MMF_PIN_BASE, "s"(apre), "s"(akeys));
+#undef MMF_PIN_BASE
   const int W = 8 * Lc + 8;  // floats of a chain-transposed vector in global memory
   const int W4 = W / 4;
   // LDS copies pad each chain row by 16 bytes so that the 8 chain lanes of a wave read
@@ -70,9 +120,8 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   const int LS = L32 + 4, WL = 8 * LS + 8, LQ = Lc + 16;
   const int tid = threadIdx.x, mi = tid >> 7, lt = tid & 127, ol = lt >> 3, j = lt & 7;
   const int ai = (NA > 1) ? mi : 0;  // this thread's activation vector
-  const int nout = (KIND == kGate) ? g.N / 2 : g.N;
+  const int nout = (KIND == kGate) ? gN / 2 : gN;
   const int ngroups_out = (nout + kGroup - 1) / kGroup;
-  const ProjDev& P = a.p[KIND == kIFG ? mi : 0];
 
   float* X = smem;           // [WL] input row
   float* S = X + WL;         // [WL] kO: silu(recur)
@@ -82,36 +131,33 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   int8_t* Q = reinterpret_cast<int8_t*>(Y);
   int32_t* CT = reinterpret_cast<int32_t*>(Q + NA * 16 * LQ);
   float* SA = reinterpret_cast<float*>(CT + NA * 8);
+  // [NM][G][Wc][128] all weight words of the block's G output groups, slab row layout
+  uint32_t* WX = (MODE == kFloat) ? reinterpret_cast<uint32_t*>(Y + NA * WL) : reinterpret_cast<uint32_t*>(SA + NA);
+  const int G = awg;
 
   // ---- entry: issue every load that does not depend on the prologue --------------------
   MMF_MARK(KIND, 0);
   MMF_SPAN(KIND, true);
   int og = blockIdx.x;
   const int o0 = og * kGroup + ol;
-  const int mrow = (KIND == kGate && mi == 1) ? g.ngroups / 2 : 0;  // gate: the up half
-  uint32_t wpf[kPF];
-  {
-    const uint32_t* s0 = P.pk + static_cast<size_t>(og + mrow) * Wc * 128 + ol * 8 + j;
-#pragma unroll
-    for (int u = 0; u < kPF; ++u) wpf[u] = (u < Wc && og < ngroups_out) ? s0[static_cast<size_t>(u) * 128] : 0u;
-  }
+  const int mrow = (KIND == kGate && mi == 1) ? gng / 2 : 0;  // gate: the up half
   const bool epi = (mi == 0 && j == 0 && og < ngroups_out && o0 < nout);
-  const int po = epi ? ((o0 < a.oK8) ? (o0 & 7) * a.oLc + (o0 >> 3) : 8 * a.oLc + (o0 - a.oK8)) : 0;
+  const int po = epi ? ((o0 < aoK8) ? (o0 & 7) * aoLc + (o0 >> 3) : 8 * aoLc + (o0 - aoK8)) : 0;
   float e_lb = 0.0f, e_st = 0.0f, e_hin = 0.0f;
   if (epi) {
     if (KIND == kIFG) {
-      if (a.lb) e_lb = a.lb[o0];
-      e_st = a.state[o0];
+      if (alb) e_lb = alb[o0];
+      e_st = astate[o0];
     }
-    if (KIND == kO || KIND == kDown) e_hin = a.hin[po];
+    if (KIND == kO || KIND == kDown) e_hin = ahin[po];
   }
 
   // layer 0: the token is the argmax over the previous lm_head's per-block keys
   int64_t tok = 0;
-  if (KIND == kIFG && a.x == nullptr) {
+  if (KIND == kIFG && ax == nullptr) {
     unsigned long long best = 0ull;
-    for (int e = tid; e < a.nkeys; e += BS) {
-      const unsigned long long k = a.keys[e];
+    for (int e = tid; e < ankeys; e += BS) {
+      const unsigned long long k = akeys[e];
       best = k > best ? k : best;
     }
     for (int off = 32; off > 0; off >>= 1) {
@@ -124,22 +170,22 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     best = r64[0];
     for (int w = 1; w < BS / 64; ++w) best = r64[w] > best ? r64[w] : best;
     tok = key_index(best);
-    if (tok < 0 || tok >= a.vocab) tok = 0;
-    if (blockIdx.x == 0 && tid == 0 && a.hist) {
-      const int pos = *a.hist_pos;
-      if (pos < a.hist_cap) a.hist[pos] = tok;
-      *a.hist_pos = pos + 1;
+    if (tok < 0 || tok >= avocab) tok = 0;
+    if (blockIdx.x == 0 && tid == 0 && ahist) {
+      const int pos = *ahist_pos;
+      if (pos < ahist_cap) ahist[pos] = tok;
+      *ahist_pos = pos + 1;
     }
   }
 
   // prologue sources (all chain-transposed, zero-padded, W floats):
   //   0: input row   1: stage-1 weight (kO: recur)   then the BitLinear norm weights
   const float* src[NP];
-  src[0] = (KIND == kIFG && a.x == nullptr) ? a.embT + static_cast<size_t>(tok) * W : a.x;
-  if (KIND == kIFG) { src[1] = a.pre_w; src[2] = a.p[0].normwT; src[3] = a.p[1].normwT; src[4] = a.p[2].normwT; }
-  if (KIND == kO) { src[1] = a.x2; src[2] = a.pre_w; src[3] = a.p[0].normwT; }
-  if (KIND == kGate || KIND == kLM) { src[1] = a.pre_w; src[2] = a.p[0].normwT; }
-  if (KIND == kDown) { src[1] = a.p[0].normwT; }
+  src[0] = (KIND == kIFG && ax == nullptr) ? aembT + static_cast<size_t>(tok) * W : ax;
+  if (KIND == kIFG) { src[1] = apre; src[2] = nw0; src[3] = nw1; src[4] = nw2; }
+  if (KIND == kO) { src[1] = ax2; src[2] = apre; src[3] = nw0; }
+  if (KIND == kGate || KIND == kLM) { src[1] = apre; src[2] = nw0; }
+  if (KIND == kDown) { src[1] = nw0; }
   float4 v[NP][NV];
 #pragma unroll
   for (int s = 0; s < NP; ++s)
@@ -148,6 +194,16 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
       const int e = tid + i * BS;
       v[s][i] = (e < W4) ? reinterpret_cast<const float4*>(src[s])[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+  // the weight words of the block's output groups (after the input, which the norms need
+  // first): straight into LDS, one dword per lane, in the slab row order
+  for (int gi = 0; gi < G; ++gi) {
+    const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
+    if (og_i >= ngroups_out) break;
+    const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * Wc * 128 + lt;
+    uint32_t* dx = WX + (mi * G + gi) * Wc * 128 + (lt & 64);  // this wave's 64 dwords of a row
+    for (int m = 0; m < Wc; ++m)
+      __builtin_amdgcn_global_load_lds(sx + m * 128, (lds_void*)(dx + m * 128), 4, 0, 0);
+  }
   // LDS float4 index of each of this thread's global float4s
   int li[NV];
 #pragma unroll
@@ -174,19 +230,8 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   // ---- stage 1: the kernel's own pre-norm -------------------------------------------------
   if (KIND != kDown) {
     chain_begin(X, Lc, LS, red);
-    if (KIND == kO && tid >= 64) {
-      // silu(recur) on wave 1 while wave 0 runs the chains (one SIMD call of H elements,
-      // rmsnorm_swishgate.cpp:24: tail elements sit after the 8 rows)
-      const int WL4 = WL / 4;
-      for (int e = tid - 64; e < WL4; e += BS - 64) {
-        float4 r = reinterpret_cast<float4*>(S)[e];
-        const bool tl = 4 * e >= 8 * LS;
-        r.x = silu_of(r.x, tl); r.y = silu_of(r.y, tl); r.z = silu_of(r.z, tl); r.w = silu_of(r.w, tl);
-        reinterpret_cast<float4*>(S)[e] = r;
-      }
-    }
     __syncthreads();
-    const float r1 = rstd_of(chain_end(X, LS, nt, red), g.K, a.eps);
+    const float r1 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
     constexpr int PW = (KIND == kO) ? 2 : 1;  // which source holds the stage-1 weight
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -208,7 +253,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   MMF_MARK(KIND, 2);
   chain_begin(X, Lc, LS, red);
   __syncthreads();
-  const float r2 = rstd_of(chain_end(X, LS, nt, red), g.K, a.eps);
+  const float r2 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
   MMF_MARK(KIND, 3);
   constexpr int NW0 = NP - NA;  // first norm-weight source
 #pragma unroll
@@ -259,7 +304,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               if (MODE == kFixed) {
-                const int32_t c = q510_body(y[u], a.qs);
+                const int32_t c = q510_body(y[u], aqs);
                 hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
                 lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
               } else {
@@ -273,7 +318,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               const int t = 4 * e - 8 * Lc + u;
-              CT[aa * 8 + t] = (t < nt) ? ((MODE == kFixed) ? q510_tail(y[u], a.qs) : q8_of(y[u], sa)) : 0;
+              CT[aa * 8 + t] = (t < nt) ? ((MODE == kFixed) ? q510_tail(y[u], aqs) : q8_of(y[u], sa)) : 0;
             }
           }
         }
@@ -281,49 +326,69 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
       if (MODE == kInt8) __syncthreads();  // red[8..] reused by the next vector's max
     }
   }
+  if (G > 0) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies landed
   __syncthreads();
 
   // ---- GEMV: each thread one chain of one matrix --------------------------------------------
   MMF_MARK(KIND, 4);
   unsigned long long best = 0ull;
-  for (; og < ngroups_out; og += gridDim.x) {
-    const uint32_t* slab = P.pk + static_cast<size_t>(og + mrow) * Wc * 128 + ol * 8 + j;
-    if (og != static_cast<int>(blockIdx.x)) {  // later groups (kLM grid-stride): reload
-#pragma unroll
-      for (int u = 0; u < kPF; ++u) wpf[u] = (u < Wc) ? slab[static_cast<size_t>(u) * 128] : 0u;
-    }
+  for (int gi = 0; og < ngroups_out; og += gridDim.x, ++gi) {
     float facc = 0.0f;
     int32_t hacc = 0, lacc = 0;
-    auto word = [&](uint32_t w, int m) {
+    // One word = 16 codes of chain j against 16 activations: act_of reads the activations
+    // from LDS, word_of runs the chain over them.
+    struct Act {
+      float4 f[MODE == kFloat ? 4 : 1];
+      uint4 h, l;
+    };
+    auto act_of = [&](int m) {
+      Act r;
       if (MODE == kFloat) {
         const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS + 16 * m);
-        const float4 y0 = yl[0], y1 = yl[1], y2 = yl[2], y3 = yl[3];
-        const float y[16] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w,
-                             y2.x, y2.y, y2.z, y2.w, y3.x, y3.y, y3.z, y3.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r.f[q] = yl[q];
+      } else {
+        const int8_t* ql = Q + ai * 16 * LQ + j * LQ + 16 * m;
+        r.h = *reinterpret_cast<const uint4*>(ql);
+        if (MODE == kFixed) r.l = *reinterpret_cast<const uint4*>(ql + 8 * LQ);
+      }
+      return r;
+    };
+    auto word_of = [&](uint32_t w, const Act& x) {
+      if (MODE == kFloat) {
+        const float y[16] = {x.f[0].x, x.f[0].y, x.f[0].z, x.f[0].w, x.f[1].x, x.f[1].y, x.f[1].z, x.f[1].w,
+                             x.f[2].x, x.f[2].y, x.f[2].z, x.f[2].w, x.f[3].x, x.f[3].y, x.f[3].z, x.f[3].w};
 #pragma unroll
         for (int t = 0; t < 16; ++t) facc = __builtin_fmaf(y[t], code_f(w, t), facc);
       } else {
-        const int8_t* ql = Q + ai * 16 * LQ + j * LQ + 16 * m;
-        const uint4 h = *reinterpret_cast<const uint4*>(ql);
         const uint32_t w0 = w4_i8(w, 0), w1 = w4_i8(w, 1), w2 = w4_i8(w, 2), w3 = w4_i8(w, 3);
-        hacc = dot4(w3, h.w, dot4(w2, h.z, dot4(w1, h.y, dot4(w0, h.x, hacc))));
-        if (MODE == kFixed) {
-          const uint4 l = *reinterpret_cast<const uint4*>(ql + 8 * LQ);
-          lacc = dot4(w3, l.w, dot4(w2, l.z, dot4(w1, l.y, dot4(w0, l.x, lacc))));
-        }
+        hacc = dot4(w3, x.h.w, dot4(w2, x.h.z, dot4(w1, x.h.y, dot4(w0, x.h.x, hacc))));
+        if (MODE == kFixed) lacc = dot4(w3, x.l.w, dot4(w2, x.l.z, dot4(w1, x.l.y, dot4(w0, x.l.x, lacc))));
       }
     };
+    if (G > 0) {  // words in LDS: 4 at a time, all their reads issued before the chain
+      const uint32_t* wl = WX + (mi * G + gi) * Wc * 128 + lt;
+      int m = 0;
+      for (; m + 4 <= Wc; m += 4) {
+        const uint32_t w0 = wl[m * 128], w1 = wl[(m + 1) * 128], w2 = wl[(m + 2) * 128], w3 = wl[(m + 3) * 128];
+        const Act x0 = act_of(m), x1 = act_of(m + 1), x2 = act_of(m + 2), x3 = act_of(m + 3);
+        word_of(w0, x0);
+        word_of(w1, x1);
+        word_of(w2, x2);
+        word_of(w3, x3);
+      }
+      for (; m < Wc; ++m) word_of(wl[m * 128], act_of(m));
+    } else {  // LDS too small for the words: read them from global memory, 8 at a time
+      const uint32_t* slab = pk + static_cast<size_t>(og + mrow) * Wc * 128 + lt;
+      constexpr int U = 8;
+      for (int m0 = 0; m0 < Wc; m0 += U) {
+        uint32_t w[U];
 #pragma unroll
-    for (int u = 0; u < kPF; ++u)
-      if (u < Wc) word(wpf[u], u);
-    constexpr int U = 8;
-    for (int m0 = kPF; m0 < Wc; m0 += U) {
-      uint32_t w[U];
+        for (int u = 0; u < U; ++u) w[u] = (m0 + u < Wc) ? slab[static_cast<size_t>(m0 + u) * 128] : 0u;
 #pragma unroll
-      for (int u = 0; u < U; ++u) w[u] = (m0 + u < Wc) ? slab[static_cast<size_t>(m0 + u) * 128] : 0u;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (m0 + u < Wc) word(w[u], m0 + u);
+        for (int u = 0; u < U; ++u)
+          if (m0 + u < Wc) word_of(w[u], act_of(m0 + u));
+      }
     }
 
     // reduce the 8 chains, add the tail, scale
@@ -336,20 +401,20 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
       if (j == 0 && o < nout) {
         const float* yt = Y + ai * WL + 8 * LS;
         for (int t = 0; t < nt; ++t) {
-          const int8_t wt = P.tail[oo * 8 + t];
+          const int8_t wt = ptail[oo * 8 + t];
           if (wt > 0) s += yt[t];
           else if (wt < 0) s -= yt[t];
         }
       }
-      val = s * P.inv_scale_w;
+      val = s * pinv;
     } else {
       int32_t s = isum8_lanes(hacc);
       if (MODE == kFixed) s = s * 256 + isum8_lanes(lacc);
       if (j == 0 && o < nout) {
-        if (MODE == kFixed) s += 128 * P.rowsum[oo];
-        for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(P.tail[oo * 8 + t]) * CT[ai * 8 + t];
-        val = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[KIND == kIFG ? mi : 0]
-                               : static_cast<float>(s) / (P.scale_w * SA[ai]);
+        if (MODE == kFixed) s += 128 * prowsum[oo];
+        for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[oo * 8 + t]) * CT[ai * 8 + t];
+        val = (MODE == kFixed) ? static_cast<float>(s) * invfx
+                               : static_cast<float>(s) / (pscale * SA[ai]);
       }
     }
     float v1 = 0.0f, v2 = 0.0f;
@@ -365,30 +430,32 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     // ---- epilogues -------------------------------------------------------------------
     const int p = (og == static_cast<int>(blockIdx.x))
                       ? po
-                      : ((o < a.oK8) ? (o & 7) * a.oLc + (o >> 3) : 8 * a.oLc + (o - a.oK8));
+                      : ((o < aoK8) ? (o & 7) * aoLc + (o >> 3) : 8 * aoLc + (o - aoK8));
     if (KIND == kIFG) {
-      const bool tl = o >= (a.H & ~7);  // sigmoid / swiglu over T*H = H elements
+      const bool tl = o >= (aH & ~7);  // sigmoid / swiglu over T*H = H elements
       float f = sigmoid_of(v1, tl);
-      if (a.lb) f = __builtin_fmaf(1.0f - e_lb, f, e_lb);
+      if (alb) f = __builtin_fmaf(1.0f - e_lb, f, e_lb);
       const float in = swiglu_of(val, 1.0f - f, tl);
       const float s = __builtin_fmaf(f, e_st, in);
-      a.state[o] = s;
-      a.recur[p] = s;
-      a.gout[p] = v2;
-      if (a.out) a.out[p] = src[0][p];  // layer 0: the embedding row becomes h
+      astate[o] = s;
+      // silu of the recurrence output, the gate of the next kO's g_norm (one SIMD call of
+      // H elements, rmsnorm_swishgate.cpp:24: the same tail rule as above)
+      arecur[p] = silu_of(s, tl);
+      agout[p] = v2;
+      if (aout) aout[p] = src[0][p];  // layer 0: the embedding row becomes h
     } else if (KIND == kO || KIND == kDown) {
-      a.out[p] = e_hin + val;
+      aout[p] = e_hin + val;
     } else if (KIND == kGate) {
-      a.out[p] = swiglu_of(val, v1, o >= (nout & ~7));
+      aout[p] = swiglu_of(val, v1, o >= (nout & ~7));
     } else {  // kLM
-      if (a.out) a.out[o] = val;
+      if (aout) aout[o] = val;
       const unsigned long long kk = amax_key(val, o);
       best = kk > best ? kk : best;
     }
   }
 
   MMF_MARK(KIND, 6);
-  if (KIND == kLM && a.keys) {  // one partial key per block, reduced by the consumer
+  if (KIND == kLM && akeys) {  // one partial key per block, reduced by the consumer
     for (int off = 32; off > 0; off >>= 1) {
       const unsigned long long other = __shfl_xor(best, off);
       best = other > best ? other : best;
@@ -396,7 +463,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     unsigned long long* r64 = reinterpret_cast<unsigned long long*>(red);
     if ((tid & 63) == 0) r64[tid >> 6] = best;
     __syncthreads();
-    if (tid == 0) a.keys[blockIdx.x] = r64[0] > r64[1] ? r64[0] : r64[1];
+    if (tid == 0) akeys[blockIdx.x] = r64[0] > r64[1] ? r64[0] : r64[1];
   }
   MMF_MARK(KIND, 7);
   MMF_SPAN(KIND, false);
@@ -425,12 +492,23 @@ hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
   const int nout = (kind == kGate) ? g.N / 2 : g.N;
   int grid = (nout + kGroup - 1) / kGroup;
   if (kind == kLM && grid > kLMBlocks) grid = kLMBlocks;
+  // all weight words of the block's output groups go to LDS at entry when they fit (the
+  // lm_head's blocks stride over several groups)
+  DecArgs b = a;
+  b.wgroups = 0;
+  const int nm = kind == kIFG ? 3 : (kind == kGate ? 2 : 1);
+  const int G = (kind == kLM) ? (((nout + kGroup - 1) / kGroup) + grid - 1) / grid : 1;
+  const size_t wx = static_cast<size_t>(nm) * G * g.Wc * 128 * sizeof(uint32_t);
+  if (lds + wx <= static_cast<size_t>(lds_limit())) {
+    b.wgroups = G;
+    lds += wx;
+  }
   switch (kind) {
-    case kIFG: return dec_kind<MODE, kIFG>(a, lds, grid, s);
-    case kO: return dec_kind<MODE, kO>(a, lds, grid, s);
-    case kGate: return dec_kind<MODE, kGate>(a, lds, grid, s);
-    case kDown: return dec_kind<MODE, kDown>(a, lds, grid, s);
-    default: return dec_kind<MODE, kLM>(a, lds, grid, s);
+    case kIFG: return dec_kind<MODE, kIFG>(b, lds, grid, s);
+    case kO: return dec_kind<MODE, kO>(b, lds, grid, s);
+    case kGate: return dec_kind<MODE, kGate>(b, lds, grid, s);
+    case kDown: return dec_kind<MODE, kDown>(b, lds, grid, s);
+    default: return dec_kind<MODE, kLM>(b, lds, grid, s);
   }
 }
 

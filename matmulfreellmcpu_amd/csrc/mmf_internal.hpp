@@ -70,13 +70,13 @@ struct DecArgs {
   const float* x;         // input vector; nullptr for layer 0 (embedding row of *key,
                           // a cleared key or one outside [0, vocab) reads row 0)
   const float* embT;      // chain-transposed embedding rows [V][8*Lc_H + 8]
-  const float* x2;        // kO: recurrence output (silu-gated)
+  const float* x2;        // kO: silu of the recurrence output (written by kIFG)
   const float* pre_w;     // stage-1 norm weight (attn / g / mlp / final norm), or nullptr
   const float* lb;        // lower bound row of this layer (kIFG; natural order), or nullptr
   const float* hin;       // kO: layer input h; kDown: resid
   int oLc, oK8;           // chain geometry of the output vector
   float* state;           // kIFG: this layer's recurrent state [H] (natural order)
-  float* recur;           // kIFG out
+  float* recur;           // kIFG out: silu(recurrence output)
   float* gout;            // kIFG out
   float* out;             // kIFG layer 0: copy of the embedding row (h); kO: resid;
                           // kGate: z; kDown: next h; kLM: logits (natural, may be null)
@@ -85,7 +85,12 @@ struct DecArgs {
   int64_t* hist;          // kIFG layer 0: token history, hist[*hist_pos]++ (below hist_cap)
   int32_t* hist_pos;
   int hist_cap;
+  int wgroups;            // set by launch_decode: output groups per block whose weight words
+                          // are copied into LDS at entry (0: read from global in the GEMV)
 };
+
+// Bytes of dynamic LDS one block may allocate on the current device.
+int lds_limit();
 
 constexpr int kLMBlocks = 512;  // lm_head grid (grid-stride over the vocabulary)
 hipError_t launch_decode(DecKind kind, Mode mode, const DecArgs& a, hipStream_t s);

@@ -345,17 +345,6 @@ constexpr int ring_bytes(int S) {
 }
 
 // The device's LDS limit per block (160 KB on gfx950).
-int lds_limit() {
-  static int v = [] {
-    int dev = 0, lim = 65536;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-      lim = 65536;
-    return lim;
-  }();
-  return v;
-}
-
 template <int WM, int WN>
 int tiles_of(const GemmArgs& a) {
   const int ng32 = (a.p[0].g.N + 31) / 32;
@@ -428,6 +417,17 @@ hipError_t mfma_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
 }
 
 }  // namespace
+
+int lds_limit() {
+  static int v = [] {
+    int dev = 0, lim = 65536;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      lim = 65536;
+    return lim;
+  }();
+  return v;
+}
 
 size_t pkm_words(const Geom& g) { return static_cast<size_t>((g.N + 31) / 32) * 16 * g.Lc; }
 
