@@ -18,9 +18,10 @@ same blob and prompt; its greedy id stream is also compared with the GPU's.
 Beside the headline (all on seeded synthetic weights of the named shapes):
   op_sweep  BitLinear with int8-absmax activations: x ~N(0,1) [M, K], M in {1, 16, 256,
             2048}, (K, N) in {(1024,1024), (1024,5632), (2816,1024), (2048,11264),
-            (5632,2048)}; microseconds per call (RMSNorm + quantisation + ternary GEMM),
-            algorithmic bytes N*K/4 + 4MK + 4MN + 4K against 8 TB/s, ops 2MNK against
-            the 5.0 POP/s int8 peak.
+            (5632,2048)}; microseconds per call (RMSNorm + quantisation + ternary GEMM)
+            with 20 calls back to back in one HIP graph (prologue_us / gemm_us: event
+            pair around each launch), algorithmic bytes N*K/4 + 4MK + 4MN + 4K against
+            8 TB/s, ops 2MNK against the 5.0 POP/s int8 peak.
   prefill   1.3B shape, 2048-token prompt, time to the first token (all layers + final
             norm, lm_head, argmax) per mode; per-GEMM microseconds and TOP/s (event pair
             around every launch); FixedQ510 runs two int8 passes (hi/lo code planes).
@@ -118,11 +119,12 @@ def measure_op_sweep(reps):
         for M in SWEEP_M:
             x = rng.standard_normal((M, K)).astype(np.float32)
             dx, do = dev(x.nbytes, x), dev(M * N * 4)
-            total, _, gemm = e.time_bitlinear(pid, dx, do, M, mode=INT8_ABSMAX, warmup=3, reps=reps)
+            total, pro, gemm = e.time_bitlinear(pid, dx, do, M, mode=INT8_ABSMAX, warmup=3, reps=reps)
             nbytes = N * K / 4 + 4 * M * K + 4 * M * N + 4 * K
             ops = 2.0 * M * N * K
             bound = "mfma" if ops / nbytes > INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
-            out.append({"M": M, "K": K, "N": N, "us": round(total, 2), "GBps": round(nbytes / total / 1e3, 1),
+            out.append({"M": M, "K": K, "N": N, "us": round(total, 2), "prologue_us": round(pro, 2),
+                        "gemm_us": round(gemm, 2), "GBps": round(nbytes / total / 1e3, 1),
                         "hbm_frac": round(nbytes / total / 1e3 / HBM_PEAK_GBS, 4),
                         "TOPS": round(ops / total / 1e6, 2), "mfma_frac": round(ops / total / 1e6 / INT8_PEAK_TOPS, 4),
                         "bound": bound})

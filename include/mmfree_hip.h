@@ -174,8 +174,10 @@ int mmf_model_time_decode(mmf_ctx* ctx, int warmup, int reps, double* step_us, d
 int mmf_model_time_prefill(mmf_ctx* ctx, const int64_t* ids, size_t T, int warmup, int reps,
                            double* total_us, double* kind_us);
 
-/* Timing of mmf_bitlinear on device buffers (same arguments): average microseconds per call,
- * and of its two launches (prologue: RMSNorm + activation codes; GEMM). Measurement only. */
+/* Timing of mmf_bitlinear on device buffers (same arguments): average microseconds per call
+ * with `reps` calls back to back in one HIP graph (device time; launched one by one when
+ * MMF_GRAPH=0), and of its two launches (prologue: RMSNorm + activation codes; GEMM) from an
+ * event pair around each launch. Measurement only. */
 int mmf_time_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps, const float* x,
                        float* out, size_t rows, int warmup, int reps, double* total_us,
                        double* prologue_us, double* gemm_us);

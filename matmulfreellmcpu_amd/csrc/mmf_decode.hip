@@ -45,10 +45,6 @@ namespace mmf {
 
 namespace {
 
-// Makes the listed uniform values live in scalar registers at this point (no instruction is
-// emitted; the loads that produce them must complete before it).
-#define MMF_PIN(...) asm volatile("" ::__VA_ARGS__)
-
 template <int KIND> struct KindTraits;
 // NM matrices (one wave pair each), NA activation vectors, NP prologue source vectors
 template <> struct KindTraits<kIFG> { static constexpr int NM = 3, NA = 3, NP = 5; };

@@ -14,6 +14,12 @@
 
 namespace mmf {
 
+// Makes the listed uniform values (kernel arguments) live in scalar registers at this point:
+// their scalar loads issue together before it, instead of one dependent load at each use,
+// which the compiler otherwise repeats inside loops that store to global memory. No
+// instruction is emitted.
+#define MMF_PIN(...) asm volatile("" ::__VA_ARGS__)
+
 // ---- packed ternary weights --------------------------------------------------------
 // A 32-bit word holds 16 two-bit two's-complement codes (00 = 0, 01 = +1, 11 = -1). Code
 // t (0..15) sits at bit 8*(t%4) + 2*(t/4), so (word >> 2i) & 0x03030303 puts the codes

@@ -892,6 +892,34 @@ double time_runs(mmf_ctx* c, int warmup, int reps, F&& f) {
   MMF_HIP(err);
   return 1000.0 * ms / reps;
 }
+
+// Average microseconds per run of f() when `reps` runs are captured back to back in one
+// HIP graph (device time without the host's per-launch cost); time_runs() if graphs are
+// off or the capture fails. f() must allocate nothing once it has run (warmup >= 1).
+template <class F>
+double time_graph_runs(mmf_ctx* c, int warmup, int reps, F&& f) {
+  if (warmup < 1) warmup = 1;
+  for (int i = 0; i < warmup; ++i) f();
+  hipGraphExec_t ge = graphs_enabled() ? capture_graph(c, [&] {
+    for (int i = 0; i < reps; ++i) f();
+  }) : nullptr;
+  if (!ge) return time_runs(c, 0, reps, f);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0.0f;
+  hipError_t err = hipGraphLaunch(ge, c->stream);  // first replay uploads the graph
+  if (err == hipSuccess) err = hipEventCreate(&e0);
+  if (err == hipSuccess) err = hipEventCreate(&e1);
+  if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+  if (err == hipSuccess) err = hipGraphLaunch(ge, c->stream);
+  if (err == hipSuccess) err = hipEventRecord(e1, c->stream);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipGraphExecDestroy(ge);
+  MMF_HIP(err);
+  return 1000.0 * ms / reps;
+}
 }  // extern "C++"
 
 int mmf_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out, size_t rows,
@@ -1357,7 +1385,7 @@ int mmf_time_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const 
   return guard(c, [&] {
     if (reps < 1 || warmup < 0 || rows == 0) fail(MMF_ERR_ARG, "invalid reps/rows");
     auto f = [&] { bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, nullptr); };
-    const double t = time_runs(c, warmup, reps, f);
+    const double t = time_graph_runs(c, warmup, reps, f);
     if (total_us) *total_us = t;
     if (prologue_us || gemm_us) {
       double k[kRkCount];

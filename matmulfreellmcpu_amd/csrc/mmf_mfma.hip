@@ -108,7 +108,8 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   constexpr int DB = BG * 2 / NW;               // B transfers per wave per stage
   static_assert(DA * NW == P * FR * 2 && DB * NW == BG * 2, "transfers must split evenly over the waves");
   constexpr int D = DA + DB;
-  extern __shared__ __align__(16) unsigned char lds[];  // [S][SS]
+  extern __shared__ __align__(16) unsigned char lds[];  // [S][SS] ring, then srow[BM]
+  float* srow = reinterpret_cast<float*>(lds + S * SS);  // Int8: the block's activation scales
 
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
@@ -152,6 +153,35 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
     cg = cg < ng32 ? cg : ng32 - 1;
     bsrc[i] = W.pkm + (static_cast<size_t>(cg) * (Lc / 4) + (f & 1)) * 64 + lane;
   }
+
+  // epilogue operands that do not depend on the accumulators, fetched before the main loop
+  // so their latency hides behind it: per-row int8 scales into LDS (DMA, one per lane),
+  // per-column Q5.10 offsets (128 * rowsum) into registers
+  if (MODE == kInt8 && wave * 64 < BM) {
+    int row = row0 + wave * 64 + lane;
+    row = row < act.rows ? row : act.rows - 1;
+    __builtin_amdgcn_global_load_lds(act.sa + static_cast<size_t>(am) * act.rows + row, (lds_void*)(srow + wave * 64),
+                                     4, 0, 0);
+  }
+  const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
+  const int ol = lane & 31;
+  int col[2];
+  int32_t csum[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int cg = cgb + wn * 2 + (EPI == kEpiSwigluPair ? 0 : b);
+    col[b] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + (b ? Nout : 0) : cg * 32 + ol;
+    csum[b] = (MODE == kFixed && ksp == 1 && col[b] < N) ? 128 * W.rowsum[col[b]] : 0;
+  }
+  float* const outz = a.out[EPI == kEpiSwigluPair ? 0 : z];
+  int32_t* const accz = a.acc[z];
+  int32_t* const wsp = a.ws;
+  const float* const addp = a.add;
+  const int8_t* const tailp = W.tail;
+  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = W.g.ntail;
+  const float invf = a.inv_fixed[z], scw = W.scale_w;
+  MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rawacc), "s"(swn), "s"(ntail), "s"(invf),
+          "s"(scw));
 
   v16i acc[P][2][2];
 #pragma unroll
@@ -197,7 +227,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 
   if (ksp > 1) {
     // split-K: exact partial sums of this stage range, logical column order
-    int32_t* wp = a.ws + (static_cast<size_t>(ks) * a.nmat + z) * act.rows * static_cast<size_t>(N);
+    int32_t* wp = wsp + (static_cast<size_t>(ks) * a.nmat + z) * act.rows * static_cast<size_t>(N);
     const int Nh = N / 2;
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj) {
@@ -217,39 +247,63 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
     return;
   }
 
-  // epilogue: exact integer totals, dequantisation, output stage. Per-column terms (the
-  // Q5.10 offset 128 * rowsum, tail weights) are loaded once per lane, per-row terms once
-  // per row, and the residual rows of a fragment in one batch before any store.
-  const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
-  const int ntail = W.g.ntail;
-  const int ol = lane & 31;
-  int col[2];
-  int32_t csum[2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int cg = cgb + wn * 2 + (EPI == kEpiSwigluPair ? 0 : b);
-    col[b] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + (b ? Nout : 0) : cg * 32 + ol;
-    csum[b] = (MODE == kFixed && col[b] < N) ? 128 * W.rowsum[col[b]] : 0;
-  }
+  // epilogue: exact integer totals, dequantisation, output stage. The residual rows of
+  // both fragments are loaded in one batch before any store.
   // stored columns of this lane: fragment b (non-pair) or the pair's gate column
   constexpr int NB = (EPI == kEpiSwigluPair) ? 1 : 2;
   bool cok[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) cok[b] = col[b] < Nout;
+  float addv[2][16][NB];
+  if (EPI == kEpiAdd) {
+#pragma unroll
+    for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int row = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5) + 8 * (i >> 2) + (i & 3);
+        row = row < act.rows ? row : act.rows - 1;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) addv[ai][i][b] = cok[b] ? addp[static_cast<size_t>(row) * N + col[b]] : 0.0f;
+      }
+  }
+  // Whole tile in range, no tail weights, no integer accumulator output, below the swiglu
+  // tail rule: one straight store per output with no per-element tests (the general path
+  // below measured several times slower per tile).
+  const bool fast = row0 + BM <= act.rows && (cgb + BG) * 32 <= N && !accz && !rawacc && ntail == 0 &&
+                    (EPI != kEpiSwigluPair || static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
+  if (fast) {
+#pragma unroll
+    for (int ai = 0; ai < 2; ++ai) {
+      const int rbase = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = rbase + 8 * (i >> 2) + (i & 3);
+        const size_t grow = static_cast<size_t>(r);
+        const float den = (MODE == kInt8) ? scw * srow[r - row0] : 1.0f;
+        float val[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int32_t s = (MODE == kFixed) ? acc[0][ai][b][i] * 256 + acc[P - 1][ai][b][i] + csum[b] : acc[0][ai][b][i];
+          val[b] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den;
+        }
+        if (EPI == kEpiSwigluPair) {
+          outz[grow * Nout + col[0]] = swiglu_of(val[0], val[1], false);
+        } else {
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+            outz[grow * N + col[b]] = (EPI == kEpiAdd) ? addv[ai][i][b] + val[b] : val[b];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ai = 0; ai < 2; ++ai) {
     const int rbase = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5);
-    float addv[16][NB];
     float den[16];
+    if (MODE == kInt8) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      int row = rbase + 8 * (i >> 2) + (i & 3);
-      row = row < act.rows ? row : act.rows - 1;
-      if (MODE == kInt8) den[i] = W.scale_w * act.sa[static_cast<size_t>(am) * act.rows + row];
-      if (EPI == kEpiAdd) {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) addv[i][b] = cok[b] ? a.add[static_cast<size_t>(row) * N + col[b]] : 0.0f;
-      }
+      for (int i = 0; i < 16; ++i) den[i] = scw * srow[rbase - row0 + 8 * (i >> 2) + (i & 3)];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -263,27 +317,27 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
       for (int b = 0; b < 2; ++b) {
         int32_t s = (MODE == kFixed) ? acc[0][ai][b][i] * 256 + acc[P - 1][ai][b][i] + csum[b] : acc[0][ai][b][i];
         if (ntail && col[b] < N)
-          for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(W.tail[col[b] * 8 + t]) * ct[t];
+          for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(tailp[col[b] * 8 + t]) * ct[t];
         tot[b] = s;
-        val[b] = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[z] : static_cast<float>(s) / den[i];
+        val[b] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den[i];
       }
       if (EPI == kEpiSwigluPair) {
         if (!cok[0]) continue;
-        if (a.acc[z]) {
-          a.acc[z][grow * N + col[0]] = tot[0];
-          a.acc[z][grow * N + col[1]] = tot[1];
+        if (accz) {
+          accz[grow * N + col[0]] = tot[0];
+          accz[grow * N + col[1]] = tot[1];
         }
-        if (a.raw_acc) continue;
+        if (rawacc) continue;
         const size_t e = grow * Nout + col[0];
-        a.out[0][e] = swiglu_of(val[0], val[1], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+        outz[e] = swiglu_of(val[0], val[1], static_cast<int64_t>(e) >= (swn & ~7));
       } else {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           if (!cok[b]) continue;
           const size_t e = grow * N + col[b];
-          if (a.acc[z]) a.acc[z][e] = tot[b];
-          if (a.raw_acc) continue;
-          a.out[z][e] = (EPI == kEpiAdd) ? addv[i][b] + val[b] : val[b];
+          if (accz) accz[e] = tot[b];
+          if (rawacc) continue;
+          outz[e] = (EPI == kEpiAdd) ? addv[ai][i][b] + val[b] : val[b];
         }
       }
     }
@@ -303,6 +357,16 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   const size_t plane = static_cast<size_t>(act.rows) * N;  // one split of one matrix
   const int am = (act.na > 1) ? z : 0;
   constexpr int NM = (EPI == kEpiSwigluPair) ? 2 : 1;
+  float* const outz = a.out[EPI == kEpiSwigluPair ? 0 : z];
+  int32_t* const accz = a.acc[z];
+  const int32_t* const wsp = a.ws;
+  const float* const addp = a.add;
+  const int8_t* const tailp = W.tail;
+  const int32_t* const rsum = W.rowsum;
+  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = W.g.ntail, ksplit = a.ksplit, nmat = a.nmat;
+  const float invf = a.inv_fixed[z], scw = W.scale_w;
+  MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rsum), "s"(rawacc), "s"(swn), "s"(ntail),
+          "s"(ksplit), "s"(nmat), "s"(invf), "s"(scw));
   for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
        e += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const int row = static_cast<int>(e / Nout), o0 = static_cast<int>(e % Nout);
@@ -313,35 +377,34 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
     for (int mi = 0; mi < NM; ++mi) {
       const int o = o0 + (mi ? Nout : 0);
       int32_t s = 0;
-      for (int ks = 0; ks < a.ksplit; ++ks)
-        s += a.ws[(static_cast<size_t>(ks) * a.nmat + z) * plane + static_cast<size_t>(row) * N + o];
-      if (MODE == kFixed) s += 128 * W.rowsum[o];
+      for (int ks = 0; ks < ksplit; ++ks)
+        s += wsp[(static_cast<size_t>(ks) * nmat + z) * plane + static_cast<size_t>(row) * N + o];
+      if (MODE == kFixed) s += 128 * rsum[o];
       const int32_t* ct = act.ct + ar * 8;
-      for (int t = 0; t < W.g.ntail; ++t) s += static_cast<int32_t>(W.tail[o * 8 + t]) * ct[t];
+      for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(tailp[o * 8 + t]) * ct[t];
       tot[mi] = s;
-      val[mi] = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[z]
-                                 : static_cast<float>(s) / (W.scale_w * act.sa[ar]);
+      val[mi] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / (scw * act.sa[ar]);
     }
     const size_t grow = static_cast<size_t>(row);
-    if (a.acc[z]) {
+    if (accz) {
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi) a.acc[z][grow * N + o0 + (mi ? Nout : 0)] = tot[mi];
+      for (int mi = 0; mi < NM; ++mi) accz[grow * N + o0 + (mi ? Nout : 0)] = tot[mi];
     }
-    if (a.raw_acc) continue;
+    if (rawacc) continue;
     if (EPI == kEpiSwigluPair) {
-      a.out[0][e] = swiglu_of(val[0], val[NM - 1], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+      outz[e] = swiglu_of(val[0], val[NM - 1], static_cast<int64_t>(e) >= (swn & ~7));
     } else if (EPI == kEpiAdd) {
-      a.out[z][e] = a.add[e] + val[0];
+      outz[e] = addp[e] + val[0];
     } else {
-      a.out[z][e] = val[0];
+      outz[e] = val[0];
     }
   }
 }
 
-// LDS bytes of a ring of S stages.
+// LDS bytes of a ring of S stages plus the block's row scales.
 template <int MODE, int WM, int WN>
 constexpr int ring_bytes(int S) {
-  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * 2 * 1024 + 2 * WN * 2 * 256);
+  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * 2 * 1024 + 2 * WN * 2 * 256) + 64 * WM * 4;
 }
 
 // The device's LDS limit per block (160 KB on gfx950).
