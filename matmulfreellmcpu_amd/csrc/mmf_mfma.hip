@@ -81,32 +81,32 @@ __device__ __forceinline__ void wait_vm() {
 // s_waitcnt lgkmcnt(0): this wave's LDS reads have returned.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// DMA of one 64-position stage into a ring slot: this wave's A fragments (16 bytes per
-// lane) and B fragments (one word per lane). (A plain function: a lambda holding these
+// DMA of one stage of 32*KQ positions into a ring slot: this wave's A fragments (16 bytes
+// per lane) and B fragments (one word per lane). (A plain function: a lambda holding these
 // builtins keeps the kernel's host stub from being emitted.)
-template <int DA, int DB, int SA>
+template <int DA, int DB, int SA, int KQ>
 __device__ __forceinline__ void issue_stage(const int8_t* const* asrc, const uint32_t* const* bsrc,
                                             unsigned char* sb, int st, int wave) {
 #pragma unroll
   for (int i = 0; i < DA; ++i)
-    __builtin_amdgcn_global_load_lds(asrc[i] + st * 64, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(asrc[i] + st * 32 * KQ, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
 #pragma unroll
   for (int i = 0; i < DB; ++i)
-    __builtin_amdgcn_global_load_lds(bsrc[i] + st * 128, (lds_void*)(sb + SA + (wave * DB + i) * 256), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(bsrc[i] + st * 64 * KQ, (lds_void*)(sb + SA + (wave * DB + i) * 256), 4, 0, 0);
 }
 
-template <int MODE, int EPI, int WM, int WN, int S>
+template <int MODE, int EPI, int WM, int WN, int S, int KQ>
 __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
   constexpr int NW = WM * WN;                   // waves per block
   constexpr int BM = 64 * WM;                   // rows per block
   constexpr int BG = 2 * WN;                    // physical 32-column groups per block
   constexpr int FR = BM / 32;                   // 32-row fragments
-  constexpr int SA = P * FR * 2 * 1024;         // A bytes per stage: [plane][frag][k-half]
-  constexpr int SS = SA + BG * 2 * 256;         // stage bytes (A, then B: [group][k-half])
-  constexpr int DA = P * FR * 2 / NW;           // A transfers per wave per stage
-  constexpr int DB = BG * 2 / NW;               // B transfers per wave per stage
-  static_assert(DA * NW == P * FR * 2 && DB * NW == BG * 2, "transfers must split evenly over the waves");
+  constexpr int SA = P * FR * KQ * 1024;        // A bytes per stage: [plane][frag][k-chunk]
+  constexpr int SS = SA + BG * KQ * 256;        // stage bytes (A, then B: [group][k-chunk])
+  constexpr int DA = P * FR * KQ / NW;          // A transfers per wave per stage
+  constexpr int DB = BG * KQ / NW;              // B transfers per wave per stage
+  static_assert(DA * NW == P * FR * KQ && DB * NW == BG * KQ, "transfers must split evenly over the waves");
   constexpr int D = DA + DB;
   extern __shared__ __align__(16) unsigned char lds[];  // [S][SS] ring, then srow[BM]
   float* srow = reinterpret_cast<float*>(lds + S * SS);  // Int8: the block's activation scales
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int cgb = (tile % nct) * BG;
   const int am = (act.na > 1) ? z : 0;
   // stage range of this block's split (all stages without split-K)
-  const int nall = Lc / 8, ksp = gridDim.y, ks = blockIdx.y;
+  const int nall = Lc / (4 * KQ), ksp = gridDim.y, ks = blockIdx.y;
   const int st0 = static_cast<int>((static_cast<long>(nall) * ks) / ksp);
   const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
   const size_t qstride = act.qstride(), plane = static_cast<size_t>(8 * Lc);
@@ -139,8 +139,8 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int8_t* asrc[DA];
 #pragma unroll
   for (int i = 0; i < DA; ++i) {
-    const int f = wave * DA + i;  // = (plane * FR + frag) * 2 + k-half
-    const int kh = f & 1, pl = (f >> 1) / FR, rf = (f >> 1) % FR;
+    const int f = wave * DA + i;  // = (plane * FR + frag) * KQ + k-chunk
+    const int kh = f % KQ, pl = (f / KQ) / FR, rf = (f / KQ) % FR;
     int row = row0 + rf * 32 + (lane & 31);
     row = row < act.rows ? row : act.rows - 1;
     asrc[i] = qbase + static_cast<size_t>(row) * qstride + pl * plane + kh * 32 + (lane >> 5) * 16;
@@ -148,10 +148,10 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const uint32_t* bsrc[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i) {
-    const int f = wave * DB + i;  // = group * 2 + k-half
-    int cg = cgb + (f >> 1);
+    const int f = wave * DB + i;  // = group * KQ + k-chunk
+    int cg = cgb + f / KQ;
     cg = cg < ng32 ? cg : ng32 - 1;
-    bsrc[i] = W.pkm + (static_cast<size_t>(cg) * (Lc / 4) + (f & 1)) * 64 + lane;
+    bsrc[i] = W.pkm + (static_cast<size_t>(cg) * (Lc / 4) + f % KQ) * 64 + lane;
   }
 
   // epilogue operands that do not depend on the accumulators, fetched before the main loop
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
-    if (st < nst) issue_stage<DA, DB, SA>(asrc, bsrc, lds + st * SS, st0 + st, wave);
+    if (st < nst) issue_stage<DA, DB, SA, KQ>(asrc, bsrc, lds + st * SS, st0 + st, wave);
   for (int st = 0; st < nst; ++st) {
     // this wave's transfers of stage st are complete once at most the later stages'
     // transfers are outstanding
@@ -203,24 +203,37 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // every wave has finished stage st - 1: its slot takes stage st + S - 1
     if (st + S - 1 < nst)
-      issue_stage<DA, DB, SA>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st0 + st + S - 1, wave);
+      issue_stage<DA, DB, SA, KQ>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st0 + st + S - 1, wave);
     const unsigned char* sb = lds + (st % S) * SS;
+    // all LDS reads of the stage first, then the matrix-core work: each read's latency
+    // then overlaps the products of the earlier operands instead of stalling its own
+    uint32_t bw[KQ][2];
+    v4i av[KQ][P][2];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      v4i bop[2];
+    for (int kh = 0; kh < KQ; ++kh)
 #pragma unroll
       for (int bj = 0; bj < 2; ++bj)
-        bop[bj] = expand_w(*reinterpret_cast<const uint32_t*>(sb + SA + ((wn * 2 + bj) * 2 + kh) * 256 + lane * 4));
+        bw[kh][bj] = *reinterpret_cast<const uint32_t*>(sb + SA + ((wn * 2 + bj) * KQ + kh) * 256 + lane * 4);
+#pragma unroll
+    for (int kh = 0; kh < KQ; ++kh)
 #pragma unroll
       for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-        for (int ai = 0; ai < 2; ++ai) {
-          const v4i av =
-              *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * 2 + kh) * 1024 + lane * 16);
+        for (int ai = 0; ai < 2; ++ai)
+          av[kh][pl][ai] = *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * KQ + kh) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kh = 0; kh < KQ; ++kh) {
+      v4i bop[2];
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj) bop[bj] = expand_w(bw[kh][bj]);
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+        for (int ai = 0; ai < 2; ++ai)
 #pragma unroll
           for (int bj = 0; bj < 2; ++bj)
-            acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bop[bj], acc[pl][ai][bj], 0, 0, 0);
-        }
+            acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[kh][pl][ai], bop[bj], acc[pl][ai][bj], 0, 0, 0);
     }
     wait_lds();
   }
@@ -402,9 +415,9 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
 }
 
 // LDS bytes of a ring of S stages plus the block's row scales.
-template <int MODE, int WM, int WN>
+template <int MODE, int WM, int WN, int KQ>
 constexpr int ring_bytes(int S) {
-  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * 2 * 1024 + 2 * WN * 2 * 256) + 64 * WM * 4;
+  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
 }
 
 // The device's LDS limit per block (160 KB on gfx950).
@@ -419,6 +432,17 @@ int tiles_of(const GemmArgs& a) {
 // With a 64 KB LDS limit the ring falls back to 3 stages.
 template <int WM, int WN>
 constexpr int ring_stages() { return 4; }
+// 32-position k-chunks per stage (one barrier per stage)
+template <int WM, int WN>
+constexpr int ring_kq() { return 2; }
+
+template <int MODE, int EPI, int WM, int WN, int S, int KQ>
+bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
+  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ>(S);
+  if (bytes > lds_limit()) return false;
+  k_mfma<MODE, EPI, WM, WN, S, KQ><<<grid, dim3(64 * WM * WN), bytes, s>>>(a, act);
+  return true;
+}
 
 // Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
 // that still gives every CU a block (all blocks of all matrices), else 128. Then K is
@@ -441,15 +465,12 @@ Plan plan_of(const GemmArgs& a) {
 
 template <int MODE, int EPI, int WM, int WN>
 hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream_t s) {
-  constexpr int S = ring_stages<WM, WN>();
   const int ntile = tiles_of<WM, WN>(a);
   const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
   dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
-  const dim3 block(64 * WM * WN);
-  if (ring_bytes<MODE, WM, WN>(S) <= lds_limit())
-    k_mfma<MODE, EPI, WM, WN, S><<<grid, block, ring_bytes<MODE, WM, WN>(S), s>>>(a, act);
-  else
-    k_mfma<MODE, EPI, WM, WN, 3><<<grid, block, ring_bytes<MODE, WM, WN>(3), s>>>(a, act);
+  if (!mfma_launch<MODE, EPI, WM, WN, ring_stages<WM, WN>(), ring_kq<WM, WN>()>(a, act, grid, s) &&
+      !mfma_launch<MODE, EPI, WM, WN, 3, 2>(a, act, grid, s))
+    return hipErrorInvalidConfiguration;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ksplit == 1) return e;
   GemmArgs b = a;
