@@ -171,7 +171,7 @@ def measure_serve(blob_dir, preset, B, T, mode_name, steps):
     prompts = rng.integers(3, 32000, (B, T))
     e.reset(B)
     t0 = time.perf_counter()
-    cur = np.array([e.prefill(b, prompts[b]) for b in range(B)], np.int64)
+    cur = e.prefill_streams(prompts)
     t_pre = time.perf_counter() - t0
     for _ in range(2):
         cur = e.step(cur)

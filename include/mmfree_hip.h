@@ -143,6 +143,13 @@ int mmf_model_reset(mmf_ctx* ctx, size_t streams);
 int mmf_model_prefill(mmf_ctx* ctx, size_t stream, const int64_t* ids, size_t n, float* logits,
                       int64_t* argmax);
 int mmf_model_step(mmf_ctx* ctx, const int64_t* tokens, float* logits, int64_t* argmax);
+/* The prompts of streams 0..n-1 (n <= the mmf_model_reset count), concatenated in ids with
+ * lens[b] ids each, prefilled together: the same states, logits [n, V] and argmax [n] as n
+ * mmf_model_prefill calls in stream order (the reference prefills stream by stream in
+ * generate_serve, hgrn_model.cpp:412-428). The prompts run as one stack of rows through
+ * every BitLinear, the recurrence scans each stream's rows from its own state. */
+int mmf_model_prefill_streams(mmf_ctx* ctx, size_t n, const int64_t* ids, const size_t* lens,
+                              float* logits, int64_t* argmax);
 /* Recurrent state [L][B][H] after the last generate / prefill / step (host out). */
 int mmf_model_state(mmf_ctx* ctx, float* out);
 

@@ -75,6 +75,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_model_generate": (i, [_vp, _i64p, _sz, _sz, C.c_int64, _i64p, _sz, C.POINTER(_sz), TOKEN_CB, _vp]),
         "mmf_model_reset": (i, [_vp, _sz]),
         "mmf_model_prefill": (i, [_vp, _sz, _i64p, _sz, _fp, _i64p]),
+        "mmf_model_prefill_streams": (i, [_vp, _sz, _i64p, C.POINTER(C.c_size_t), _fp, _i64p]),
         "mmf_model_step": (i, [_vp, _i64p, _fp, _i64p]),
         "mmf_model_state": (i, [_vp, _fp]),
         "mmf_model_forward": (i, [_vp, _i64p, _sz, _fp]),
@@ -233,6 +234,20 @@ class Engine:
                                              lg.ctypes.data_as(_fp) if lg is not None else None,
                                              am.ctypes.data_as(_i64p)))
         return (int(am[0]), lg) if want_logits else int(am[0])
+
+    def prefill_streams(self, prompts, want_logits=False):
+        """Prefill streams 0..len(prompts)-1 together (mmf_model_prefill_streams): the same
+        first tokens, logits and states as one prefill() per stream in order."""
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int64).ravel() for p in prompts]), np.int64)
+        lens = np.ascontiguousarray([len(p) for p in prompts], np.uint64)
+        n = lens.size
+        lg = np.empty((n, self.cfg.vocab_size), np.float32) if want_logits else None
+        am = np.zeros(n, np.int64)
+        self._chk(self.lib.mmf_model_prefill_streams(self.h, n, ids.ctypes.data_as(_i64p),
+                                                     lens.ctypes.data_as(C.POINTER(C.c_size_t)),
+                                                     lg.ctypes.data_as(_fp) if lg is not None else None,
+                                                     am.ctypes.data_as(_i64p)))
+        return (am, lg) if want_logits else am
 
     def step(self, tokens, want_logits=False):
         t = np.ascontiguousarray(tokens, np.int64)

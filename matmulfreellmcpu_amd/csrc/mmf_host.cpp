@@ -93,6 +93,7 @@ struct LayerDev {
 struct RowScratch {
   DBuf ids, h, resid, i, f, g, recur, scan, z, logits, state0, am;
   DBuf acty, actq, actct, actsa;
+  DBuf segs;  // stacked prompts: nseg + 1 row offsets, then the nseg last-row indices
 };
 
 struct Model {
@@ -330,7 +331,7 @@ void alloc_decode(mmf_ctx* c, Model& m) {
 // layer's state ([H] time scan or [rows, H] streams); internals (may be null): device
 // [5][rows][H] copy targets for the trace.
 void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, bool stream_state,
-                float* trace_dev) {
+                float* trace_dev, const int* segs = nullptr, int nseg = 0) {
   const int H = static_cast<int>(m.cfg.hidden_size), I = static_cast<int>(m.cfg.intermediate_size);
   const Mode mode = static_cast<Mode>(m.mode);
   const LayerDev& L = m.layers[l];
@@ -342,7 +343,8 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
   float* rb = s.recur.as<float>(static_cast<size_t>(rows) * H);
   float* resid = s.resid.as<float>(static_cast<size_t>(rows) * H);
   float* zb = s.z.as<float>(static_cast<size_t>(rows) * I * 2);
-  float* scan = (trace_dev || (!stream_state && rows > 1)) ? s.scan.as<float>(static_cast<size_t>(rows) * H) : nullptr;
+  float* scan = (trace_dev || segs || (!stream_state && rows > 1)) ? s.scan.as<float>(static_cast<size_t>(rows) * H)
+                                                                   : nullptr;
 
   // attention: attn_norm -> i/f/g BitLinears (hgrn_model.cpp:95-107)
   {
@@ -369,7 +371,10 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
   }
   // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
   tbeg(c, kRkMixer);
-  MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, st));
+  if (segs)
+    MMF_HIP(launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H, st));
+  else
+    MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, st));
   tend(c);
   if (trace_dev) {
     const size_t n = static_cast<size_t>(rows) * H * sizeof(float);
@@ -667,6 +672,45 @@ float* prefill_rows(mmf_ctx* c, Model& m, size_t b, const int64_t* ids, size_t T
   if (trace_int || trace_h || trace_state) MMF_HIP(hipStreamSynchronize(c->stream));
   tbuf.release();
   return h;
+}
+
+// Whether the prompts of several streams may be stacked into one row range: every elementwise
+// SIMD call of the reference then covers whole groups of 8 in each stream (T * H and T * I
+// elements), so no element is a tail element and stacking changes no rounding.
+bool stackable(const Model& m) { return m.cfg.hidden_size % 8 == 0 && m.cfg.intermediate_size % 8 == 0; }
+
+// Prefill the prompts of streams 0..n-1 (ids concatenated, lens[b] each) as one stack of
+// rows: the prologues and GEMMs of every layer run over all prompt rows at once and the
+// recurrence scans each stream's segment from its own state. The last row of each stream
+// -> final norm + lm_head -> logits [n, V] (device), as a per-stream prefill computes them.
+float* prefill_stacked(mmf_ctx* c, Model& m, size_t n, const int64_t* ids, const size_t* lens) {
+  const size_t H = m.cfg.hidden_size, L = m.cfg.num_hidden_layers, B = m.streams, V = m.cfg.vocab_size;
+  std::vector<int> seg(2 * n + 1);
+  size_t R = 0;
+  for (size_t b = 0; b < n; ++b) {
+    if (lens[b] == 0) fail(MMF_ERR_ARG, "empty prompt");
+    seg[b] = static_cast<int>(R);
+    R += lens[b];
+    seg[n + 1 + b] = static_cast<int>(R - 1);
+  }
+  if (R * H > static_cast<size_t>(INT32_MAX)) fail(MMF_ERR_ARG, "prompts too long");
+  seg[n] = static_cast<int>(R);
+  check_ids(m, ids, R);
+  RowScratch& s = m.rs;
+  int64_t* dids = s.ids.as<int64_t>(R);
+  int* dseg = s.segs.as<int>(seg.size());
+  MMF_HIP(hipMemcpyAsync(dids, ids, R * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+  MMF_HIP(hipMemcpyAsync(dseg, seg.data(), seg.size() * sizeof(int), hipMemcpyHostToDevice, c->stream));
+  float* h = s.h.as<float>(R * H);
+  MMF_HIP(launch_embed(m.emb, dids, h, static_cast<int>(R), static_cast<int>(H), c->stream));
+  for (size_t l = 0; l < L; ++l)
+    layer_rows(c, m, static_cast<int>(l), static_cast<int>(R), h, static_cast<float*>(m.state.p) + l * B * H, false,
+               nullptr, dseg, static_cast<int>(n));
+  float* last = s.resid.as<float>(n * H);  // free once the layers are done
+  MMF_HIP(launch_gather_rows(h, dseg + n + 1, last, static_cast<int>(n), static_cast<int>(H), c->stream));
+  float* lg = s.logits.as<float>(n * V);
+  lm_rows(c, m, static_cast<int>(n), last, lg);
+  return lg;
 }
 
 // The token of the last lm_head: the max over its per-block argmax keys.
@@ -1215,6 +1259,32 @@ int mmf_model_prefill(mmf_ctx* c, size_t stream, const int64_t* ids, size_t n, f
                             static_cast<int>(m.cfg.hidden_size), m.gH.Lc, c->stream));
     lm_single(c, m, static_cast<float*>(m.h.p), lg, false);
     deliver_rows(c, m, lg, 1, logits, argmax);
+  });
+}
+
+int mmf_model_prefill_streams(mmf_ctx* c, size_t n, const int64_t* ids, const size_t* lens, float* logits,
+                              int64_t* argmax) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (n == 0 || n > m.streams) fail(MMF_ERR_ARG, "stream count beyond mmf_model_reset's count");
+    if (!ids || !lens) fail(MMF_ERR_ARG, "null prompts");
+    const size_t V = m.cfg.vocab_size, H = m.cfg.hidden_size;
+    if (stackable(m)) {
+      float* lg = prefill_stacked(c, m, n, ids, lens);
+      deliver_rows(c, m, lg, n, logits, argmax);
+      return;
+    }
+    size_t at = 0;  // one stream at a time (a stack would move SIMD tail elements)
+    for (size_t b = 0; b < n; ++b) {
+      if (lens[b] == 0) fail(MMF_ERR_ARG, "empty prompt");
+      float* h = prefill_rows(c, m, b, ids + at, lens[b], nullptr, nullptr, nullptr);
+      float* lg = m.logits.as<float>(V);
+      MMF_HIP(launch_to_chain(h + (lens[b] - 1) * H, static_cast<float*>(m.h.p), 1, static_cast<int>(H), m.gH.Lc,
+                              c->stream));
+      lm_single(c, m, static_cast<float*>(m.h.p), lg, false);
+      deliver_rows(c, m, lg, 1, logits ? logits + b * V : nullptr, argmax ? argmax + b : nullptr);
+      at += lens[b];
+    }
   });
 }
 

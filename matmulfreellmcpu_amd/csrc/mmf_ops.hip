@@ -801,6 +801,46 @@ __global__ __launch_bounds__(64) void k_scan_seq(const float* __restrict__ g, co
   state[c] = s;
 }
 
+// The recurrence of several independent sequences stacked as row segments (the prompts of
+// the serving streams): segment b = rows [off[b], off[b + 1]) starts from state b
+// (state + b * H) and leaves its last value there. One thread per (column, segment); each
+// segment is scanned in time order exactly as k_scan_seq scans one sequence.
+__global__ __launch_bounds__(64) void k_scan_segs(const float* __restrict__ g, const float* __restrict__ in,
+                                                  float* __restrict__ recur, float* __restrict__ state,
+                                                  const int* __restrict__ off, int H) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= H) return;
+  const int b = blockIdx.y, t0 = off[b], t1 = off[b + 1];
+  float* st = state + static_cast<size_t>(b) * H;
+  float s = st[c];
+  constexpr int U = 16;
+  for (int t = t0; t < t1; t += U) {
+    float gc[U], ic[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int tt = t + u < t1 ? t + u : t1 - 1;
+      gc[u] = g[static_cast<size_t>(tt) * H + c];
+      ic[u] = in[static_cast<size_t>(tt) * H + c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t + u < t1) {
+        s = __builtin_fmaf(gc[u], s, ic[u]);
+        recur[static_cast<size_t>(t + u) * H + c] = s;
+      }
+    }
+  }
+  st[c] = s;
+}
+
+// rows idx[r] of x [*, K] -> out [n, K]
+__global__ void k_gather_rows(const float* __restrict__ x, const int* __restrict__ idx, float* __restrict__ out,
+                              int K) {
+  const float* src = x + static_cast<size_t>(idx[blockIdx.x]) * K;
+  float* dst = out + static_cast<size_t>(blockIdx.x) * K;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) dst[k] = src[k];
+}
+
 // The recurrence for H % 16 == 0, staged through LDS so that enough bytes are in flight:
 // a block owns 16 columns (H/16 blocks spread over the CUs) and walks time in tiles of
 // kScTT steps. Waves by role: wave 0 runs the 16 column chains (state = fma(g, state, in),
@@ -1138,6 +1178,23 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
   }
   const int n = stream_state ? rows * H : H;
   k_mixer<<<(n + 255) / 256, 256, 0, s>>>(i, f, scan_out, recur, state, lb, rows, H, stream_state ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_mixer_segs(const float* i, float* f, float* scan, float* recur, float* state, const float* lb,
+                             const int* off, int nseg, int rows, int H, hipStream_t s) {
+  if (H % 8 != 0) return hipErrorInvalidValue;  // a SIMD tail per segment would differ
+  const size_t n = static_cast<size_t>(rows) * H;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
+  k_gate<<<blocks, 256, 0, s>>>(i, f, scan, lb, rows, H);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_scan_segs<<<dim3((H + 63) / 64, nseg), 64, 0, s>>>(f, scan, recur, state, off, H);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float* x, const int* idx, float* out, int n, int K, hipStream_t s) {
+  k_gather_rows<<<n, 256, 0, s>>>(x, idx, out, K);
   return hipGetLastError();
 }
 

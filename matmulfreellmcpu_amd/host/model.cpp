@@ -179,15 +179,22 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
   std::vector<std::int64_t> am(B);
   check(ctx_, mmf_model_reset(ctx_, B), "mmf_model_reset");
   streams_ = B;
-  // per-stream prefill, staggered first-token callbacks (model.hpp:60-66 of the reference)
-  for (std::size_t b = 0; b < B; ++b) {
-    {
-      MMFREE_PROFILE("prefill");
-      check(ctx_, mmf_model_prefill(ctx_, b, prompts[b].data(), prompts[b].size(), greedy ? nullptr : lg.data(),
-                                    &am[b]),
-            "mmf_model_prefill");
+  // all prompts prefilled together (the same states and first tokens as the reference's
+  // stream-by-stream prefill), then the first-token callbacks in stream order, each stream
+  // sampling from its own generator (model.hpp:60-66, hgrn_model.cpp:412-428)
+  {
+    MMFREE_PROFILE("prefill");
+    std::vector<std::int64_t> cat;
+    std::vector<std::size_t> lens(B);
+    for (std::size_t b = 0; b < B; ++b) {
+      cat.insert(cat.end(), prompts[b].begin(), prompts[b].end());
+      lens[b] = prompts[b].size();
     }
-    const std::int64_t t0 = greedy ? am[b] : pick(lg.data(), V, samp, rng[b], cand);
+    check(ctx_, mmf_model_prefill_streams(ctx_, B, cat.data(), lens.data(), greedy ? nullptr : lg.data(), am.data()),
+          "mmf_model_prefill_streams");
+  }
+  for (std::size_t b = 0; b < B; ++b) {
+    const std::int64_t t0 = greedy ? am[b] : pick(lg.data() + b * V, V, samp, rng[b], cand);
     streams[b].push_back(t0);
     if (on_token) on_token(b, t0);
     if (t0 == eos_id) done[b] = 1;

@@ -223,6 +223,71 @@ def test_serve_matches_oracle(blobs, oracle, mode):
     e.close()
 
 
+@pytest.mark.parametrize("name", ["small", "odd"])
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_prefill_streams_matches_per_stream(blobs, name, mode):
+    """Stacked prefill of ragged prompts (one row range through every BitLinear, the scan
+    per stream) against one prefill per stream: first tokens, logits and every layer's
+    state bit for bit, also when fewer streams are prefilled than were reset. "odd"
+    (hidden 100) takes the per-stream path (SIMD tails)."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    print(f"prefill_streams blob={name} mode={mode}", flush=True)
+    blob = read_blob(blobs(name))
+    V = blob.config.vocab_size
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(3, V, n) for n in (5, 12, 1, 7, 40, 3)]
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    B = len(prompts) + 2
+    e.reset(B)
+    want = [e.prefill(b, prompts[b], want_logits=True) for b in range(len(prompts))]
+    want_state = e.state()
+    e.reset(B)
+    am, lg = e.prefill_streams(prompts, want_logits=True)
+    got_state = e.state()
+    for b in range(len(prompts)):
+        assert int(am[b]) == want[b][0], b
+        assert_bitexact(lg[b], want[b][1], f"stream {b} logits")
+    assert_bitexact(got_state, want_state, "states after prefill")
+    # the streams decode on from the stacked prefill exactly as from per-stream ones
+    e2 = Engine(0)
+    e2.load_blob(blob, mode)
+    e2.reset(B)
+    for b in range(len(prompts)):
+        e2.prefill(b, prompts[b])
+    tok = np.concatenate([am, [5, 6]]).astype(np.int64)
+    for _ in range(3):
+        a1, a2 = e.step(tok), e2.step(tok)
+        np.testing.assert_array_equal(a1, a2)
+        tok = a1
+    assert_bitexact(e.state(), e2.state(), "states after decode steps")
+    e.close()
+    e2.close()
+
+
+@pytest.mark.parametrize("mode", [FLOAT, FIXED])
+def test_serve_stacked_matches_oracle(blobs, oracle, mode):
+    """The serving path with the stacked prefill against the oracle's generate_serve."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("small"))
+    om = oracle.model(blob)
+    rng = np.random.default_rng(19)
+    V = blob.config.vocab_size
+    prompts = [rng.integers(3, V, n) for n in (9, 1, 33, 4)]
+    want = om.generate_serve(prompts, 6, mode)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    e.reset(len(prompts))
+    streams = [list(p) + [int(t)] for p, t in zip(prompts, e.prefill_streams(prompts))]
+    for _ in range(5):
+        nxt = e.step([s[-1] for s in streams])
+        for b in range(len(prompts)):
+            streams[b].append(int(nxt[b]))
+    for b in range(len(prompts)):
+        np.testing.assert_array_equal(np.array(streams[b]), want[b])
+    e.close()
+
+
 @pytest.mark.parametrize("mode", [FLOAT, FIXED])
 def test_generate_370m(blobs, oracle, mode):
     """Full 370M shape: 16-token prompt, 32 greedy tokens, bit-exact state."""
