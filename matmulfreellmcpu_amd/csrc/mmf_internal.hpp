@@ -161,7 +161,7 @@ hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s)
 // Bytes of int32 workspace launch_gemm needs for `a` (0 when it will not split K); the
 // caller passes at least that much in a.ws.
 size_t gemm_workspace_bytes(const GemmArgs& a);
-// Rows from which the integer modes use the matrix cores (MMF_MFMA_MIN_ROWS, default 32;
+// Rows from which the integer modes use the matrix cores (MMF_MFMA_MIN_ROWS, default 8;
 // 0 disables them).
 int mfma_min_rows();
 

@@ -549,18 +549,18 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a, ActBuf act) {
 // ------------------------------------------------------------------------------------
 // Float-mode ternary GEMM over row tiles, register-blocked over outputs. Block = 128 threads
 // = 16 output lanes x 8 chains; thread (ol, j) runs chain j (the reference's AVX2 lane j,
-// simd.hpp:92-122: fma(y_k, w_k, a) over k = j + 8t in t order) of kFNO outputs from kFNO
+// simd.hpp:92-122: fma(y_k, w_k, a) over k = j + 8t in t order) of NO outputs from NO
 // slabs, for R rows. Activations of kFW words per chain are staged in LDS for the R rows,
 // chain rows padded by 4 floats so the 8 chains of a wave hit distinct banks; each value
-// read feeds kFNO FMAs and each weight word R x 16. PAIR: the first half of the slabs are
+// read feeds NO FMAs and each weight word R x 16. PAIR: the first half of the slabs are
 // gate outputs, the second half their up partners N/2 later (swiglu epilogue).
 // ------------------------------------------------------------------------------------
-constexpr int kFNO = 4;               // outputs per thread
 constexpr int kFW = 4;                // words per chain per LDS chunk
 constexpr int kFCS = kFW * 16 + 4;    // floats per staged chain row
 
-template <int R, bool PAIR>
+template <int R, int NO, bool PAIR>
 __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
+  static_assert(!PAIR || NO % 2 == 0, "gate/up pairs need an even output count");
   extern __shared__ float smem[];
   const int z = blockIdx.z;
   const ProjDev& P = a.p[z];
@@ -571,37 +571,37 @@ __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
   const int nrows = min(R, a.rows - row0);
   const int am = (act.na > 1) ? z : 0;
   const int half = g.ngroups / 2;
-  int grp[kFNO];
-  bool gok[kFNO];
+  int grp[NO];
+  bool gok[NO];
 #pragma unroll
-  for (int s = 0; s < kFNO; ++s) {
+  for (int s = 0; s < NO; ++s) {
     if (PAIR) {
-      const int gg = blockIdx.x * (kFNO / 2) + (s % (kFNO / 2));
+      const int gg = blockIdx.x * (NO / 2) + (s % (NO / 2));
       gok[s] = gg < half;
-      grp[s] = (s < kFNO / 2) ? gg : half + gg;
+      grp[s] = (s < NO / 2) ? gg : half + gg;
     } else {
-      grp[s] = blockIdx.x * kFNO + s;
+      grp[s] = blockIdx.x * NO + s;
       gok[s] = grp[s] < g.ngroups;
     }
     if (!gok[s]) grp[s] = 0;
   }
-  const uint32_t* slab[kFNO];
+  const uint32_t* slab[NO];
 #pragma unroll
-  for (int s = 0; s < kFNO; ++s) slab[s] = P.pk + static_cast<size_t>(grp[s]) * Wc * 128 + ol * 8 + j;
-  float acc[kFNO][R];
+  for (int s = 0; s < NO; ++s) slab[s] = P.pk + static_cast<size_t>(grp[s]) * Wc * 128 + ol * 8 + j;
+  float acc[NO][R];
 #pragma unroll
-  for (int s = 0; s < kFNO; ++s)
+  for (int s = 0; s < NO; ++s)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[s][r] = 0.0f;
   constexpr int PR = 8 * kFCS;  // LDS floats per staged row
   const float* ybase = act.y + (static_cast<size_t>(am) * act.rows + row0) * act.ystride();
   for (int m0 = 0; m0 < Wc; m0 += kFW) {
     const int mw = min(kFW, Wc - m0);
-    uint32_t w[kFW][kFNO];
+    uint32_t w[kFW][NO];
 #pragma unroll
     for (int mm = 0; mm < kFW; ++mm)
 #pragma unroll
-      for (int s = 0; s < kFNO; ++s)
+      for (int s = 0; s < NO; ++s)
         w[mm][s] = (mm < mw && gok[s]) ? slab[s][static_cast<size_t>(m0 + mm) * 128] : 0u;
     __syncthreads();
     const int n4 = mw * 4;
@@ -616,9 +616,9 @@ __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
 #pragma unroll
     for (int mm = 0; mm < kFW; ++mm) {
       if (mm >= mw) break;
-      float wf[kFNO][16];
+      float wf[NO][16];
 #pragma unroll
-      for (int s = 0; s < kFNO; ++s)
+      for (int s = 0; s < NO; ++s)
 #pragma unroll
         for (int t = 0; t < 16; ++t) wf[s][t] = code_f(w[mm][s], t);
 #pragma unroll
@@ -634,7 +634,7 @@ __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
           y[4 * q4 + 3] = v.w;
         }
 #pragma unroll
-        for (int s = 0; s < kFNO; ++s)
+        for (int s = 0; s < NO; ++s)
 #pragma unroll
           for (int t = 0; t < 16; ++t) acc[s][r] = __builtin_fmaf(y[t], wf[s][t], acc[s][r]);
       }
@@ -645,9 +645,9 @@ __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const size_t ar = static_cast<size_t>(am) * act.rows + row0 + r;
-    float val[kFNO];
+    float val[NO];
 #pragma unroll
-    for (int s = 0; s < kFNO; ++s) {
+    for (int s = 0; s < NO; ++s) {
       float sum = hsum8_lanes(acc[s][r]);
       const int o = grp[s] * 16 + ol;
       if (j == 0 && r < nrows && gok[s] && o < g.N) {
@@ -664,15 +664,15 @@ __global__ __launch_bounds__(128) void k_gemm_f(GemmArgs a, ActBuf act) {
     const size_t grow = static_cast<size_t>(row0 + r);
     if (PAIR) {
 #pragma unroll
-      for (int s = 0; s < kFNO / 2; ++s) {
+      for (int s = 0; s < NO / 2; ++s) {
         const int o = grp[s] * 16 + ol;
         if (!gok[s] || o >= Nout) continue;
         const size_t e = grow * Nout + o;
-        a.out[0][e] = swiglu_of(val[s], val[s + kFNO / 2], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+        a.out[0][e] = swiglu_of(val[s], val[s + NO / 2], static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < kFNO; ++s) {
+      for (int s = 0; s < NO; ++s) {
         const int o = grp[s] * 16 + ol;
         if (!gok[s] || o >= g.N) continue;
         const size_t e = grow * g.N + o;
@@ -1113,22 +1113,43 @@ static hipError_t gemm_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s)
   return hipGetLastError();
 }
 
-template <int R, bool PAIR>
+template <int R, int NO, bool PAIR>
+static int gemm_f_blocks(const GemmArgs& a) {
+  const Geom& g = a.p[0].g;
+  const int gx = PAIR ? (g.ngroups / 2 + NO / 2 - 1) / (NO / 2) : (g.ngroups + NO - 1) / NO;
+  return gx * ((a.rows + R - 1) / R) * (PAIR ? 1 : a.nmat);
+}
+
+template <int R, int NO, bool PAIR>
 static hipError_t gemm_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Geom& g = a.p[0].g;
   const size_t lds = static_cast<size_t>(R) * 8 * kFCS * sizeof(float);
-  const int gx = PAIR ? (g.ngroups / 2 + kFNO / 2 - 1) / (kFNO / 2) : (g.ngroups + kFNO - 1) / kFNO;
+  const int gx = PAIR ? (g.ngroups / 2 + NO / 2 - 1) / (NO / 2) : (g.ngroups + NO - 1) / NO;
   dim3 grid(gx, (a.rows + R - 1) / R, PAIR ? 1 : a.nmat);
-  k_gemm_f<R, PAIR><<<grid, 128, lds, s>>>(a, act);
+  k_gemm_f<R, NO, PAIR><<<grid, 128, lds, s>>>(a, act);
   return hipGetLastError();
+}
+
+// Four outputs per thread while that leaves at least 1024 blocks (two waves per SIMD),
+// else two, else one: a small launch is latency-bound and wants more waves more than
+// fewer LDS reads.
+template <int R, bool PAIR>
+static hipError_t gemm_f_rows(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  if (gemm_f_blocks<R, 4, PAIR>(a) >= 1024) return gemm_f_inst<R, 4, PAIR>(a, act, s);
+  if constexpr (PAIR) {  // a block holds gate/up pairs: at least two outputs per thread
+    return gemm_f_inst<R, 2, PAIR>(a, act, s);
+  } else {
+    if (gemm_f_blocks<R, 2, PAIR>(a) >= 1024) return gemm_f_inst<R, 2, PAIR>(a, act, s);
+    return gemm_f_inst<R, 1, PAIR>(a, act, s);
+  }
 }
 
 template <int MODE>
 static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   if (MODE == kFloat && a.rows > 4) {
     const bool pair = a.epi == kEpiSwigluPair;
-    if (a.rows <= 64) return pair ? gemm_f_inst<8, true>(a, act, s) : gemm_f_inst<8, false>(a, act, s);
-    return pair ? gemm_f_inst<16, true>(a, act, s) : gemm_f_inst<16, false>(a, act, s);
+    if (a.rows <= 64) return pair ? gemm_f_rows<8, true>(a, act, s) : gemm_f_rows<8, false>(a, act, s);
+    return pair ? gemm_f_rows<16, true>(a, act, s) : gemm_f_rows<16, false>(a, act, s);
   }
   const bool pair = a.epi == kEpiSwigluPair;
   if (a.rows <= 1) return pair ? gemm_inst<MODE, 1, true>(a, act, s) : gemm_inst<MODE, 1, false>(a, act, s);
@@ -1139,7 +1160,7 @@ static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s)
 int mfma_min_rows() {
   static const int v = [] {
     const char* e = std::getenv("MMF_MFMA_MIN_ROWS");
-    return e ? std::atoi(e) : 32;
+    return e ? std::atoi(e) : 8;
   }();
   return v;
 }
