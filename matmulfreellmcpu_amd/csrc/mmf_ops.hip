@@ -896,23 +896,38 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
       const float* I = ring + ((k % kScNR) * 2 + 1) * kScTT * kScCols;
       float* Rt = R + (k & 1) * kScTT * kScCols;
       const int n = min(kScTT, T - k * kScTT);
-      int t = 0;
-      for (; t + 8 <= n; t += 8) {
-        float gv[8], iv[8];
+      if (n == kScTT) {
+        // whole tile: the operands of the next 8 steps are read while the current 8 are
+        // chained (reads past the tile's end stay inside the ring and are not used)
+        float gv[8], iv[8], gn[8], in8[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          gv[u] = G[(t + u) * kScCols + lane];
-          iv[u] = I[(t + u) * kScCols + lane];
+          gv[u] = G[u * kScCols + lane];
+          iv[u] = I[u * kScCols + lane];
         }
+        for (int t = 0; t < kScTT; t += 8) {
+          const int tn = t + 8 < kScTT ? t + 8 : t;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          s = __builtin_fmaf(gv[u], s, iv[u]);
-          Rt[(t + u) * kScCols + lane] = s;
+          for (int u = 0; u < 8; ++u) {
+            gn[u] = G[(tn + u) * kScCols + lane];
+            in8[u] = I[(tn + u) * kScCols + lane];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            s = __builtin_fmaf(gv[u], s, iv[u]);
+            Rt[(t + u) * kScCols + lane] = s;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            gv[u] = gn[u];
+            iv[u] = in8[u];
+          }
         }
-      }
-      for (; t < n; ++t) {
-        s = __builtin_fmaf(G[t * kScCols + lane], s, I[t * kScCols + lane]);
-        Rt[t * kScCols + lane] = s;
+      } else {
+        for (int t = 0; t < n; ++t) {
+          s = __builtin_fmaf(G[t * kScCols + lane], s, I[t * kScCols + lane]);
+          Rt[t * kScCols + lane] = s;
+        }
       }
     }
     if (wave >= 5 && k >= 1) {
