@@ -226,7 +226,10 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
   const int LS = lds_stride(Lc);
   float* X = smem;
-  float* S = X + 8 * LS + 8;
+  // second LDS row: silu(x2), then the BitLinear-normed rows; with one norm weight and no
+  // x2 the normed row overwrites x in place (each position read and written by one thread)
+  constexpr bool INPLACE = NA == 1 && PRE != kPreSwish;
+  float* S = INPLACE ? X : X + 8 * LS + 8;
   float* red = S + 8 * LS + 8;
   const float* src[NV];
   src[0] = a.x + static_cast<size_t>(row) * K;
@@ -234,14 +237,19 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
   if (PRE != kPreNone) src[IPW] = a.pre_w;
 #pragma unroll
   for (int i = 0; i < NA; ++i) src[INW + i] = a.normw[i];
-  float4 v[NV][MAXV];
+  // the row (and x2) in registers at entry; the norm weights, the same for every row and
+  // so L2-resident, are read in the pass that uses them: fewer registers per thread, more
+  // rows resident per CU
+  constexpr int NX = 1 + (PRE == kPreSwish ? 1 : 0);
+  float4 v[NX][MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int k4 = threadIdx.x + j * blockDim.x;
 #pragma unroll
-    for (int vi = 0; vi < NV; ++vi)
+    for (int vi = 0; vi < NX; ++vi)
       v[vi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[vi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  auto wt = [&](int vi, int k4) { return reinterpret_cast<const float4*>(src[vi])[k4]; };
   auto el = [](const float4& f, int c) { return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w)); };
   // x (and silu(x2)) into the padded chain-transposed LDS rows
 #pragma unroll
@@ -266,10 +274,11 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
       if (k4 >= K4) continue;
+      const float4 w = wt(IPW, k4);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int p = act_pos(4 * k4 + c, K8, LS);
-        float x = (X[p] * r1) * el(v[IPW][j], c);
+        float x = (X[p] * r1) * el(w, c);
         if (PRE == kPreSwish) x = x * S[p];
         X[p] = x;
       }
@@ -286,10 +295,11 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
       if (k4 >= K4) continue;
+      const float4 w = wt(INW + ai, k4);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int p = act_pos(4 * k4 + c, K8, LS);
-        const float y = (X[p] * r2) * el(v[INW + ai][j], c);
+        const float y = (X[p] * r2) * el(w, c);
         Y[p] = y;
         if (MODE == kInt8) m = fmaxf(m, fabsf(y));
       }
@@ -1089,7 +1099,9 @@ static hipError_t prologue4_mode(const PrologueArgs& a, ActBuf& act, size_t lds,
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
-  const size_t lds = (2 * static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8) + 16) * sizeof(float);
+  const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);
+  const bool inplace = a.na == 1 && a.pre != kPreSwish;  // k_prologue4 keeps one LDS row
+  const size_t lds = (2 * rowf + 16) * sizeof(float), lds4 = ((inplace ? 1 : 2) * rowf + 16) * sizeof(float);
   bool fast = act.K % 4 == 0 && act.K / 4 <= 7 * 256 && aligned16(a.x) && (a.na == 1 || a.na == 3);
   if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
   if (a.pre == kPreSwish) fast = fast && aligned16(a.x2);
@@ -1097,9 +1109,9 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
   if (fast) {
     hipError_t e = hipErrorNotSupported;
     switch (mode) {
-      case kFloat: e = prologue4_mode<kFloat>(a, act, lds, s); break;
-      case kFixed: e = prologue4_mode<kFixed>(a, act, lds, s); break;
-      default: e = prologue4_mode<kInt8>(a, act, lds, s); break;
+      case kFloat: e = prologue4_mode<kFloat>(a, act, lds4, s); break;
+      case kFixed: e = prologue4_mode<kFixed>(a, act, lds4, s); break;
+      default: e = prologue4_mode<kInt8>(a, act, lds4, s); break;
     }
     if (e != hipErrorNotSupported) return e;
   }
