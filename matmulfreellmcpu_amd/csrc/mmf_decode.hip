@@ -152,9 +152,12 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   int64_t tok = 0;
   if (KIND == kIFG && ax == nullptr) {
     unsigned long long best = 0ull;
-    for (int e = tid; e < ankeys; e += BS) {
-      const unsigned long long k = akeys[e];
-      best = k > best ? k : best;
+    for (int e0 = tid; e0 < ankeys; e0 += 8 * BS) {  // 8 keys per thread in flight at once
+      unsigned long long k[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) k[u] = e0 + u * BS < ankeys ? akeys[e0 + u * BS] : 0ull;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) best = k[u] > best ? k[u] : best;
     }
     for (int off = 32; off > 0; off >>= 1) {
       const unsigned long long other = __shfl_xor(best, off);
@@ -487,7 +490,7 @@ hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
   lds += (MODE == kFloat) ? na * WL * sizeof(float) : na * (16 * LQ + 8 * sizeof(int32_t) + sizeof(float));
   const int nout = (kind == kGate) ? g.N / 2 : g.N;
   int grid = (nout + kGroup - 1) / kGroup;
-  if (kind == kLM && grid > kLMBlocks) grid = kLMBlocks;
+  if (kind == kLM) grid = lm_blocks(grid, g.K);
   // all weight words of the block's output groups go to LDS at entry when they fit (the
   // lm_head's blocks stride over several groups)
   DecArgs b = a;

@@ -477,7 +477,7 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
 
 int lm_grid(const Model& m) {
   const int g = static_cast<int>((m.cfg.vocab_size + kGroup - 1) / kGroup);
-  return g < kLMBlocks ? g : kLMBlocks;
+  return lm_blocks(g, static_cast<int>(m.cfg.hidden_size));
 }
 
 DecArgs dec_base(Model& m) {

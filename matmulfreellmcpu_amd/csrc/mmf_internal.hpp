@@ -92,7 +92,14 @@ struct DecArgs {
 // Bytes of dynamic LDS one block may allocate on the current device.
 int lds_limit();
 
-constexpr int kLMBlocks = 512;  // lm_head grid (grid-stride over the vocabulary)
+constexpr int kLMBlocks = 2048;  // most lm_head blocks (argmax key slots)
+// lm_head grid for `groups` output groups over hidden size K: every block recomputes the
+// final norms over K, so wide rows take fewer blocks, each striding over several groups
+// (measured: one group per block at K = 1024, 512 blocks at K = 2048 and 2560).
+inline int lm_blocks(int groups, int K) {
+  const int cap = K <= 1024 ? kLMBlocks : 512;
+  return groups < cap ? groups : cap;
+}
 hipError_t launch_decode(DecKind kind, Mode mode, const DecArgs& a, hipStream_t s);
 // rows of x [rows, K] -> chain-transposed rows out [rows, 8*Lc + 8]
 hipError_t launch_to_chain(const float* x, float* out, int rows, int K, int Lc, hipStream_t s);
