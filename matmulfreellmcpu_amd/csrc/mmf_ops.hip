@@ -226,10 +226,8 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
   const int LS = lds_stride(Lc);
   float* X = smem;
-  // second LDS row: silu(x2), then the BitLinear-normed rows; with one norm weight and no
-  // x2 the normed row overwrites x in place (each position read and written by one thread)
-  constexpr bool INPLACE = NA == 1 && PRE != kPreSwish;
-  float* S = INPLACE ? X : X + 8 * LS + 8;
+  // second LDS row only for silu(x2) (g_norm); the normed values never go through LDS
+  float* S = (PRE == kPreSwish) ? X + 8 * LS + 8 : X;
   float* red = S + 8 * LS + 8;
   const float* src[NV];
   src[0] = a.x + static_cast<size_t>(row) * K;
@@ -286,69 +284,79 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
     __syncthreads();
   }
   const float r2 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
-  float* Y = S;
+  // Each thread keeps the BitLinear-normed values of its own elements in registers and
+  // writes them (or their codes) straight to their chain-transposed positions: no staging
+  // row, no extra pass.
 #pragma unroll
   for (int ai = 0; ai < NA; ++ai) {
     const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+    float4 yv[MAXV];
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
       if (k4 >= K4) continue;
       const float4 w = wt(INW + ai, k4);
+      float y[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int p = act_pos(4 * k4 + c, K8, LS);
-        const float y = (X[p] * r2) * el(w, c);
-        Y[p] = y;
-        if (MODE == kInt8) m = fmaxf(m, fabsf(y));
+        y[c] = (X[act_pos(4 * k4 + c, K8, LS)] * r2) * el(w, c);
+        if (MODE == kInt8) m = fmaxf(m, fabsf(y[c]));
       }
+      yv[j] = make_float4(y[0], y[1], y[2], y[3]);
     }
     float sa = 0.0f;
     if (MODE == kInt8) {
       m = block_max(m, red);
       sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
       if (threadIdx.x == 0) act.sa[ar] = sa;
-    } else {
-      __syncthreads();
     }
-    if (MODE == kFloat) {
-      float* yo = act.y + ar * act.ystride();
-      for (int jr = 0; jr < 8; ++jr)
-        for (int t = threadIdx.x; t < Lc; t += blockDim.x) yo[jr * Lc + t] = (t < nb) ? Y[jr * LS + t] : 0.0f;
-      for (int t = threadIdx.x; t < 8; t += blockDim.x) yo[8 * Lc + t] = (t < nt) ? Y[8 * LS + t] : 0.0f;
-    } else {
-      int8_t* q = act.q + ar * act.qstride();
-      const int n4 = Lc / 4;
-      for (int w = threadIdx.x; w < 8 * n4; w += blockDim.x) {
-        const int jr = w / n4, t4 = (w - jr * n4) * 4;
-        uint32_t hi = 0, lo = 0;
-        for (int u = 0; u < 4; ++u) {
-          const int t = t4 + u;
-          if (t < nb) {
-            const float y = Y[jr * LS + t];
-            if (MODE == kFixed) {
-              const int32_t c = q510_body(y, a.qs);
-              hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
-              lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
-            } else {
-              hi |= static_cast<uint32_t>(q8_of(y, sa) & 0xFF) << (8 * u);
-            }
+    float* yo = act.y + ar * act.ystride();
+    int8_t* q = act.q + ar * act.qstride();
+    int32_t* ct = act.ct + ar * 8;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int k4 = threadIdx.x + j * blockDim.x;
+      if (k4 >= K4) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = 4 * k4 + c;
+        const float y = el(yv[j], c);
+        if (k < K8) {  // chain k % 8, position k / 8
+          const int pos = (k & 7) * Lc + (k >> 3);
+          if (MODE == kFloat) {
+            yo[pos] = y;
+          } else if (MODE == kFixed) {
+            const int32_t code = q510_body(y, a.qs);
+            q[pos] = static_cast<int8_t>((code >> 8) & 0xFF);
+            q[8 * Lc + pos] = static_cast<int8_t>(((code & 0xFF) - 128) & 0xFF);
+          } else {
+            q[pos] = static_cast<int8_t>(q8_of(y, sa));
           }
+        } else if (MODE == kFloat) {
+          yo[8 * Lc + (k - K8)] = y;
+        } else {
+          ct[k - K8] = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
         }
-        *reinterpret_cast<uint32_t*>(q + jr * Lc + t4) = hi;
-        if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + jr * Lc + t4) = lo;
-      }
-      for (int t = threadIdx.x; t < 8; t += blockDim.x) {
-        int32_t c = 0;
-        if (t < nt) {
-          const float y = Y[8 * LS + t];
-          c = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
-        }
-        act.ct[ar * 8 + t] = c;
       }
     }
-    __syncthreads();
+    // zeros past each chain's last element and past the tail (padding the GEMMs read)
+    const int padw = Lc - nb;
+    for (int e = threadIdx.x; e < 8 * padw + (8 - nt); e += blockDim.x) {
+      if (e < 8 * padw) {
+        const int pos = (e / padw) * Lc + nb + e % padw;
+        if (MODE == kFloat) {
+          yo[pos] = 0.0f;
+        } else {
+          q[pos] = 0;
+          if (MODE == kFixed) q[8 * Lc + pos] = 0;
+        }
+      } else {
+        const int t = nt + (e - 8 * padw);
+        if (MODE == kFloat) yo[8 * Lc + t] = 0.0f;
+        else ct[t] = 0;
+      }
+    }
   }
 }
 
@@ -1100,8 +1108,8 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);
-  const bool inplace = a.na == 1 && a.pre != kPreSwish;  // k_prologue4 keeps one LDS row
-  const size_t lds = (2 * rowf + 16) * sizeof(float), lds4 = ((inplace ? 1 : 2) * rowf + 16) * sizeof(float);
+  const size_t lds = (2 * rowf + 16) * sizeof(float);
+  const size_t lds4 = ((a.pre == kPreSwish ? 2 : 1) * rowf + 16) * sizeof(float);  // k_prologue4
   bool fast = act.K % 4 == 0 && act.K / 4 <= 7 * 256 && aligned16(a.x) && (a.na == 1 || a.na == 3);
   if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
   if (a.pre == kPreSwish) fast = fast && aligned16(a.x2);
