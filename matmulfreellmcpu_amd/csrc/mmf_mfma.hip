@@ -446,7 +446,7 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 
 // Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
 // that still gives every CU a block (all blocks of all matrices), else 128. Then K is
-// split in powers of two until there is a block per CU (each split >= 4 stages).
+// split in powers of two until there are 128 blocks (each split >= 4 stages).
 struct Plan {
   int wm, wn, ksplit;
 };
@@ -457,9 +457,10 @@ Plan plan_of(const GemmArgs& a) {
   if (p.wm == 1 ? tiles_of<1, 4>(a) * nz < 256 : tiles_of<2, 4>(a) * nz < 256) p.wn = 2;
   const int tiles = (p.wm == 1 ? (p.wn == 4 ? tiles_of<1, 4>(a) : tiles_of<1, 2>(a))
                                : (p.wn == 4 ? tiles_of<2, 4>(a) : tiles_of<2, 2>(a))) * nz;
-  // split K until there is a block per CU, keeping >= 4 stages per split
+  // split K until there are 128 blocks (one per two CUs; more splits measured slower, the
+  // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
-  while (tiles * p.ksplit < 256 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
+  while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
   return p;
 }
 
