@@ -134,6 +134,31 @@ def measure_op_sweep(reps):
     return out
 
 
+def vendor_int8_gemm(T, H, I, reps=20):
+    """The vendor library's dense int8 GEMM (hipBLASLt through torch._int_mm) on the four
+    projection shapes of one prefill layer: rows T, int8 activations times int8 weights
+    (here ternary values stored as full int8), int32 out. Reported beside the prefill
+    GEMMs as the rate a tuned library reaches at the same M, N, K."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(5)
+    shapes = {"gemm_ifg": (H, 3 * H), "gemm_o": (H, H), "gemm_gate": (H, 2 * I), "gemm_down": (I, H)}
+    out = {}
+    for k, (K, N) in shapes.items():
+        a = torch.randint(-127, 128, (T, K), dtype=torch.int8, device="cuda", generator=g)
+        w = torch.randint(-1, 2, (N, K), dtype=torch.int8, device="cuda", generator=g).t()  # K x N, column-major
+        torch._int_mm(a, w)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch._int_mm(a, w)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[k] = round(2.0 * T * K * N / us / 1e6, 1)
+    return out
+
+
 def measure_prefill(blob_dir, T=2048, modes=("fixed", "int8", "float")):
     from matmulfreellmcpu_amd import MODES, Engine
     V, H, L, I = DIMS["s2"]
@@ -159,6 +184,15 @@ def measure_prefill(blob_dir, T=2048, modes=("fixed", "int8", "float")):
             r["mfma_frac_all_gemms"] = round(planes * allops / alltime / 1e6 / INT8_PEAK_TOPS, 4)
         res[name] = r
         log(f"[bench] prefill 1.3B T={T} {name}: {r['ms']} ms ({r['tok_s']} tok/s)")
+    # torch's bundled HIP runtime cannot open the device in a process where this library's
+    # runtime already has it: the comparison runs in a child process that imports only torch
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-int8", f"{T},{H},{I}"],
+                           capture_output=True, text=True, timeout=300, check=True)
+        res["vendor_int8_gemm_TOPS"] = json.loads(r.stdout.strip().splitlines()[-1])
+        log(f"[bench] hipBLASLt int8 GEMM at the same shapes (TOP/s): {res['vendor_int8_gemm_TOPS']}")
+    except Exception as ex:  # a comparison line only; the prefill numbers stand without it
+        log(f"[bench] vendor int8 GEMM comparison skipped: {ex}")
     return res
 
 
@@ -217,7 +251,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--sections", default="decode,op_sweep,prefill,serve",
                     help="comma list of decode,op_sweep,prefill,serve (decode is always run)")
+    ap.add_argument("--vendor-int8", default=None, metavar="T,H,I",
+                    help="only time the vendor int8 GEMM on one prefill layer's shapes (child process)")
     args = ap.parse_args()
+    if args.vendor_int8:
+        T, H, I = (int(x) for x in args.vendor_int8.split(","))
+        print(json.dumps(vendor_int8_gemm(T, H, I)))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the HGRN-Bit hot path here runs on a single MI355X and this "
               f"build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)

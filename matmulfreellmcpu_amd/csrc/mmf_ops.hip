@@ -217,8 +217,8 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
 // row (x, the gate input x2, the stage-1 weight, the NA BitLinear norm weights) is loaded
 // as float4 at entry -- one memory round trip -- and each thread then works on exactly the
 // elements it loaded. Arithmetic and order are those of k_prologue.
-template <int MODE, int PRE, int NA, int MAXV>
-__global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
+template <int MODE, int PRE, int NA, int MAXV, bool PW, int BT>
+__global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
   constexpr int NV = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
   constexpr int IX2 = 1, IPW = (PRE == kPreSwish) ? 2 : 1, INW = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
@@ -235,19 +235,30 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
   if (PRE != kPreNone) src[IPW] = a.pre_w;
 #pragma unroll
   for (int i = 0; i < NA; ++i) src[INW + i] = a.normw[i];
-  // the row (and x2) in registers at entry; the norm weights, the same for every row and
-  // so L2-resident, are read in the pass that uses them: fewer registers per thread, more
-  // rows resident per CU
+  // The row (and x2) in registers at entry. The norm weights, the same for every row and
+  // so L2-resident, are read in the pass that uses them (fewer registers per thread, more
+  // rows resident per CU) or, with PW (a few rows: the launch is one row's latency), loaded
+  // at entry with the row, so that no pass waits for a memory round trip of its own.
   constexpr int NX = 1 + (PRE == kPreSwish ? 1 : 0);
+  constexpr int NWV = PW ? NV - NX : 1;
   float4 v[NX][MAXV];
+  float4 wv[NWV][PW ? MAXV : 1];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int k4 = threadIdx.x + j * blockDim.x;
 #pragma unroll
     for (int vi = 0; vi < NX; ++vi)
       v[vi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[vi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (PW) {
+#pragma unroll
+      for (int wi = 0; wi < NWV; ++wi)
+        wv[wi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[NX + wi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
-  auto wt = [&](int vi, int k4) { return reinterpret_cast<const float4*>(src[vi])[k4]; };
+  auto wt = [&](int vi, int k4, int j) {
+    if constexpr (PW) return wv[vi - NX][j];
+    else return reinterpret_cast<const float4*>(src[vi])[k4];
+  };
   auto el = [](const float4& f, int c) { return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w)); };
   // x (and silu(x2)) into the padded chain-transposed LDS rows
 #pragma unroll
@@ -272,7 +283,7 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
       if (k4 >= K4) continue;
-      const float4 w = wt(IPW, k4);
+      const float4 w = wt(IPW, k4, j);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int p = act_pos(4 * k4 + c, K8, LS);
@@ -296,7 +307,7 @@ __global__ __launch_bounds__(256) void k_prologue4(PrologueArgs a, ActBuf act) {
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
       if (k4 >= K4) continue;
-      const float4 w = wt(INW + ai, k4);
+      const float4 w = wt(INW + ai, k4, j);
       float y[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -1085,12 +1096,24 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
 
 static int host_lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
 
+// Up to kPrologueFewRows rows (two per CU, the CUs otherwise idle) a row gets a 1024-thread
+// block with every input, the norm weights included, loaded at entry: each thread then
+// encodes 4-8 elements instead of 12-28, with four waves per SIMD to hide each other's
+// latency. Above it, 256-thread blocks that read the weights in the pass that uses them
+// keep more rows resident per CU.
+constexpr int kPrologueFewRows = 512;
+
 template <int MODE, int PRE, int NA>
 static hipError_t prologue4_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
-  if (act.K / 4 <= 3 * 256)
-    k_prologue4<MODE, PRE, NA, 3><<<act.rows, 256, lds, s>>>(a, act);
-  else
-    k_prologue4<MODE, PRE, NA, 7><<<act.rows, 256, lds, s>>>(a, act);
+  const int K4 = act.K / 4;
+  if (act.rows <= kPrologueFewRows) {
+    if (K4 <= 1024) k_prologue4<MODE, PRE, NA, 1, true, 1024><<<act.rows, 1024, lds, s>>>(a, act);
+    else k_prologue4<MODE, PRE, NA, 2, true, 1024><<<act.rows, 1024, lds, s>>>(a, act);
+  } else if (K4 <= 3 * 256) {
+    k_prologue4<MODE, PRE, NA, 3, false, 256><<<act.rows, 256, lds, s>>>(a, act);
+  } else {
+    k_prologue4<MODE, PRE, NA, 7, false, 256><<<act.rows, 256, lds, s>>>(a, act);
+  }
   return hipGetLastError();
 }
 
