@@ -259,7 +259,7 @@ ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, 
   if (mode == kFloat) {
     a.y = y.as<float>(nr * a.ystride());
   } else {
-    a.q = q.as<int8_t>(nr * a.qstride());
+    a.q = q.as<int8_t>(2 * static_cast<size_t>(na) * a.qplane());
     a.ct = ct.as<int32_t>(nr * 8);
     a.sa = sa.as<float>(nr);
   }

@@ -113,8 +113,12 @@ __host__ __device__ inline int64_t key_index(unsigned long long k) {
 // ---- generic row kernels (mmf_ops.hip) ------------------------------------------------
 // Chain-transposed activations of `rows` rows for NA projections:
 //   float: y  [NA][rows][8*Lc + 8]
-//   int:   q  [NA][rows][2][8*Lc] int8 planes (plane 1 unused in kInt8),
+//   int:   q  [NA][2 planes][fragment tiles] int8 codes (plane 1 unused in kInt8),
 //          ct [NA][rows][8] int32 tail codes, sa [NA][rows] int8 scales
+// The integer planes are stored in the matrix cores' operand order: rows in groups of 32,
+// chain positions in chunks of 32, and each (group, chunk) fragment one contiguous 1 KB in
+// which lane l = row % 32 + 32 * (pos / 16 % 2) holds 16 consecutive positions. A fragment
+// then moves to LDS as one linear 1 KB transfer. Each plane holds rows rounded up to 32.
 struct ActBuf {
   float* y = nullptr;
   int8_t* q = nullptr;
@@ -122,7 +126,20 @@ struct ActBuf {
   float* sa = nullptr;
   int Lc = 0, K = 0, K8 = 0, nb = 0, ntail = 0, rows = 0, na = 0;
   __host__ __device__ size_t ystride() const { return static_cast<size_t>(8 * Lc + 8); }
-  __host__ __device__ size_t qstride() const { return static_cast<size_t>(2 * 8 * Lc); }
+  __host__ __device__ int rows32() const { return (rows + 31) & ~31; }
+  // bytes of one plane of one projection
+  __host__ __device__ size_t qplane() const { return static_cast<size_t>(rows32()) * 8 * Lc; }
+  // byte offset of the row's first fragment within a plane (position 0)
+  __host__ __device__ size_t qrow(int row) const {
+    return static_cast<size_t>(row >> 5) * (Lc / 4) * 1024 + (row & 31) * 16;
+  }
+  // byte offset of chain position pos from the row's base
+  __host__ __device__ static size_t qpos(int pos) {
+    return static_cast<size_t>(pos >> 5) * 1024 + ((pos >> 4) & 1) * 512 + (pos & 15);
+  }
+  __host__ __device__ size_t qoff(int proj, int plane, int row, int pos) const {
+    return (2 * static_cast<size_t>(proj) + plane) * qplane() + qrow(row) + qpos(pos);
+  }
 };
 
 // Stage kinds of the row prologue (what happens before the BitLinear's own RMSNorm).

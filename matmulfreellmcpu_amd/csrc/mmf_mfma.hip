@@ -21,6 +21,10 @@
 // (gate group c at cg = 2c, its up partner N/2 + 32c at cg = 2c + 1) so that one wave holds
 // both halves of swiglu(gate, up) (hgrn_model.cpp:171-185) in registers.
 //
+// Activations: the prologues store the int8 planes already in fragment order (32 rows x 32
+// positions per contiguous 1 KB, lanes as the matrix cores take them), so an A transfer is
+// one linear 1 KB read.
+//
 // Block: WM x WN waves (2 x 4 for long row ranges and wide matrices: 128 x 256 tiles, so
 // the activations are re-read once per 256 columns), each wave a 64 x 64 tile (2 x 2
 // fragments).
@@ -89,7 +93,7 @@ __device__ __forceinline__ void issue_stage(const int8_t* const* asrc, const uin
                                             unsigned char* sb, int st, int wave) {
 #pragma unroll
   for (int i = 0; i < DA; ++i)
-    __builtin_amdgcn_global_load_lds(asrc[i] + st * 32 * KQ, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(asrc[i] + st * 1024 * KQ, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
 #pragma unroll
   for (int i = 0; i < DB; ++i)
     __builtin_amdgcn_global_load_lds(bsrc[i] + st * 64 * KQ, (lds_void*)(sb + SA + (wave * DB + i) * 256), 4, 0, 0);
@@ -132,18 +136,21 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int nall = Lc / (4 * KQ), ksp = gridDim.y, ks = blockIdx.y;
   const int st0 = static_cast<int>((static_cast<long>(nall) * ks) / ksp);
   const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
-  const size_t qstride = act.qstride(), plane = static_cast<size_t>(8 * Lc);
-  const int8_t* qbase = act.q + static_cast<size_t>(am) * act.rows * qstride;
+  const int8_t* qbase = act.q + 2 * static_cast<size_t>(am) * act.qplane();
 
-  // per-lane sources of this wave's transfers (advanced by 64 bytes / 128 words per stage)
+  // per-lane sources of this wave's transfers (advanced by KQ fragments = KQ KB of the
+  // fragment-tiled activations / 128 words per stage). Row groups past the last 32-row
+  // group of the activations (a row tile that overhangs it) read that last group again;
+  // their products are never stored.
   const int8_t* asrc[DA];
+  const int lastg = act.rows32() / 32 - 1;
 #pragma unroll
   for (int i = 0; i < DA; ++i) {
     const int f = wave * DA + i;  // = (plane * FR + frag) * KQ + k-chunk
     const int kh = f % KQ, pl = (f / KQ) / FR, rf = (f / KQ) % FR;
-    int row = row0 + rf * 32 + (lane & 31);
-    row = row < act.rows ? row : act.rows - 1;
-    asrc[i] = qbase + static_cast<size_t>(row) * qstride + pl * plane + kh * 32 + (lane >> 5) * 16;
+    int g = (row0 >> 5) + rf;
+    g = g < lastg ? g : lastg;
+    asrc[i] = qbase + pl * act.qplane() + (static_cast<size_t>(g) * (Lc / 4) + kh) * 1024 + lane * 16;
   }
   const uint32_t* bsrc[DB];
 #pragma unroll

@@ -119,6 +119,17 @@ __global__ void k_pack(const int8_t* __restrict__ wq, Geom g, uint32_t* __restri
   }
 }
 
+// Row of block b in the row kernels that write the fragment-tiled integer codes. A 128-byte
+// line of those codes holds 16 bytes of each of 8 consecutive rows; blocks go to the 8 XCDs
+// in turn (block b on XCD b % 8), so XCD x takes the 8-row groups x, x + 8, x + 16, ... and
+// the partial lines of one group merge in one L2 instead of meeting in memory from several.
+// The grid is the row count rounded up to 64; blocks past the last row exit at once.
+__device__ __forceinline__ int xcd_row(int b) {
+  const int x = b & 7, i = b >> 3;
+  return (((i >> 3) << 3) + x) * 8 + (i & 7);
+}
+static int row_grid(int rows) { return (rows + 63) / 64 * 64; }
+
 // ------------------------------------------------------------------------------------
 // BitLinear prologue over rows: optional stage-1 norm, the BitLinear RMSNorm
 // (bitlinear.cpp:62-78, 99-107) and the activation encoding of each of na projections.
@@ -126,7 +137,8 @@ __global__ void k_pack(const int8_t* __restrict__ wq, Geom g, uint32_t* __restri
 template <int MODE>
 __global__ void k_prologue(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
-  const int row = blockIdx.x;
+  const int row = xcd_row(blockIdx.x);
+  if (row >= act.rows) return;
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail;
   const int LS = lds_stride(Lc);
   float* X = smem;                   // [8*LS + 8]
@@ -178,8 +190,10 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
         for (int t = threadIdx.x; t < Lc; t += blockDim.x) yo[j * Lc + t] = (t < nb) ? Y[j * LS + t] : 0.0f;
       for (int t = threadIdx.x; t < 8; t += blockDim.x) yo[8 * Lc + t] = (t < nt) ? Y[8 * LS + t] : 0.0f;
     } else {
-      int8_t* q = act.q + ar * act.qstride();
-      // 4 consecutive chain positions per thread -> one 32-bit store per plane
+      int8_t* q = act.q + act.qoff(ai, 0, row, 0);
+      const size_t lop = act.qplane();
+      // 4 consecutive chain positions per thread -> one 32-bit store per plane (4 consecutive
+      // positions from a multiple of 4 stay in one 16-byte run of the fragment layout)
       const int n4 = Lc / 4;
       for (int w = threadIdx.x; w < 8 * n4; w += blockDim.x) {
         const int j = w / n4, t4 = (w - j * n4) * 4;
@@ -197,8 +211,8 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
             }
           }
         }
-        *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
-        if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
+        *reinterpret_cast<uint32_t*>(q + ActBuf::qpos(j * Lc + t4)) = hi;
+        if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + lop + ActBuf::qpos(j * Lc + t4)) = lo;
       }
       for (int t = threadIdx.x; t < 8; t += blockDim.x) {
         int32_t c = 0;
@@ -222,7 +236,8 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
   constexpr int NV = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
   constexpr int IX2 = 1, IPW = (PRE == kPreSwish) ? 2 : 1, INW = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
-  const int row = blockIdx.x;
+  const int row = xcd_row(blockIdx.x);
+  if (row >= act.rows) return;
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
   const int LS = lds_stride(Lc);
   float* X = smem;
@@ -323,7 +338,8 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
       if (threadIdx.x == 0) act.sa[ar] = sa;
     }
     float* yo = act.y + ar * act.ystride();
-    int8_t* q = act.q + ar * act.qstride();
+    int8_t* q = act.q + act.qoff(ai, 0, row, 0);  // plane 0 of this row; plane 1 at + qplane
+    const size_t lop = act.qplane();
     int32_t* ct = act.ct + ar * 8;
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
@@ -339,10 +355,11 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
             yo[pos] = y;
           } else if (MODE == kFixed) {
             const int32_t code = q510_body(y, a.qs);
-            q[pos] = static_cast<int8_t>((code >> 8) & 0xFF);
-            q[8 * Lc + pos] = static_cast<int8_t>(((code & 0xFF) - 128) & 0xFF);
+            const size_t o = ActBuf::qpos(pos);
+            q[o] = static_cast<int8_t>((code >> 8) & 0xFF);
+            q[lop + o] = static_cast<int8_t>(((code & 0xFF) - 128) & 0xFF);
           } else {
-            q[pos] = static_cast<int8_t>(q8_of(y, sa));
+            q[ActBuf::qpos(pos)] = static_cast<int8_t>(q8_of(y, sa));
           }
         } else if (MODE == kFloat) {
           yo[8 * Lc + (k - K8)] = y;
@@ -359,8 +376,8 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
         if (MODE == kFloat) {
           yo[pos] = 0.0f;
         } else {
-          q[pos] = 0;
-          if (MODE == kFixed) q[8 * Lc + pos] = 0;
+          q[ActBuf::qpos(pos)] = 0;
+          if (MODE == kFixed) q[lop + ActBuf::qpos(pos)] = 0;
         }
       } else {
         const int t = nt + (e - 8 * padw);
@@ -373,9 +390,11 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
 
 // int16-range codes -> split planes (the TernaryBackend path: codes arrive quantised)
 __global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
-  const int row = blockIdx.x, Lc = act.Lc, nb = act.nb;
+  const int row = xcd_row(blockIdx.x), Lc = act.Lc, nb = act.nb;
+  if (row >= act.rows) return;
   const int32_t* xr = x + static_cast<size_t>(row) * act.K;
-  int8_t* q = act.q + static_cast<size_t>(row) * act.qstride();
+  int8_t* q = act.q + act.qoff(0, 0, row, 0);
+  const size_t lop = act.qplane();
   for (int j = 0; j < 8; ++j)
     for (int t4 = threadIdx.x * 4; t4 < Lc; t4 += blockDim.x * 4) {
       uint32_t hi = 0, lo = 0;
@@ -387,8 +406,8 @@ __global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
           lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
         }
       }
-      *reinterpret_cast<uint32_t*>(q + j * Lc + t4) = hi;
-      *reinterpret_cast<uint32_t*>(q + 8 * Lc + j * Lc + t4) = lo;
+      *reinterpret_cast<uint32_t*>(q + ActBuf::qpos(j * Lc + t4)) = hi;
+      *reinterpret_cast<uint32_t*>(q + lop + ActBuf::qpos(j * Lc + t4)) = lo;
     }
   for (int t = threadIdx.x; t < 8; t += blockDim.x)
     act.ct[static_cast<size_t>(row) * 8 + t] = (t < act.ntail) ? xr[act.K8 + t] : 0;
@@ -451,9 +470,7 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a, ActBuf act) {
                   rem2 = rem - pl * 8 * mw * 4, jj = rem2 / (mw * 4), d = rem2 - jj * mw * 4;
         uint32_t v = 0;
         if (r < nrows)
-          v = *reinterpret_cast<const uint32_t*>(
-              act.q + (static_cast<size_t>(ai) * act.rows + row0 + r) * act.qstride() + pl * 8 * Lc +
-              jj * Lc + m0 * 16 + d * 4);
+          v = *reinterpret_cast<const uint32_t*>(act.q + act.qoff(ai, pl, row0 + r, jj * Lc + m0 * 16 + d * 4));
         L[e] = v;
       }
     }
@@ -1107,12 +1124,12 @@ template <int MODE, int PRE, int NA>
 static hipError_t prologue4_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
   const int K4 = act.K / 4;
   if (act.rows <= kPrologueFewRows) {
-    if (K4 <= 1024) k_prologue4<MODE, PRE, NA, 1, true, 1024><<<act.rows, 1024, lds, s>>>(a, act);
-    else k_prologue4<MODE, PRE, NA, 2, true, 1024><<<act.rows, 1024, lds, s>>>(a, act);
+    if (K4 <= 1024) k_prologue4<MODE, PRE, NA, 1, true, 1024><<<row_grid(act.rows), 1024, lds, s>>>(a, act);
+    else k_prologue4<MODE, PRE, NA, 2, true, 1024><<<row_grid(act.rows), 1024, lds, s>>>(a, act);
   } else if (K4 <= 3 * 256) {
-    k_prologue4<MODE, PRE, NA, 3, false, 256><<<act.rows, 256, lds, s>>>(a, act);
+    k_prologue4<MODE, PRE, NA, 3, false, 256><<<row_grid(act.rows), 256, lds, s>>>(a, act);
   } else {
-    k_prologue4<MODE, PRE, NA, 7, false, 256><<<act.rows, 256, lds, s>>>(a, act);
+    k_prologue4<MODE, PRE, NA, 7, false, 256><<<row_grid(act.rows), 256, lds, s>>>(a, act);
   }
   return hipGetLastError();
 }
@@ -1148,15 +1165,15 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
   }
   const int threads = 256;
   switch (mode) {
-    case kFloat: k_prologue<kFloat><<<act.rows, threads, lds, s>>>(a, act); break;
-    case kFixed: k_prologue<kFixed><<<act.rows, threads, lds, s>>>(a, act); break;
-    default: k_prologue<kInt8><<<act.rows, threads, lds, s>>>(a, act); break;
+    case kFloat: k_prologue<kFloat><<<row_grid(act.rows), threads, lds, s>>>(a, act); break;
+    case kFixed: k_prologue<kFixed><<<row_grid(act.rows), threads, lds, s>>>(a, act); break;
+    default: k_prologue<kInt8><<<row_grid(act.rows), threads, lds, s>>>(a, act); break;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_codes_to_planes(const int32_t* x, ActBuf& act, hipStream_t s) {
-  k_codes<<<act.rows, 256, 0, s>>>(x, act);
+  k_codes<<<row_grid(act.rows), 256, 0, s>>>(x, act);
   return hipGetLastError();
 }
 
