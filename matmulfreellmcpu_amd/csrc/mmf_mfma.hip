@@ -28,16 +28,20 @@
 // Block: WM x WN waves (2 x 4 for long row ranges and wide matrices: 128 x 256 tiles, so
 // the activations are re-read once per 256 columns), each wave a 64 x 64 tile (2 x 2
 // fragments).
-// The operands of each 64-position stage travel from global memory to LDS by direct DMA
-// (global_load_lds: lane l's 16 or 4 bytes land at LDS base + 16l or 4l), laid out in the
-// matrix cores' own lane order, so every fragment read is one linear 1 KB (A) or 256 B (B)
-// LDS access. A ring of S stages keeps S - 1 stages in flight; each wave waits for its own
-// transfers (s_waitcnt vmcnt) and one barrier per stage publishes them to the block.
+// The operands of each 64-position stage are staged through registers: every wave loads its
+// share of the stage (16 bytes or one word per lane, in the matrix cores' lane order) two
+// stages ahead into one of two register sets, writes it to one of two LDS slots a stage
+// ahead, and one barrier per stage publishes the slot to the block. Every fragment read is
+// one linear 1 KB (A) or 256 B (B) LDS access. Direct global-to-LDS DMA into a 4-slot ring
+// measured 5-9% slower: the compiler cannot count LDS reads against an outstanding LDS DMA,
+// so each stage's first product waited for all of that stage's LDS reads.
 //
 // Split-K: when a GEMM has too few tiles to occupy the chip (a few dozen rows, or narrow
 // matrices), blockIdx.y selects a contiguous range of stages; each block stores its exact
 // int32 partial tile, and k_splitk_epi adds the partials in split order and applies the
 // epilogue (integer sums: the order does not change the result).
+#include <type_traits>
+
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
 
@@ -47,7 +51,6 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 __global__ void k_pack_mfma(const uint32_t* __restrict__ pk, Geom g, int pair, uint32_t* __restrict__ pkm) {
   const int nK32 = g.Lc / 4;
@@ -82,24 +85,13 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
-// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned.
+// s_waitcnt lgkmcnt(0): this wave's LDS reads and writes have returned.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// DMA of one stage of 32*KQ positions into a ring slot: this wave's A fragments (16 bytes
-// per lane) and B fragments (one word per lane). (A plain function: a lambda holding these
-// builtins keeps the kernel's host stub from being emitted.)
-template <int DA, int DB, int SA, int KQ>
-__device__ __forceinline__ void issue_stage(const int8_t* const* asrc, const uint32_t* const* bsrc,
-                                            unsigned char* sb, int st, int wave) {
-#pragma unroll
-  for (int i = 0; i < DA; ++i)
-    __builtin_amdgcn_global_load_lds(asrc[i] + st * 1024 * KQ, (lds_void*)(sb + (wave * DA + i) * 1024), 16, 0, 0);
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-    __builtin_amdgcn_global_load_lds(bsrc[i] + st * 64 * KQ, (lds_void*)(sb + SA + (wave * DB + i) * 256), 4, 0, 0);
-}
+template <int V>
+using ic = std::integral_constant<int, V>;
 
-template <int MODE, int EPI, int WM, int WN, int S, int KQ>
+template <int MODE, int EPI, int WM, int WN, int KQ>
 __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
   constexpr int NW = WM * WN;                   // waves per block
@@ -111,9 +103,8 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   constexpr int DA = P * FR * KQ / NW;          // A transfers per wave per stage
   constexpr int DB = BG * KQ / NW;              // B transfers per wave per stage
   static_assert(DA * NW == P * FR * KQ && DB * NW == BG * KQ, "transfers must split evenly over the waves");
-  constexpr int D = DA + DB;
-  extern __shared__ __align__(16) unsigned char lds[];  // [S][SS] ring, then srow[BM]
-  float* srow = reinterpret_cast<float*>(lds + S * SS);  // Int8: the block's activation scales
+  extern __shared__ __align__(16) unsigned char lds[];  // [2][SS] slots, then srow[BM]
+  float* srow = reinterpret_cast<float*>(lds + 2 * SS);  // Int8: the block's activation scales
 
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
@@ -138,7 +129,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
   const int8_t* qbase = act.q + 2 * static_cast<size_t>(am) * act.qplane();
 
-  // per-lane sources of this wave's transfers (advanced by KQ fragments = KQ KB of the
+  // per-lane sources of this wave's loads (advanced by KQ fragments = KQ KB of the
   // fragment-tiled activations / 128 words per stage). Row groups past the last 32-row
   // group of the activations (a row tile that overhangs it) read that last group again;
   // their products are never stored.
@@ -162,13 +153,13 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   }
 
   // epilogue operands that do not depend on the accumulators, fetched before the main loop
-  // so their latency hides behind it: per-row int8 scales into LDS (DMA, one per lane),
-  // per-column Q5.10 offsets (128 * rowsum) into registers
+  // so their latency hides behind it: per-row int8 scales (one per lane, to LDS after the
+  // loop), per-column Q5.10 offsets (128 * rowsum)
+  float sv = 0.0f;
   if (MODE == kInt8 && wave * 64 < BM) {
     int row = row0 + wave * 64 + lane;
     row = row < act.rows ? row : act.rows - 1;
-    __builtin_amdgcn_global_load_lds(act.sa + static_cast<size_t>(am) * act.rows + row, (lds_void*)(srow + wave * 64),
-                                     4, 0, 0);
+    sv = act.sa[static_cast<size_t>(am) * act.rows + row];
   }
   const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
   const int ol = lane & 31;
@@ -198,22 +189,37 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 #pragma unroll
       for (int bj = 0; bj < 2; ++bj) acc[pl][ai][bj] = v16i{};
 
+  // Register sets: stage s lives in set s % 2 from its load (two stages ahead) to its LDS
+  // write (one stage ahead); LDS slot s % 2 holds it while it is multiplied. Loads past the
+  // last stage repeat the last stage (never written to a slot that is read), so every
+  // path through the loop has the same loads in flight and the compiler's vmcnt waits
+  // for a register set let the other set's loads stay outstanding.
+  v4i ra[2][DA];
+  uint32_t rb[2][DB];
+  auto gload = [&](auto setc, int s2) {
+    constexpr int SET = decltype(setc)::value;
 #pragma unroll
-  for (int st = 0; st < S - 1; ++st)
-    if (st < nst) issue_stage<DA, DB, SA, KQ>(asrc, bsrc, lds + st * SS, st0 + st, wave);
-  for (int st = 0; st < nst; ++st) {
-    // this wave's transfers of stage st are complete once at most the later stages'
-    // transfers are outstanding
-    if (st + S - 2 < nst) wait_vm<(S - 2) * D>();
-    else wait_vm<0>();
+    for (int i = 0; i < DA; ++i) ra[SET][i] = *reinterpret_cast<const v4i*>(asrc[i] + (st0 + s2) * 1024 * KQ);
+#pragma unroll
+    for (int i = 0; i < DB; ++i) rb[SET][i] = bsrc[i][(st0 + s2) * 64 * KQ];
+  };
+  auto lwrite = [&](auto setc) {
+    constexpr int SET = decltype(setc)::value;
+    unsigned char* sb = lds + SET * SS;
+#pragma unroll
+    for (int i = 0; i < DA; ++i) *reinterpret_cast<v4i*>(sb + (wave * DA + i) * 1024 + lane * 16) = ra[SET][i];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) *reinterpret_cast<uint32_t*>(sb + SA + (wave * DB + i) * 256 + lane * 4) = rb[SET][i];
+  };
+  // one stage: slot SET is complete once every wave's LDS writes have returned and all
+  // have passed the barrier, which also means every wave has finished reading slot SET ^ 1
+  // (the previous stage), so the next stage goes there
+  auto stage = [&](auto setc, int st) {
+    constexpr int SET = decltype(setc)::value;
+    wait_lds();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // every wave has finished stage st - 1: its slot takes stage st + S - 1
-    if (st + S - 1 < nst)
-      issue_stage<DA, DB, SA, KQ>(asrc, bsrc, lds + ((st + S - 1) % S) * SS, st0 + st + S - 1, wave);
-    const unsigned char* sb = lds + (st % S) * SS;
-    // all LDS reads of the stage first, then the matrix-core work: each read's latency
-    // then overlaps the products of the earlier operands instead of stalling its own
+    const unsigned char* sb = lds + SET * SS;
     uint32_t bw[KQ][2];
     v4i av[KQ][P][2];
 #pragma unroll
@@ -228,6 +234,10 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 #pragma unroll
         for (int ai = 0; ai < 2; ++ai)
           av[kh][pl][ai] = *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * KQ + kh) * 1024 + lane * 16);
+    lwrite(ic<SET ^ 1>{});
+    gload(ic<SET ^ 1>{}, min(st + 3, nst - 1));
+    // all LDS reads of the stage first, then the matrix-core work: each product waits only
+    // for its own operands while the later reads are in flight
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kh = 0; kh < KQ; ++kh) {
@@ -242,7 +252,26 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
           for (int bj = 0; bj < 2; ++bj)
             acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[kh][pl][ai], bop[bj], acc[pl][ai][bj], 0, 0, 0);
     }
-    wait_lds();
+  };
+  if (nst > 0) {
+    gload(ic<0>{}, 0);
+    gload(ic<1>{}, min(1, nst - 1));
+    lwrite(ic<0>{});
+    gload(ic<0>{}, min(2, nst - 1));
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {  // straight-line pairs: the same loads in flight on every path
+      stage(ic<0>{}, st);
+      stage(ic<1>{}, st + 1);
+    }
+    if (st < nst) stage(ic<0>{}, st);
+  }
+  wait_lds();
+  wait_vm<0>();
+  if (MODE == kInt8) {
+    // the scales to LDS for the epilogue (every wave has finished its last stage's reads)
+    __builtin_amdgcn_s_barrier();
+    if (wave * 64 < BM) srow[wave * 64 + lane] = sv;
+    __syncthreads();
   }
 
   if (ksp > 1) {
@@ -421,33 +450,27 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   }
 }
 
-// LDS bytes of a ring of S stages plus the block's row scales.
+// LDS bytes: two slots of one stage each, then the int8 row scales
 template <int MODE, int WM, int WN, int KQ>
-constexpr int ring_bytes(int S) {
-  return S * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
+constexpr int ring_bytes() {
+  return 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
 }
 
-// The device's LDS limit per block (160 KB on gfx950).
 template <int WM, int WN>
 int tiles_of(const GemmArgs& a) {
   const int ng32 = (a.p[0].g.N + 31) / 32;
   return ((ng32 + 2 * WN - 1) / (2 * WN)) * ((a.rows + 64 * WM - 1) / (64 * WM));
 }
 
-// Ring depth 4 (3 stages in flight, up to 80 KB per block). Deeper rings measured slower
-// on the 1.3B shapes: 6 stages of 20 KB in flight on the 32 CUs of an XCD fill its 4 MB L2.
-// With a 64 KB LDS limit the ring falls back to 3 stages.
-template <int WM, int WN>
-constexpr int ring_stages() { return 4; }
-// 32-position k-chunks per stage (one barrier per stage)
-template <int WM, int WN>
-constexpr int ring_kq() { return 2; }
+// 32-position k-chunks per stage (one barrier per stage). 128-position stages measured
+// slower for Int8Absmax (one block per CU instead of two).
+constexpr int kStageKQ = 2;
 
-template <int MODE, int EPI, int WM, int WN, int S, int KQ>
+template <int MODE, int EPI, int WM, int WN, int KQ>
 bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
-  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ>(S);
+  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ>();  // at most 41 KB
   if (bytes > lds_limit()) return false;
-  k_mfma<MODE, EPI, WM, WN, S, KQ><<<grid, dim3(64 * WM * WN), bytes, s>>>(a, act);
+  k_mfma<MODE, EPI, WM, WN, KQ><<<grid, dim3(64 * WM * WN), bytes, s>>>(a, act);
   return true;
 }
 
@@ -476,9 +499,7 @@ hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream
   const int ntile = tiles_of<WM, WN>(a);
   const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
   dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
-  if (!mfma_launch<MODE, EPI, WM, WN, ring_stages<WM, WN>(), ring_kq<WM, WN>()>(a, act, grid, s) &&
-      !mfma_launch<MODE, EPI, WM, WN, 3, 2>(a, act, grid, s))
-    return hipErrorInvalidConfiguration;
+  if (!mfma_launch<MODE, EPI, WM, WN, kStageKQ>(a, act, grid, s)) return hipErrorInvalidConfiguration;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ksplit == 1) return e;
   GemmArgs b = a;
@@ -510,6 +531,7 @@ hipError_t mfma_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
 
 }  // namespace
 
+// The device's LDS limit per block (160 KB on gfx950).
 int lds_limit() {
   static int v = [] {
     int dev = 0, lim = 65536;
