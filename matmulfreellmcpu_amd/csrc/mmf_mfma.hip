@@ -91,10 +91,10 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-template <int MODE, int EPI, int WM, int WN, int KQ>
-__global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
+template <int MODE, int EPI, int WM, int WN, int KQ, int KW>
+__global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
-  constexpr int NW = WM * WN;                   // waves per block
+  constexpr int NW = WM * WN;                   // waves per K-group (one tile)
   constexpr int BM = 64 * WM;                   // rows per block
   constexpr int BG = 2 * WN;                    // physical 32-column groups per block
   constexpr int FR = BM / 32;                   // 32-row fragments
@@ -103,8 +103,9 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   constexpr int DA = P * FR * KQ / NW;          // A transfers per wave per stage
   constexpr int DB = BG * KQ / NW;              // B transfers per wave per stage
   static_assert(DA * NW == P * FR * KQ && DB * NW == BG * KQ, "transfers must split evenly over the waves");
-  extern __shared__ __align__(16) unsigned char lds[];  // [2][SS] slots, then srow[BM]
-  float* srow = reinterpret_cast<float*>(lds + 2 * SS);  // Int8: the block's activation scales
+  static_assert(KW == 1 || NW * 64 * 64 * 4 <= KW * 2 * SS, "the K-group reduction reuses the stage slots");
+  extern __shared__ __align__(16) unsigned char lds[];  // [KW][2][SS] slots, then srow[BM]
+  float* srow = reinterpret_cast<float*>(lds + KW * 2 * SS);  // Int8: the block's activation scales
 
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
@@ -118,7 +119,11 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int ntile = nct * nrt, share = (ntile + 7) / 8;
   const int tile = (blockIdx.x & 7) * share + (blockIdx.x >> 3);
   if (tile >= ntile) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // K-groups: with KW > 1 the block's waves form KW groups of NW waves; group kg multiplies
+  // the kg-th of KW equal runs of the block's stages through its own LDS slots, and the
+  // groups' partial tiles are added in LDS before the epilogue (exact int32 sums)
+  const int kg = (KW > 1) ? (tid >> 6) / NW : 0, wave = (KW > 1) ? (tid >> 6) % NW : (tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int row0 = (tile / nct) * BM;
   const int cgb = (tile % nct) * BG;
@@ -127,6 +132,9 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   const int nall = Lc / (4 * KQ), ksp = gridDim.y, ks = blockIdx.y;
   const int st0 = static_cast<int>((static_cast<long>(nall) * ks) / ksp);
   const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
+  const int cnt = (nst + KW - 1) / KW;           // loop stages of every group
+  const int gb = kg * cnt;                       // the group's first stage (from st0)
+  const int ng = max(0, min(cnt, nst - gb));     // stages the group multiplies
   const int8_t* qbase = act.q + 2 * static_cast<size_t>(am) * act.qplane();
 
   // per-lane sources of this wave's loads (advanced by KQ fragments = KQ KB of the
@@ -156,7 +164,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
   // so their latency hides behind it: per-row int8 scales (one per lane, to LDS after the
   // loop), per-column Q5.10 offsets (128 * rowsum)
   float sv = 0.0f;
-  if (MODE == kInt8 && wave * 64 < BM) {
+  if (MODE == kInt8 && kg == 0 && wave * 64 < BM) {
     int row = row0 + wave * 64 + lane;
     row = row < act.rows ? row : act.rows - 1;
     sv = act.sa[static_cast<size_t>(am) * act.rows + row];
@@ -191,21 +199,23 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
 
   // Register sets: stage s lives in set s % 2 from its load (two stages ahead) to its LDS
   // write (one stage ahead); LDS slot s % 2 holds it while it is multiplied. Loads past the
-  // last stage repeat the last stage (never written to a slot that is read), so every
+  // block's last stage repeat that stage (never written to a slot that is read), so every
   // path through the loop has the same loads in flight and the compiler's vmcnt waits
   // for a register set let the other set's loads stay outstanding.
   v4i ra[2][DA];
   uint32_t rb[2][DB];
+  unsigned char* const gslots = lds + kg * 2 * SS;
   auto gload = [&](auto setc, int s2) {
     constexpr int SET = decltype(setc)::value;
+    const int sg = st0 + min(gb + s2, nst - 1);
 #pragma unroll
-    for (int i = 0; i < DA; ++i) ra[SET][i] = *reinterpret_cast<const v4i*>(asrc[i] + (st0 + s2) * 1024 * KQ);
+    for (int i = 0; i < DA; ++i) ra[SET][i] = *reinterpret_cast<const v4i*>(asrc[i] + sg * 1024 * KQ);
 #pragma unroll
-    for (int i = 0; i < DB; ++i) rb[SET][i] = bsrc[i][(st0 + s2) * 64 * KQ];
+    for (int i = 0; i < DB; ++i) rb[SET][i] = bsrc[i][sg * 64 * KQ];
   };
   auto lwrite = [&](auto setc) {
     constexpr int SET = decltype(setc)::value;
-    unsigned char* sb = lds + SET * SS;
+    unsigned char* sb = gslots + SET * SS;
 #pragma unroll
     for (int i = 0; i < DA; ++i) *reinterpret_cast<v4i*>(sb + (wave * DA + i) * 1024 + lane * 16) = ra[SET][i];
 #pragma unroll
@@ -219,7 +229,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
     wait_lds();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    const unsigned char* sb = lds + SET * SS;
+    const unsigned char* sb = gslots + SET * SS;
     uint32_t bw[KQ][2];
     v4i av[KQ][P][2];
 #pragma unroll
@@ -235,10 +245,11 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
         for (int ai = 0; ai < 2; ++ai)
           av[kh][pl][ai] = *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * KQ + kh) * 1024 + lane * 16);
     lwrite(ic<SET ^ 1>{});
-    gload(ic<SET ^ 1>{}, min(st + 3, nst - 1));
+    gload(ic<SET ^ 1>{}, st + 3);
     // all LDS reads of the stage first, then the matrix-core work: each product waits only
     // for its own operands while the later reads are in flight
     __builtin_amdgcn_sched_barrier(0);
+    if (KW > 1 && st >= ng) return;  // a group past its run (uneven split): loads only
 #pragma unroll
     for (int kh = 0; kh < KQ; ++kh) {
       v4i bop[2];
@@ -253,25 +264,63 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN > 4) ? 1 : 2) void k_mfma(Ge
             acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[kh][pl][ai], bop[bj], acc[pl][ai][bj], 0, 0, 0);
     }
   };
-  if (nst > 0) {
+  if (cnt > 0) {
     gload(ic<0>{}, 0);
-    gload(ic<1>{}, min(1, nst - 1));
+    gload(ic<1>{}, 1);
     lwrite(ic<0>{});
-    gload(ic<0>{}, min(2, nst - 1));
+    gload(ic<0>{}, 2);
     int st = 0;
-    for (; st + 1 < nst; st += 2) {  // straight-line pairs: the same loads in flight on every path
+    for (; st + 1 < cnt; st += 2) {  // straight-line pairs: the same loads in flight on every path
       stage(ic<0>{}, st);
       stage(ic<1>{}, st + 1);
     }
-    if (st < nst) stage(ic<0>{}, st);
+    if (st < cnt) stage(ic<0>{}, st);
   }
   wait_lds();
   wait_vm<0>();
   if (MODE == kInt8) {
     // the scales to LDS for the epilogue (every wave has finished its last stage's reads)
     __builtin_amdgcn_s_barrier();
-    if (wave * 64 < BM) srow[wave * 64 + lane] = sv;
+    if (kg == 0 && wave * 64 < BM) srow[wave * 64 + lane] = sv;
     __syncthreads();
+  }
+  if constexpr (KW > 1) {
+    // K-group reduction: FixedQ510 folds its planes first (hi * 256 + lo into plane 1, as
+    // the split-K partials do), then groups 1..KW-1 in turn hand their tiles to group 0
+    // through the stage slots, free once every wave has passed the barrier
+    if constexpr (MODE == kFixed) {
+#pragma unroll
+      for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            acc[1][ai][bj][i] = acc[0][ai][bj][i] * 256 + acc[1][ai][bj][i];
+            acc[0][ai][bj][i] = 0;
+          }
+    }
+    int32_t* red = reinterpret_cast<int32_t*>(lds);  // [NW][64 values][64 lanes]
+    for (int r = 1; r < KW; ++r) {
+      __syncthreads();
+      if (kg == r) {
+#pragma unroll
+        for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[(wave * 64 + (ai * 2 + bj) * 16 + i) * 64 + lane] = acc[P - 1][ai][bj][i];
+      }
+      __syncthreads();
+      if (kg == 0) {
+#pragma unroll
+        for (int ai = 0; ai < 2; ++ai)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[P - 1][ai][bj][i] += red[(wave * 64 + (ai * 2 + bj) * 16 + i) * 64 + lane];
+      }
+    }
+    if (kg != 0) return;
   }
 
   if (ksp > 1) {
@@ -450,10 +499,10 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   }
 }
 
-// LDS bytes: two slots of one stage each, then the int8 row scales
-template <int MODE, int WM, int WN, int KQ>
+// LDS bytes: two slots of one stage per K-group, then the int8 row scales
+template <int MODE, int WM, int WN, int KQ, int KW>
 constexpr int ring_bytes() {
-  return 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
+  return KW * 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
 }
 
 template <int WM, int WN>
@@ -466,24 +515,31 @@ int tiles_of(const GemmArgs& a) {
 // slower for Int8Absmax (one block per CU instead of two).
 constexpr int kStageKQ = 2;
 
-template <int MODE, int EPI, int WM, int WN, int KQ>
+template <int MODE, int EPI, int WM, int WN, int KQ, int KW>
 bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
-  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ>();  // at most 41 KB
+  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ, KW>();  // at most 97 KB
   if (bytes > lds_limit()) return false;
-  k_mfma<MODE, EPI, WM, WN, KQ><<<grid, dim3(64 * WM * WN), bytes, s>>>(a, act);
+  k_mfma<MODE, EPI, WM, WN, KQ, KW><<<grid, dim3(64 * WM * WN * KW), bytes, s>>>(a, act);
   return true;
 }
 
 // Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
 // that still gives every CU a block (all blocks of all matrices), else 128. Then K is
-// split in powers of two until there are 128 blocks (each split >= 4 stages).
+// split in powers of two until there are 128 blocks (each split >= 4 stages). A GEMM of
+// 49-64 rows with at least kKGroupTiles tiles replaces its split by four K-groups in one
+// block (kw), whose partial tiles meet in LDS: no partials through memory and no split-K
+// epilogue launch. With fewer tiles each block would stream the whole activation range
+// through one CU, which measured slower than the split (64 x 2560 x 2560: 17.8 against
+// 14.1 us; 64 x 2560 x 13824 with 108 tiles: 18.2 against 21.5 us); at 32-48 rows the
+// split was faster on every shape measured (32 x 2048 x 6144: 12.9 against 16.5 us).
 struct Plan {
-  int wm, wn, ksplit;
+  int wm, wn, ksplit, kw;
 };
+constexpr int kKGroupTiles = 48;
 
 Plan plan_of(const GemmArgs& a) {
   const int nz = (a.epi == kEpiSwigluPair) ? 1 : a.nmat;
-  Plan p{a.rows <= 64 ? 1 : 2, 4, 1};
+  Plan p{a.rows <= 64 ? 1 : 2, 4, 1, 1};
   if (p.wm == 1 ? tiles_of<1, 4>(a) * nz < 256 : tiles_of<2, 4>(a) * nz < 256) p.wn = 2;
   const int tiles = (p.wm == 1 ? (p.wn == 4 ? tiles_of<1, 4>(a) : tiles_of<1, 2>(a))
                                : (p.wn == 4 ? tiles_of<2, 4>(a) : tiles_of<2, 2>(a))) * nz;
@@ -491,15 +547,21 @@ Plan plan_of(const GemmArgs& a) {
   // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
+  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && tiles >= kKGroupTiles && nst >= 8) {
+    // (a 4-wave-wide tile never splits: it has >= 256 tiles)
+    p.kw = 4;
+    p.wn = 2;  // 8 waves of 64 x 64 per block: the 512-thread limit of the accumulators' registers
+    p.ksplit = 1;
+  }
   return p;
 }
 
-template <int MODE, int EPI, int WM, int WN>
+template <int MODE, int EPI, int WM, int WN, int KW>
 hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream_t s) {
   const int ntile = tiles_of<WM, WN>(a);
   const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
   dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
-  if (!mfma_launch<MODE, EPI, WM, WN, kStageKQ>(a, act, grid, s)) return hipErrorInvalidConfiguration;
+  if (!mfma_launch<MODE, EPI, WM, WN, kStageKQ, KW>(a, act, grid, s)) return hipErrorInvalidConfiguration;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ksplit == 1) return e;
   GemmArgs b = a;
@@ -515,9 +577,10 @@ template <int MODE, int EPI>
 hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Plan p = plan_of(a);
   const int ks = a.ws ? p.ksplit : 1;
+  if (p.kw == 4) return mfma_inst<MODE, EPI, 1, 2, 4>(a, act, ks, s);
   if (p.wm == 1)
-    return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2>(a, act, ks, s);
-  return p.wn == 4 ? mfma_inst<MODE, EPI, 2, 4>(a, act, ks, s) : mfma_inst<MODE, EPI, 2, 2>(a, act, ks, s);
+    return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2, 1>(a, act, ks, s);
+  return p.wn == 4 ? mfma_inst<MODE, EPI, 2, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 2, 2, 1>(a, act, ks, s);
 }
 
 template <int MODE>

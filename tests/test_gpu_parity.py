@@ -75,6 +75,28 @@ def test_bitlinear_op(eng, oracle, rows, K, N, mode):
     assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
 
 
+@pytest.mark.parametrize("rows", [64, 57])
+@pytest.mark.parametrize("mode", [FIXED, INT8])
+def test_bitlinear_op_kgroups(eng, oracle, rows, mode):
+    """A 64-row tile with 49 column tiles: the matrix-core GEMM runs four K-groups per
+    block and adds their partial tiles in LDS (no split-K partials), ragged rows included."""
+    K, N = 1024, 6176
+    print(f"bitlinear k-groups rows={rows} K={K} N={N} mode={mode}", flush=True)
+    rng = np.random.default_rng(rows * 7 + mode)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, mode)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    dacc = Dev(eng, shape=(rows, N), dtype=np.int32)
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=mode, acc=dacc.ptr)
+    eng.sync()
+    np.testing.assert_array_equal(dacc.get(), want["acc"])
+    assert_bitexact(dout.get(), want["out"], f"bitlinear k-groups out mode {mode}")
+
+
 def test_bitlinear_cluster_matches_single(eng, oracle):
     rng = np.random.default_rng(5)
     rows, K, N = 4, 256, 96
@@ -280,6 +302,30 @@ def test_serve_stacked_matches_oracle(blobs, oracle, mode):
     e.reset(len(prompts))
     streams = [list(p) + [int(t)] for p, t in zip(prompts, e.prefill_streams(prompts))]
     for _ in range(5):
+        nxt = e.step([s[-1] for s in streams])
+        for b in range(len(prompts)):
+            streams[b].append(int(nxt[b]))
+    for b in range(len(prompts)):
+        np.testing.assert_array_equal(np.array(streams[b]), want[b])
+    e.close()
+
+
+@pytest.mark.parametrize("mode", [FIXED, INT8])
+def test_serve_kgroups_matches_oracle(blobs, oracle, mode):
+    """Serving steps of 56 streams whose MLP gate GEMM (6144 columns) runs as K-groups with
+    the swiglu-pair epilogue after the LDS reduction."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    blob = read_blob(blobs("wide"))
+    om = oracle.model(blob)
+    rng = np.random.default_rng(23)
+    prompts = [rng.integers(3, blob.config.vocab_size, 1 + (7 * b) % 12) for b in range(56)]
+    print(f"serve k-groups mode={mode}", flush=True)
+    want = om.generate_serve(prompts, 5, mode)
+    e = Engine(0)
+    e.load_blob(blob, mode)
+    e.reset(len(prompts))
+    streams = [list(p) + [int(t)] for p, t in zip(prompts, e.prefill_streams(prompts))]
+    for _ in range(4):
         nxt = e.step([s[-1] for s in streams])
         for b in range(len(prompts)):
             streams[b].append(int(nxt[b]))
