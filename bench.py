@@ -268,6 +268,8 @@ def main():
     eng = Engine(0)
     devname, cus = eng.device_info()
     log(f"[bench] device {devname}, {cus} CUs")
+    peaks = eng.measure_peaks()
+    log(f"[bench] measured ceilings: {peaks}")
     shapes = [s.strip() for s in args.shapes.split(",") if s.strip()]
     if "370M" not in shapes:
         shapes.insert(0, "370M")
@@ -355,6 +357,7 @@ def main():
         "kernels": {n: r["kernels"] for n, r in results.items()},
         "parity": parity,
         "device": f"{devname}, {cus} CUs",
+        "measured_ceilings": peaks,
     }
     out.update(extra)
     print(json.dumps(out), flush=True)

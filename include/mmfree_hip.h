@@ -189,6 +189,13 @@ int mmf_time_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float
                        float* out, size_t rows, int warmup, int reps, double* total_us,
                        double* prologue_us, double* gemm_us);
 
+/* Device calibration for the rooflines: sustained HBM read bandwidth (GB/s, a 2 GiB buffer),
+ * Infinity Cache read bandwidth (GB/s, a 128 MiB buffer read 8 times), int8 matrix-core rate
+ * (TOP/s, independent v_mfma_i32_32x32x32_i8) and non-packed fp32 FMA rate (TFLOP/s), into
+ * out[0..3]. Each comes from a kernel that does only that work; the context's stream is
+ * synchronized. No counterpart in the reference engine: measurement only. */
+int mmf_measure_peaks(mmf_ctx* ctx, double* out4);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_model_time_prefill": (i, [_vp, _i64p, _sz, i, i, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "mmf_time_bitlinear": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, i, i, C.POINTER(C.c_double),
                                    C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "mmf_measure_peaks": (i, [_vp, C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -300,6 +301,14 @@ class Engine:
         self._chk(self.lib.mmf_model_time_prefill(self.h, ids.ctypes.data_as(_i64p), ids.size, warmup, reps,
                                                   C.byref(total), k if kinds else None))
         return total.value, (dict(zip(self.PREFILL_KINDS, list(k))) if kinds else None)
+
+    def measure_peaks(self):
+        """Measured device ceilings: HBM and Infinity Cache read GB/s, int8 MFMA TOP/s, fp32
+        FMA TFLOP/s (each from a kernel doing only that work)."""
+        v = (C.c_double * 4)()
+        self._chk(self.lib.mmf_measure_peaks(self.h, v))
+        return {"hbm_read_GBps": round(v[0], 1), "mall_read_GBps": round(v[1], 1),
+                "int8_mfma_TOPS": round(v[2], 1), "fp32_fma_TFLOPS": round(v[3], 2)}
 
     def time_bitlinear(self, proj_id, x, out, rows, mode=FLOAT, frac_bits=10, eps=1e-6, warmup=3, reps=20):
         """(total, prologue, gemm) microseconds per mmf_bitlinear call on device buffers."""

@@ -1466,6 +1466,16 @@ int mmf_time_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const 
   });
 }
 
+int mmf_measure_peaks(mmf_ctx* c, double* out4) {
+  return guard(c, [&] {
+    if (!out4) fail(MMF_ERR_ARG, "null output");
+    int dev = 0, cus = 0;
+    MMF_HIP(hipGetDevice(&dev));
+    MMF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    MMF_HIP(measure_peaks(cus, c->stream, out4));
+  });
+}
+
 int mmf_model_time_prefill(mmf_ctx* c, const int64_t* ids, size_t T, int warmup, int reps, double* total_us,
                            double* kind_us) {
   return guard(c, [&] {

@@ -182,6 +182,11 @@ struct GemmArgs {
 // mfma_min_rows() rows on, everything else to the dot-product kernel.
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+
+// ---- device calibration (mmf_peaks.hip) ----------------------------------------------------
+// out = {HBM read GB/s, Infinity Cache read GB/s, int8 MFMA TOP/s, fp32 FMA TFLOP/s}; allocates
+// and frees 2 GiB of scratch, synchronizes the stream.
+hipError_t measure_peaks(int cus, hipStream_t s, double out[4]);
 // Bytes of int32 workspace launch_gemm needs for `a` (0 when it will not split K); the
 // caller passes at least that much in a.ws.
 size_t gemm_workspace_bytes(const GemmArgs& a);
