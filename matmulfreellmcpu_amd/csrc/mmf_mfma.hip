@@ -474,12 +474,29 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       const int o = o0 + (mi ? Nout : 0);
+      // the partials of 8 splits at a time are all loaded before any is added: one memory
+      // round trip per 8 splits instead of one per split
       int32_t s = 0;
-      for (int ks = 0; ks < ksplit; ++ks)
-        s += wsp[(static_cast<size_t>(ks) * nmat + z) * plane + static_cast<size_t>(row) * N + o];
+      const int32_t* wo = wsp + static_cast<size_t>(z) * plane + static_cast<size_t>(row) * N + o;
+      for (int k0 = 0; k0 < ksplit; k0 += 8) {
+        int32_t pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) pv[u] = (k0 + u < ksplit) ? wo[static_cast<size_t>(k0 + u) * nmat * plane] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += pv[u];
+      }
       if (MODE == kFixed) s += 128 * rsum[o];
-      const int32_t* ct = act.ct + ar * 8;
-      for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(tailp[o * 8 + t]) * ct[t];
+      if (ntail) {
+        const int32_t* ct = act.ct + ar * 8;
+        int32_t tw[8], tc[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          tw[t] = (t < ntail) ? static_cast<int32_t>(tailp[o * 8 + t]) : 0;
+          tc[t] = (t < ntail) ? ct[t] : 0;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s += tw[t] * tc[t];
+      }
       tot[mi] = s;
       val[mi] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / (scw * act.sa[ar]);
     }
