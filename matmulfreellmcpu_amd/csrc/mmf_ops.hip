@@ -1040,9 +1040,22 @@ __global__ void k_argmax_rows(const float* __restrict__ lg, int V, int64_t* __re
   __shared__ unsigned long long red[16];
   const float* r = lg + static_cast<size_t>(blockIdx.x) * V;
   unsigned long long best = 0;
-  for (int v = threadIdx.x; v < V; v += blockDim.x) {
-    const unsigned long long k = amax_key(r[v], v);
-    best = k > best ? k : best;
+  // 16 logits per thread loaded before any is compared: one memory round trip per 16
+  // instead of one per logit
+  constexpr int U = 16;
+  for (int v0 = threadIdx.x; v0 < V; v0 += U * blockDim.x) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x;
+      x[u] = v < V ? r[v] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int v = v0 + u * blockDim.x;
+      const unsigned long long k = v < V ? amax_key(x[u], v) : 0ull;
+      best = k > best ? k : best;
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     const unsigned long long other = __shfl_xor(best, o);
