@@ -91,6 +91,15 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// LDS bytes before the int8 row scales: KW groups of two stage slots, or the K-group
+// reduction buffer (one int32 tile per wave of a group) when that is larger.
+template <int MODE, int WM, int WN, int KQ, int KW>
+__host__ __device__ constexpr int lds_main() {
+  const int slots = KW * 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256);
+  const int red = (KW > 1) ? WM * WN * 64 * 64 * 4 : 0;
+  return slots > red ? slots : red;
+}
+
 template <int MODE, int EPI, int WM, int WN, int KQ, int KW>
 __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
@@ -103,9 +112,9 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   constexpr int DA = P * FR * KQ / NW;          // A transfers per wave per stage
   constexpr int DB = BG * KQ / NW;              // B transfers per wave per stage
   static_assert(DA * NW == P * FR * KQ && DB * NW == BG * KQ, "transfers must split evenly over the waves");
-  static_assert(KW == 1 || NW * 64 * 64 * 4 <= KW * 2 * SS, "the K-group reduction reuses the stage slots");
-  extern __shared__ __align__(16) unsigned char lds[];  // [KW][2][SS] slots, then srow[BM]
-  float* srow = reinterpret_cast<float*>(lds + KW * 2 * SS);  // Int8: the block's activation scales
+  constexpr int LB = lds_main<MODE, WM, WN, KQ, KW>();  // stage slots, reused by the K-group reduction
+  extern __shared__ __align__(16) unsigned char lds[];   // [KW][2][SS] slots, then srow[BM]
+  float* srow = reinterpret_cast<float*>(lds + LB);      // Int8: the block's activation scales
 
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
@@ -516,10 +525,10 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   }
 }
 
-// LDS bytes: two slots of one stage per K-group, then the int8 row scales
+// LDS bytes: the stage slots (or the K-group reduction buffer), then the int8 row scales
 template <int MODE, int WM, int WN, int KQ, int KW>
 constexpr int ring_bytes() {
-  return KW * 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256) + 64 * WM * 4;
+  return lds_main<MODE, WM, WN, KQ, KW>() + 64 * WM * 4;
 }
 
 template <int WM, int WN>
@@ -570,6 +579,10 @@ Plan plan_of(const GemmArgs& a) {
     p.wn = 2;  // 8 waves of 64 x 64 per block: the 512-thread limit of the accumulators' registers
     p.ksplit = 1;
   }
+  // 128 x 128 tiles at one block per CU (the 2048-column o/down GEMMs of a long prefill):
+  // two K-groups per block give each SIMD two waves instead of one, with the same tile
+  // and operand traffic
+  if (p.wm == 2 && p.wn == 2 && p.ksplit == 1 && tiles <= 256 && nst >= 8) p.kw = 2;
   return p;
 }
 
@@ -595,6 +608,7 @@ hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Plan p = plan_of(a);
   const int ks = a.ws ? p.ksplit : 1;
   if (p.kw == 4) return mfma_inst<MODE, EPI, 1, 2, 4>(a, act, ks, s);
+  if (p.kw == 2) return mfma_inst<MODE, EPI, 2, 2, 2>(a, act, ks, s);
   if (p.wm == 1)
     return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2, 1>(a, act, ks, s);
   return p.wn == 4 ? mfma_inst<MODE, EPI, 2, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 2, 2, 1>(a, act, ks, s);

@@ -75,14 +75,14 @@ def test_bitlinear_op(eng, oracle, rows, K, N, mode):
     assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
 
 
-@pytest.mark.parametrize("rows", [64, 57])
+@pytest.mark.parametrize("rows,K,N", [(64, 1024, 6176), (57, 1024, 6176), (1030, 512, 2048), (1030, 523, 2048)])
 @pytest.mark.parametrize("mode", [FIXED, INT8])
-def test_bitlinear_op_kgroups(eng, oracle, rows, mode):
-    """A 64-row tile with 49 column tiles: the matrix-core GEMM runs four K-groups per
-    block and adds their partial tiles in LDS (no split-K partials), ragged rows included."""
-    K, N = 1024, 6176
+def test_bitlinear_op_kgroups(eng, oracle, rows, K, N, mode):
+    """K-groups in the matrix-core GEMM: a 64-row tile with 49 column tiles (four groups
+    per block) and 128 x 128 tiles at one block per CU (two groups), ragged rows and a K
+    tail included; the groups' partial tiles are added in LDS."""
     print(f"bitlinear k-groups rows={rows} K={K} N={N} mode={mode}", flush=True)
-    rng = np.random.default_rng(rows * 7 + mode)
+    rng = np.random.default_rng(rows * 7 + K + mode)
     x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
     nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
