@@ -40,6 +40,11 @@
 // matrices), blockIdx.y selects a contiguous range of stages; each block stores its exact
 // int32 partial tile, and k_splitk_epi adds the partials in split order and applies the
 // epilogue (integer sums: the order does not change the result).
+//
+// K-groups (KW > 1): the split can also live inside one block. Its waves form KW groups of
+// WM x WN waves that take equal runs of the stages of the same tile, each through its own
+// LDS slots; group 0 adds the others' int32 tiles from LDS and runs the epilogue. That
+// gives more waves per SIMD (or no partials through memory) with the same tile traffic.
 #include <type_traits>
 
 #include "mmf_device.hpp"
