@@ -374,7 +374,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
   if (segs)
     MMF_HIP(launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H, st));
   else
-    MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, st));
+    MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, trace_dev != nullptr, st));
   tend(c);
   if (trace_dev) {
     const size_t n = static_cast<size_t>(rows) * H * sizeof(float);

@@ -197,10 +197,12 @@ int mfma_min_rows();
 // HGRN gate + recurrence over rows (hgrn_model.cpp:109-150). i, f, g: [rows, H].
 // stream_state = false: rows are time steps of one sequence, state [H] carried in order.
 // stream_state = true: rows are independent streams, state [rows, H].
-// f is overwritten with the gated forget values; scan_out (the recurrence input, [rows, H])
-// is required scratch for a time scan of more than one row and may be null otherwise.
+// keep_gates: f is overwritten with the gated forget values and scan_out receives the
+// recurrence input ([rows, H]; required for a time scan of more than one row). Without it,
+// a time scan with H % 16 == 0 computes the gates inside the scan kernel and leaves f and
+// scan_out untouched.
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
-                        const float* lb, int rows, int H, bool stream_state, hipStream_t s);
+                        const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s);
 // The same over nseg sequences stacked as row segments [off[b], off[b + 1]) (device array of
 // nseg + 1 offsets), segment b scanning from and into state + b * H. Needs H % 8 == 0, so
 // that no element of any segment is a SIMD tail element of the gate math.

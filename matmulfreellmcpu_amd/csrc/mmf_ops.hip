@@ -912,9 +912,16 @@ __device__ __forceinline__ void scan_issue(const float* g, const float* in, floa
   }
 }
 
+// GATE: g and in are the raw f and i projections. The six non-chain waves apply the gate
+// math (sigmoid, lower bound, swiglu; hgrn_model.cpp:113-124, the same functions as k_gate)
+// to each tile in LDS one iteration before the chain wave reads it, so the gated values
+// never go through memory. Tile k + 1 must then be complete at the barrier of iteration k
+// (one tile less in flight), and an extra first iteration converts tile 0. Element tail
+// rules do not arise: this kernel requires H % 16 == 0.
+template <bool GATE>
 __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __restrict__ g, const float* __restrict__ in,
-                                                             float* __restrict__ recur, float* __restrict__ state,
-                                                             int T, int H) {
+                                                             const float* __restrict__ lb, float* __restrict__ recur,
+                                                             float* __restrict__ state, int T, int H) {
   extern __shared__ __align__(16) float sm[];
   float* ring = sm;                                      // [kScNR][2][kScTT][16]
   float* R = sm + kScNR * 2 * kScTT * kScCols;           // [2][kScTT][16]
@@ -923,21 +930,46 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
   const int ntiles = (T + kScTT - 1) / kScTT;
   const bool loader = wave >= 1 && wave <= 4;
   float s = (wave == 0 && lane < kScCols) ? state[c0 + lane] : 0.0f;
+  // GATE: the column a gate lane converts is fixed (384 lanes, 16 columns per tile row)
+  const float lbc = (GATE && wave >= 1 && lb) ? lb[c0 + (threadIdx.x - 64) % kScCols] : 0.0f;
   if (loader)
     for (int t = 0; t < kScNR - 1 && t < ntiles; ++t) scan_issue(g, in, ring, t, t, T, H, c0, wave - 1, lane);
-  for (int k = 0; k <= ntiles; ++k) {
-    // this wave's LDS writes (wave 0's results) have landed before the barrier publishes them
+  for (int k = GATE ? -1 : 0; k <= ntiles; ++k) {
+    // this wave's LDS writes (wave 0's results, converted gates) have landed before the
+    // barrier publishes them
     __builtin_amdgcn_s_waitcnt(0xC07F);
     if (loader) {
-      // this wave's transfers of tile k are done once only later tiles' are outstanding
-      if (k + kScNR - 2 < ntiles) __builtin_amdgcn_s_waitcnt(((kScNR - 2) * 4 & 0xF) | (((kScNR - 2) * 4 >> 4) << 14) | 0x0F70);
-      else __builtin_amdgcn_s_waitcnt(0x0F70);
+      // this wave's transfers of tile k (GATE: k + 1) are done once only later tiles' are
+      // outstanding
+      if (GATE) {
+        if (k >= 0 && k + kScNR - 2 < ntiles)
+          __builtin_amdgcn_s_waitcnt(((kScNR - 3) * 4 & 0xF) | (((kScNR - 3) * 4 >> 4) << 14) | 0x0F70);
+        else
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+      } else {
+        if (k + kScNR - 2 < ntiles)
+          __builtin_amdgcn_s_waitcnt(((kScNR - 2) * 4 & 0xF) | (((kScNR - 2) * 4 >> 4) << 14) | 0x0F70);
+        else
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
     }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    if (loader && k + kScNR - 1 < ntiles)
+    if (loader && k >= 0 && k + kScNR - 1 < ntiles)
       scan_issue(g, in, ring, k + kScNR - 1, (k + kScNR - 1) % kScNR, T, H, c0, wave - 1, lane);
-    if (wave == 0 && k < ntiles && lane < kScCols) {
+    if (GATE && wave >= 1 && k + 1 < ntiles) {
+      // gate math on tile k + 1, in place: g' = sigmoid(f) (then the lower bound), in =
+      // swiglu(i, 1 - g')
+      float* Gt = ring + (((k + 1) % kScNR) * 2 + 0) * kScTT * kScCols;
+      float* It = ring + (((k + 1) % kScNR) * 2 + 1) * kScTT * kScCols;
+      for (int e = threadIdx.x - 64; e < kScTT * kScCols; e += 64 * (kScWaves - 1)) {
+        float gg = sigmoid_of(Gt[e], false);
+        if (lb) gg = __builtin_fmaf(1.0f - lbc, gg, lbc);
+        It[e] = swiglu_of(It[e], 1.0f - gg, false);
+        Gt[e] = gg;
+      }
+    }
+    if (wave == 0 && k >= 0 && k < ntiles && lane < kScCols) {
       const float* G = ring + ((k % kScNR) * 2 + 0) * kScTT * kScCols;
       const float* I = ring + ((k % kScNR) * 2 + 1) * kScTT * kScCols;
       float* Rt = R + (k & 1) * kScTT * kScCols;
@@ -1271,7 +1303,14 @@ hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
 }
 
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
-                        const float* lb, int rows, int H, bool stream_state, hipStream_t s) {
+                        const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s) {
+  if (!stream_state && !keep_gates && rows > 1 && H % kScCols == 0 &&
+      ((reinterpret_cast<uintptr_t>(i) | reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(recur)) & 15) == 0) {
+    // one kernel: the gate math runs inside the scan on each tile (k_scan_ring<true>)
+    const size_t lds = (static_cast<size_t>(kScNR) * 2 + 2) * kScTT * kScCols * sizeof(float);
+    k_scan_ring<true><<<H / kScCols, 64 * kScWaves, lds, s>>>(f, i, lb, recur, state, rows, H);
+    return hipGetLastError();
+  }
   if (!stream_state && scan_out && rows > 1) {
     const size_t n = static_cast<size_t>(rows) * H;
     const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
@@ -1282,7 +1321,7 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
                            reinterpret_cast<uintptr_t>(recur)) & 15) == 0;
     if (H % kScCols == 0 && aligned) {
       const size_t lds = (static_cast<size_t>(kScNR) * 2 + 2) * kScTT * kScCols * sizeof(float);
-      k_scan_ring<<<H / kScCols, 64 * kScWaves, lds, s>>>(f, scan_out, recur, state, rows, H);
+      k_scan_ring<false><<<H / kScCols, 64 * kScWaves, lds, s>>>(f, scan_out, nullptr, recur, state, rows, H);
     } else {
       k_scan_seq<<<(H + 63) / 64, 64, 0, s>>>(f, scan_out, recur, state, rows, H);
     }
