@@ -372,7 +372,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
   // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
   tbeg(c, kRkMixer);
   if (segs)
-    MMF_HIP(launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H, st));
+    MMF_HIP(launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H, trace_dev != nullptr, st));
   else
     MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, trace_dev != nullptr, st));
   tend(c);

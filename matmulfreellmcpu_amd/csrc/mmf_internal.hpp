@@ -205,9 +205,10 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
                         const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s);
 // The same over nseg sequences stacked as row segments [off[b], off[b + 1]) (device array of
 // nseg + 1 offsets), segment b scanning from and into state + b * H. Needs H % 8 == 0, so
-// that no element of any segment is a SIMD tail element of the gate math.
+// that no element of any segment is a SIMD tail element of the gate math. keep_gates as
+// for launch_mixer (without it the gate math runs inside the segment scan).
 hipError_t launch_mixer_segs(const float* i, float* f, float* scan, float* recur, float* state, const float* lb,
-                             const int* off, int nseg, int rows, int H, hipStream_t s);
+                             const int* off, int nseg, int rows, int H, bool keep_gates, hipStream_t s);
 // rows idx[r] (device) of x [*, K] -> out [n, K]
 hipError_t launch_gather_rows(const float* x, const int* idx, float* out, int n, int K, hipStream_t s);
 

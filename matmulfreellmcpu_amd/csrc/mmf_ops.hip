@@ -851,14 +851,18 @@ __global__ __launch_bounds__(64) void k_scan_seq(const float* __restrict__ g, co
 // the serving streams): segment b = rows [off[b], off[b + 1]) starts from state b
 // (state + b * H) and leaves its last value there. One thread per (column, segment); each
 // segment is scanned in time order exactly as k_scan_seq scans one sequence.
+// GATE: g and in are the raw f and i projections and the gate math (k_gate's arithmetic,
+// no element tail since H % 8 == 0) runs on each step beside the chain.
+template <bool GATE>
 __global__ __launch_bounds__(64) void k_scan_segs(const float* __restrict__ g, const float* __restrict__ in,
-                                                  float* __restrict__ recur, float* __restrict__ state,
-                                                  const int* __restrict__ off, int H) {
+                                                  const float* __restrict__ lb, float* __restrict__ recur,
+                                                  float* __restrict__ state, const int* __restrict__ off, int H) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= H) return;
   const int b = blockIdx.y, t0 = off[b], t1 = off[b + 1];
   float* st = state + static_cast<size_t>(b) * H;
   float s = st[c];
+  const float lbc = (GATE && lb) ? lb[c] : 0.0f;
   constexpr int U = 16;
   for (int t = t0; t < t1; t += U) {
     float gc[U], ic[U];
@@ -871,7 +875,13 @@ __global__ __launch_bounds__(64) void k_scan_segs(const float* __restrict__ g, c
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (t + u < t1) {
-        s = __builtin_fmaf(gc[u], s, ic[u]);
+        float gg = gc[u], xin = ic[u];
+        if (GATE) {
+          gg = sigmoid_of(gg, false);
+          if (lb) gg = __builtin_fmaf(1.0f - lbc, gg, lbc);
+          xin = swiglu_of(xin, 1.0f - gg, false);
+        }
+        s = __builtin_fmaf(gg, s, xin);
         recur[static_cast<size_t>(t + u) * H + c] = s;
       }
     }
@@ -1333,14 +1343,18 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
 }
 
 hipError_t launch_mixer_segs(const float* i, float* f, float* scan, float* recur, float* state, const float* lb,
-                             const int* off, int nseg, int rows, int H, hipStream_t s) {
+                             const int* off, int nseg, int rows, int H, bool keep_gates, hipStream_t s) {
   if (H % 8 != 0) return hipErrorInvalidValue;  // a SIMD tail per segment would differ
+  if (!keep_gates) {  // one kernel: the gate math beside each segment's chain
+    k_scan_segs<true><<<dim3((H + 63) / 64, nseg), 64, 0, s>>>(f, i, lb, recur, state, off, H);
+    return hipGetLastError();
+  }
   const size_t n = static_cast<size_t>(rows) * H;
   const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 16384));
   k_gate<<<blocks, 256, 0, s>>>(i, f, scan, lb, rows, H);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  k_scan_segs<<<dim3((H + 63) / 64, nseg), 64, 0, s>>>(f, scan, recur, state, off, H);
+  k_scan_segs<false><<<dim3((H + 63) / 64, nseg), 64, 0, s>>>(f, scan, nullptr, recur, state, off, H);
   return hipGetLastError();
 }
 
