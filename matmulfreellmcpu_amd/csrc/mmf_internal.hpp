@@ -182,6 +182,10 @@ struct GemmArgs {
 // mfma_min_rows() rows on, everything else to the dot-product kernel.
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+// Float mode on the fp32 matrix cores (mmf_mfma_f.hip), bit-exact with the FMA chains;
+// used from float_mfma_min_rows() rows on when mfma_f_ok(a).
+bool mfma_f_ok(const GemmArgs& a);
+hipError_t launch_gemm_mfma_f(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 
 // ---- device calibration (mmf_peaks.hip) ----------------------------------------------------
 // out = {HBM read GB/s, Infinity Cache read GB/s, int8 MFMA TOP/s, fp32 FMA TFLOP/s}; allocates
@@ -193,6 +197,9 @@ size_t gemm_workspace_bytes(const GemmArgs& a);
 // Rows from which the integer modes use the matrix cores (MMF_MFMA_MIN_ROWS, default 8;
 // 0 disables them).
 int mfma_min_rows();
+// Rows from which float mode uses the fp32 matrix cores (MMF_FLOAT_MFMA_MIN_ROWS, default
+// 16; 0 disables them).
+int float_mfma_min_rows();
 
 // HGRN gate + recurrence over rows (hgrn_model.cpp:109-150). i, f, g: [rows, H].
 // stream_state = false: rows are time steps of one sequence, state [H] carried in order.

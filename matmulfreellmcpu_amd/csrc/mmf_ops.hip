@@ -1276,6 +1276,8 @@ static hipError_t gemm_f_rows(const GemmArgs& a, const ActBuf& act, hipStream_t 
 
 template <int MODE>
 static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  if (MODE == kFloat && float_mfma_min_rows() > 0 && a.rows >= float_mfma_min_rows() && mfma_f_ok(a))
+    return launch_gemm_mfma_f(a, act, s);
   if (MODE == kFloat && a.rows > 4) {
     const bool pair = a.epi == kEpiSwigluPair;
     // up to 64 rows (serving steps): 4-row tiles, so that the >= 1024-block rule keeps two
@@ -1288,6 +1290,14 @@ static hipError_t gemm_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s)
   if (a.rows <= 1) return pair ? gemm_inst<MODE, 1, true>(a, act, s) : gemm_inst<MODE, 1, false>(a, act, s);
   if (a.rows <= 4) return pair ? gemm_inst<MODE, 4, true>(a, act, s) : gemm_inst<MODE, 4, false>(a, act, s);
   return pair ? gemm_inst<MODE, 8, true>(a, act, s) : gemm_inst<MODE, 8, false>(a, act, s);
+}
+
+int float_mfma_min_rows() {
+  static const int v = [] {
+    const char* e = std::getenv("MMF_FLOAT_MFMA_MIN_ROWS");
+    return e ? std::atoi(e) : 16;
+  }();
+  return v;
 }
 
 int mfma_min_rows() {

@@ -97,6 +97,25 @@ def test_bitlinear_op_kgroups(eng, oracle, rows, K, N, mode):
     assert_bitexact(dout.get(), want["out"], f"bitlinear k-groups out mode {mode}")
 
 
+@pytest.mark.parametrize("rows,K,N", [(16, 64, 64), (64, 1024, 2560), (100, 1031, 333), (1030, 523, 2048),
+                                      (2048, 256, 1000)])
+def test_bitlinear_op_float_mfma(eng, oracle, rows, K, N):
+    """Float mode on the fp32 matrix cores: 8 chains per wave (wide launches) and 2 chains per
+    wave with the partial tiles added in LDS (narrow ones), ragged rows and columns, K tails."""
+    print(f"bitlinear float mfma rows={rows} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(rows * 3 + K + N)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, FLOAT)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=FLOAT)
+    eng.sync()
+    assert_bitexact(dout.get(), want["out"], "bitlinear float mfma")
+
+
 def test_measured_ceilings(eng):
     """The calibration kernels run and give rates below the published peaks (HBM 8 TB/s,
     int8 dense 5.0 POP/s, fp32 vector FMA without packing 78.6 TFLOP/s) and well above zero."""
