@@ -18,18 +18,21 @@
 //
 // Operands. Activations are the fp32 chain rows of the prologue (row r, chain j, position
 // t at y[r * (8 Lc + 8) + j * Lc + t]); a block stages the 16 rows x 8 chains x 16 positions
-// of one chunk in LDS (double-buffered, loaded a chunk ahead through registers), and each
+// of one chunk in one of two LDS slots (loaded several chunks ahead into register sets), and each
 // lane reads 4 positions of one chain per ds_read_b128. Weights are the 2-bit slabs of the
 // GEMV path: the word (group n / 16, chunk c, output n % 16, chain j) holds the 16 codes of
 // chain j at t = 16c .. 16c + 15, one v_bfe_i32 + v_cvt_f32_i32 per code.
 //
-// Chains per wave (CW):
-//   CW = 8: each of the 4 waves owns 64 columns and all 8 chains (128 accumulator
-//           registers) and reduces them in registers: a 16 x 256 block tile;
-//   CW = 2: the 4 waves share one 16 x 64 tile, wave w running chains w and w + 4, for
-//           launches with too few tiles to fill the chip (serving steps). Each wave adds
-//           its two chains (a_w + a_{w+4}, the first level of hsum_ps) and wave 0 adds the
-//           four partial tiles through LDS in the remaining order.
+// Tiling: RM 16-row subtiles per wave share each decoded weight; the 8 chains of a tile are
+// split over 8 / CW waves of a block (CW chains each), so the accumulators (RM x CW x 16
+// registers) stay within 128 and two waves fit per SIMD:
+//   RM = 2, CW = 4 (long row ranges, prefill): a block is 32 rows x 128 columns; the wave
+//           pair of a column group runs chains {0, 4, 1, 5} and {2, 6, 3, 7};
+//   RM = 1, CW = 2 (a few dozen rows, serving steps): a block is 16 rows x 64 columns, wave
+//           w runs chains w and w + 4, so the launch has 4x the waves per column.
+// Each wave adds its chains in pairs (a_j + a_{j+4}, the first level of hsum_ps), and the
+// wave of the column group with the first chains adds the other partial tiles through LDS in
+// the remaining order.
 // Epilogues: store, residual add, and the MLP pair (wave columns 0..31 gate outputs c0 ..
 // c0+31, columns 32..63 their up partners N/2 later: swiglu in registers).
 #include "mmf_device.hpp"
@@ -41,14 +44,17 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kFT = 16;                   // rows of a tile
-constexpr int kFRS = 8 * 16 + 4;          // LDS floats per staged row (8 chains x 16, padded)
-constexpr int kFBuf = kFT * kFRS;         // LDS floats per chunk buffer
+constexpr int kFRS = 8 * 16 + 4;  // LDS floats per staged row (8 chains x 16 positions, padded)
+// register sets of chunk loads in flight: a 16-row tile's chunk is ~0.5 us of matrix work
+// (2 chains per wave), short against a load from HBM or another XCD's writes (the serving
+// steps stream every layer's weights), so those tiles keep more chunks in flight
+template <int CW> constexpr int f_stages() { return CW == 2 ? 3 : 2; }
 
-template <int EPI, int CW>
+template <int EPI, int RM, int CW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f(GemmArgs a, ActBuf act) {
+  static_assert(CW != 2 || RM == 1, "two chains per wave: one 16-row subtile");
   constexpr bool PAIR = EPI == kEpiSwigluPair;
-  constexpr int NC = CW;                  // accumulators (chains) per wave
+  constexpr int NC = CW, TR = 16 * RM, S = f_stages<CW>(), BUFF = TR * kFRS, WH = 8 / CW, WCOL = 4 / WH;
   extern __shared__ float smem[];
   const int z = blockIdx.z;
   const ProjDev& P = a.p[z];
@@ -56,27 +62,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int Lc = act.Lc, Wc = g.Wc;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row0 = blockIdx.y * kFT;
+  const int wh = wv % WH, wc = wv / WH;
+  const int row0 = blockIdx.y * TR;
   const int am = (act.na > 1) ? z : 0;
   const int N = g.N, Nh = N / 2;
-  // this lane's B column (weight row) and the tile's column base
-  int n;
+  // this lane's B column (weight row) and the wave's first output column
+  int n, cbase;
   bool nok;
-  int cbase;  // PAIR: first gate column of the wave; else first column of the wave
   if (PAIR) {
-    cbase = (blockIdx.x * (CW == 8 ? 4 : 1) + (CW == 8 ? wv : 0)) * 32;
+    cbase = (blockIdx.x * WCOL + wc) * 32;
     const int c = cbase + (lane & 31);
     nok = c < Nh;
     n = (lane < 32) ? c : Nh + c;
   } else {
-    cbase = (blockIdx.x * (CW == 8 ? 4 : 1) + (CW == 8 ? wv : 0)) * 64;
+    cbase = (blockIdx.x * WCOL + wc) * 64;
     n = cbase + lane;
     nok = n < N;
   }
-  // chains of this wave
   int jc[NC];
 #pragma unroll
-  for (int q = 0; q < NC; ++q) jc[q] = (CW == 8) ? q : wv + 4 * q;
+  for (int q = 0; q < NC; ++q) {
+    if (CW == 8) jc[q] = q;
+    else if (CW == 4) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
+    else jc[q] = wh + 4 * q;                                     // {wh, wh+4}
+  }
   const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
   auto load_w = [&](int c, uint32_t (&w)[NC]) {
     if constexpr (CW == 8) {
@@ -89,80 +98,157 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       for (int q = 0; q < NC; ++q) w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
     }
   };
-  // activation tile loads: 512 float4 per chunk, two per thread
+  // activation tile loads: TR rows x 8 chains x 4 float4 per chunk, 2 RM per thread
   const float* ybase = act.y + (static_cast<size_t>(am) * act.rows + row0) * act.ystride();
-  const int nrows = min(kFT, a.rows - row0);
-  int ge_off[2], ls_off[2];
-  bool ge_ok[2];
+  const int nrows = min(TR, a.rows - row0);
+  constexpr int NL = 2 * RM;
+  int ge_off[NL], ls_off[NL];
+  bool ge_ok[NL];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < NL; ++h) {
     const int e = tid + 256 * h, r = e >> 5, ch = (e >> 2) & 7, f4 = e & 3;
     ge_ok[h] = r < nrows;
     ge_off[h] = r * static_cast<int>(act.ystride()) + ch * Lc + 4 * f4;
     ls_off[h] = r * kFRS + ch * 16 + 4 * f4;
   }
-  auto load_y = [&](int c, float4 (&v)[2]) {
+  auto load_y = [&](int c, float4 (&v)[NL]) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NL; ++h)
       v[h] = ge_ok[h] ? *reinterpret_cast<const float4*>(ybase + ge_off[h] + 16 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
   };
-  v16f acc[NC];
+  v16f acc[RM][NC];
 #pragma unroll
-  for (int q = 0; q < NC; ++q) acc[q] = v16f{};
-  uint32_t wcur[NC], wnext[NC];
-  float4 ynext[2];
-  load_w(0, wcur);
-  load_y(0, ynext);
+  for (int m = 0; m < RM; ++m)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) *reinterpret_cast<float4*>(smem + ls_off[h]) = ynext[h];
-  __syncthreads();
-  const int ri = lane & 15;  // this lane's A row within the tile
-  for (int c = 0; c < Wc; ++c) {
-    const int buf = c & 1;
-    const bool more = c + 1 < Wc;
-    if (more) {
-      load_w(c + 1, wnext);
-      load_y(c + 1, ynext);
-    }
-    const float* yl = smem + buf * kFBuf + ri * kFRS;
+    for (int q = 0; q < NC; ++q) acc[m][q] = v16f{};
+  const int ri = lane & 15;  // this lane's A row within a subtile
+  if constexpr (CW == 2) {
+    // Each wave's two chains are its own: no activation is shared between the waves of the
+    // block, so every wave loads its operands straight into registers (S chunks in flight)
+    // and runs without barriers. Lanes l, l + 16, l + 32, l + 48 read the same row.
+    const bool rok = row0 + ri < a.rows;
+    const float* yrow = ybase + static_cast<size_t>(ri) * act.ystride();
+    auto load_a = [&](int c, float4 (&v)[NC][4]) {
 #pragma unroll
-    for (int tq = 0; tq < 4; ++tq) {
-      float4 av[NC];
+      for (int q = 0; q < NC; ++q)
 #pragma unroll
-      for (int q = 0; q < NC; ++q) av[q] = *reinterpret_cast<const float4*>(yl + jc[q] * 16 + 4 * tq);
+        for (int tq = 0; tq < 4; ++tq)
+          v[q][tq] = rok ? *reinterpret_cast<const float4*>(yrow + jc[q] * Lc + 16 * c + 4 * tq)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    float4 ar[S][NC][4];
+    uint32_t wr[S][NC];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+    for (int u = 0; u < S; ++u)
+      if (u < Wc) {
+        load_a(u, ar[u]);
+        load_w(u, wr[u]);
+      }
+    for (int c0 = 0; c0 < Wc; c0 += S) {
 #pragma unroll
-        for (int q = 0; q < NC; ++q) {
-          const float y = tt == 0 ? av[q].x : tt == 1 ? av[q].y : tt == 2 ? av[q].z : av[q].w;
-          acc[q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(wcur[q], 4 * tq + tt), acc[q], 0, 0, 0);
+      for (int u = 0; u < S; ++u) {
+        const int c = c0 + u;
+        if (c >= Wc) break;
+#pragma unroll
+        for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int q = 0; q < NC; ++q) {
+              const float4 v = ar[u][q][tq];
+              const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+              acc[0][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(wr[u][q], 4 * tq + tt), acc[0][q], 0, 0, 0);
+            }
+        if (c + S < Wc) {
+          load_a(c + S, ar[u]);
+          load_w(c + S, wr[u]);
         }
       }
     }
-    if (more) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) *reinterpret_cast<float4*>(smem + (buf ^ 1) * kFBuf + ls_off[h]) = ynext[h];
-#pragma unroll
-      for (int q = 0; q < NC; ++q) wcur[q] = wnext[q];
-    }
+  } else {
+    // S register sets in flight: set u holds the activations and weights of the chunks
+    // c = u (mod S). Chunk c's activations are loaded at the top of iteration c - S, written to
+    // LDS slot (c & 1) at the bottom of iteration c - 1; its weights are loaded at the bottom of
+    // iteration c - S and used in iteration c. The loop body is unrolled S times so that every
+    // set index is a compile-time constant.
+    float4 yr[S][NL];
+    uint32_t wr[S][NC];
+  #pragma unroll
+    for (int u = 0; u < S; ++u)
+      if (u < Wc) {
+        load_y(u, yr[u]);
+        load_w(u, wr[u]);
+      }
+  #pragma unroll
+    for (int h = 0; h < NL; ++h) *reinterpret_cast<float4*>(smem + ls_off[h]) = yr[0][h];
     __syncthreads();
+    for (int c0 = 0; c0 < Wc; c0 += S) {
+  #pragma unroll
+      for (int u = 0; u < S; ++u) {
+        const int c = c0 + u;
+        if (c >= Wc) break;
+        const float* yb = smem + (c & 1) * BUFF + ri * kFRS;
+        if (c + S < Wc) load_y(c + S, yr[u]);
+  #pragma unroll
+        for (int tq = 0; tq < 4; ++tq) {
+          float4 av[RM][NC];
+  #pragma unroll
+          for (int m = 0; m < RM; ++m)
+  #pragma unroll
+            for (int q = 0; q < NC; ++q) av[m][q] = *reinterpret_cast<const float4*>(yb + 16 * m * kFRS + jc[q] * 16 + 4 * tq);
+  #pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+  #pragma unroll
+            for (int q = 0; q < NC; ++q) {
+              const float b = code_f(wr[u][q], 4 * tq + tt);
+  #pragma unroll
+              for (int m = 0; m < RM; ++m) {
+                const float y = tt == 0 ? av[m][q].x : tt == 1 ? av[m][q].y : tt == 2 ? av[m][q].z : av[m][q].w;
+                acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, b, acc[m][q], 0, 0, 0);
+              }
+            }
+          }
+        }
+        if (c + 1 < Wc) {
+  #pragma unroll
+          for (int h = 0; h < NL; ++h)
+            *reinterpret_cast<float4*>(smem + ((c + 1) & 1) * BUFF + ls_off[h]) = yr[(u + 1) % S][h];
+        }
+        if (c + S < Wc) load_w(c + S, wr[u]);
+        __syncthreads();
+      }
+    }
   }
   // ---- chain reduction in the hsum_ps order --------------------------------------------
-  float val[16];
+  float val[RM][16];
   if constexpr (CW == 8) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      val[r] = ((acc[0][r] + acc[4][r]) + (acc[1][r] + acc[5][r])) + ((acc[2][r] + acc[6][r]) + (acc[3][r] + acc[7][r]));
+    for (int m = 0; m < RM; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        val[m][r] = ((acc[m][0][r] + acc[m][4][r]) + (acc[m][1][r] + acc[m][5][r])) +
+                    ((acc[m][2][r] + acc[m][6][r]) + (acc[m][3][r] + acc[m][7][r]));
   } else {
-    // partial s_w = a_w + a_{w+4}; LDS [w][r][lane]; wave 0 finishes (s0 + s1) + (s2 + s3)
+    // partial tiles in LDS [wc][wh][m][r][lane]: CW = 4: s_{2wh} + s_{2wh+1}; CW = 2: s_wh
+    constexpr int PS = RM * 16 * 64;  // floats of one wave's partial tile
 #pragma unroll
-    for (int r = 0; r < 16; ++r) smem[(wv * 16 + r) * 64 + lane] = acc[0][r] + acc[1][r];
+    for (int m = 0; m < RM; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = (CW == 4) ? (acc[m][0][r] + acc[m][1][r]) + (acc[m][2][r] + acc[m][3][r])
+                                  : acc[m][0][r] + acc[m][1][r];
+        smem[(wc * WH + wh) * PS + (m * 16 + r) * 64 + lane] = p;
+      }
     __syncthreads();
-    if (wv != 0) return;
+    if (wh != 0) return;
+    const float* rp = smem + wc * WH * PS + lane;
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      val[r] = (smem[(0 * 16 + r) * 64 + lane] + smem[(1 * 16 + r) * 64 + lane]) +
-               (smem[(2 * 16 + r) * 64 + lane] + smem[(3 * 16 + r) * 64 + lane]);
+    for (int m = 0; m < RM; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = (m * 16 + r) * 64;
+        val[m][r] = (CW == 4) ? rp[o] + rp[PS + o] : (rp[o] + rp[PS + o]) + (rp[2 * PS + o] + rp[3 * PS + o]);
+      }
   }
   // ---- tails, scale, epilogue ----------------------------------------------------------
   const int col = lane & 15, rq = 4 * (lane >> 4);
@@ -175,51 +261,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
     return s * P.inv_scale_w;
   };
-  if (PAIR) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int row = row0 + rq + (r & 3);
-      const int c = cbase + 16 * (r >> 2) + col;
-      if (row >= a.rows || c >= Nh) continue;
-      const float vg = finish(val[r], c, row), vu = finish(val[r + 8], Nh + c, row);
-      const size_t e = static_cast<size_t>(row) * Nh + c;
-      a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
-    }
-  } else {
+  for (int m = 0; m < RM; ++m) {
+    if (PAIR) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = row0 + rq + (r & 3);
-      const int o = cbase + 16 * (r >> 2) + col;
-      if (row >= a.rows || o >= N) continue;
-      const float v = finish(val[r], o, row);
-      const size_t e = static_cast<size_t>(row) * N + o;
-      a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
+      for (int r = 0; r < 8; ++r) {
+        const int row = row0 + 16 * m + rq + (r & 3);
+        const int c = cbase + 16 * (r >> 2) + col;
+        if (row >= a.rows || c >= Nh) continue;
+        const float vg = finish(val[m][r], c, row), vu = finish(val[m][r + 8], Nh + c, row);
+        const size_t e = static_cast<size_t>(row) * Nh + c;
+        a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + 16 * m + rq + (r & 3);
+        const int o = cbase + 16 * (r >> 2) + col;
+        if (row >= a.rows || o >= N) continue;
+        const float v = finish(val[m][r], o, row);
+        const size_t e = static_cast<size_t>(row) * N + o;
+        a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
+      }
     }
   }
 }
 
-template <int EPI, int CW>
+template <int EPI, int RM, int CW>
+long mfma_f_blocks(const GemmArgs& a) {
+  const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW / 2);
+  const int cols = EPI == kEpiSwigluPair ? a.p[0].g.N / 2 : a.p[0].g.N;
+  return static_cast<long>((cols + per - 1) / per) * ((a.rows + 16 * RM - 1) / (16 * RM)) *
+         (EPI == kEpiSwigluPair ? 1 : a.nmat);
+}
+
+template <int EPI, int RM, int CW>
 hipError_t mfma_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Geom& g = a.p[0].g;
-  const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW == 8 ? 4 : 1);
+  const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW / 2);
   const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
-  dim3 grid((cols + per - 1) / per, (a.rows + kFT - 1) / kFT, EPI == kEpiSwigluPair ? 1 : a.nmat);
-  const size_t lds = 2 * kFBuf * sizeof(float);  // also holds CW = 2's 4 x 16 x 64 partials
-  static_assert(2 * kFBuf >= 4 * 16 * 64, "reduction buffer");
-  k_mfma_f<EPI, CW><<<grid, 256, lds, s>>>(a, act);
+  dim3 grid((cols + per - 1) / per, (a.rows + 16 * RM - 1) / (16 * RM), EPI == kEpiSwigluPair ? 1 : a.nmat);
+  const size_t ring = static_cast<size_t>(2) * 16 * RM * kFRS * sizeof(float);
+  const size_t red = CW == 8 ? 0 : static_cast<size_t>(4) * RM * 16 * 64 * sizeof(float);
+  k_mfma_f<EPI, RM, CW><<<grid, 256, ring > red ? ring : red, s>>>(a, act);
   return hipGetLastError();
 }
 
+// 32 x 128 block tiles while that leaves at least 1024 blocks (four per CU), else 16 x 64
 template <int EPI>
 hipError_t mfma_f_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
-  const Geom& g = a.p[0].g;
-  const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
-  const int per8 = (EPI == kEpiSwigluPair ? 32 : 64) * 4;
-  const long blocks8 = static_cast<long>((cols + per8 - 1) / per8) * ((a.rows + kFT - 1) / kFT) *
-                       (EPI == kEpiSwigluPair ? 1 : a.nmat);
-  // all 8 chains per wave while that gives at least two blocks per CU
-  if (blocks8 >= 512) return mfma_f_inst<EPI, 8>(a, act, s);
-  return mfma_f_inst<EPI, 2>(a, act, s);
+  if (mfma_f_blocks<EPI, 2, 4>(a) >= 1024) return mfma_f_inst<EPI, 2, 4>(a, act, s);
+  return mfma_f_inst<EPI, 1, 2>(a, act, s);
 }
 
 }  // namespace

@@ -98,10 +98,11 @@ def test_bitlinear_op_kgroups(eng, oracle, rows, K, N, mode):
 
 
 @pytest.mark.parametrize("rows,K,N", [(16, 64, 64), (64, 1024, 2560), (100, 1031, 333), (1030, 523, 2048),
-                                      (2048, 256, 1000)])
+                                      (1030, 523, 8192), (2048, 256, 4008)])
 def test_bitlinear_op_float_mfma(eng, oracle, rows, K, N):
-    """Float mode on the fp32 matrix cores: 8 chains per wave (wide launches) and 2 chains per
-    wave with the partial tiles added in LDS (narrow ones), ragged rows and columns, K tails."""
+    """Float mode on the fp32 matrix cores: 32 x 128 block tiles (4 chains per wave, the last
+    two shapes) and 16 x 64 tiles (2 chains per wave), the chains' partial tiles added in LDS;
+    ragged rows and columns, K tails."""
     print(f"bitlinear float mfma rows={rows} K={K} N={N}", flush=True)
     rng = np.random.default_rng(rows * 3 + K + N)
     x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
@@ -245,6 +246,21 @@ def test_forward_logits(blobs, oracle, mode):
     e = Engine(0)
     e.load_blob(blob, mode)
     assert_bitexact(e.forward(ids), om.forward(ids, mode), "forward logits")
+    e.close()
+
+
+def test_forward_float_long_prompt(blobs, oracle):
+    """6144-token float forward: every GEMM kind (i/f/g store, o and down residual add, the
+    gate/up swiglu pair) runs on 32 x 128 matrix-core tiles; all logits bit for bit."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    print("forward float long prompt", flush=True)
+    blob = read_blob(blobs("tall"))
+    om = oracle.model(blob)
+    ids = np.random.default_rng(17).integers(3, blob.config.vocab_size, 6144)
+    want = om.forward(ids, FLOAT)
+    e = Engine(0)
+    e.load_blob(blob, FLOAT)
+    assert_bitexact(e.forward(ids), want, "long-prompt forward logits")
     e.close()
 
 
