@@ -53,6 +53,7 @@ template <int CW> constexpr int f_stages() { return CW == 2 ? 3 : 2; }
 template <int EPI, int RM, int CW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f(GemmArgs a, ActBuf act) {
   static_assert(CW != 2 || RM == 1, "two chains per wave: one 16-row subtile");
+  static_assert(CW == 2 || CW == 4, "the 8 chains of a tile are split over 2 or 4 waves");
   constexpr bool PAIR = EPI == kEpiSwigluPair;
   constexpr int NC = CW, TR = 16 * RM, S = f_stages<CW>(), BUFF = TR * kFRS, WH = 8 / CW, WCOL = 4 / WH;
   extern __shared__ float smem[];
@@ -82,21 +83,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   int jc[NC];
 #pragma unroll
   for (int q = 0; q < NC; ++q) {
-    if (CW == 8) jc[q] = q;
-    else if (CW == 4) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
-    else jc[q] = wh + 4 * q;                                     // {wh, wh+4}
+    if (CW == 4) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
+    else jc[q] = wh + 4 * q;                               // {wh, wh+4}
   }
   const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
   auto load_w = [&](int c, uint32_t (&w)[NC]) {
-    if constexpr (CW == 8) {
-      const uint4* p4 = reinterpret_cast<const uint4*>(wrow + static_cast<size_t>(c) * 128);
-      uint4 lo = nok ? p4[0] : make_uint4(0, 0, 0, 0), hi = nok ? p4[1] : make_uint4(0, 0, 0, 0);
-      w[0] = lo.x; w[1] = lo.y; w[2] = lo.z; w[3] = lo.w;
-      w[4] = hi.x; w[5] = hi.y; w[6] = hi.z; w[7] = hi.w;
-    } else {
 #pragma unroll
-      for (int q = 0; q < NC; ++q) w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
-    }
+    for (int q = 0; q < NC; ++q) w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
   };
   // activation tile loads: TR rows x 8 chains x 4 float4 per chunk, 2 RM per thread
   const float* ybase = act.y + (static_cast<size_t>(am) * act.rows + row0) * act.ystride();
@@ -221,14 +214,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
   // ---- chain reduction in the hsum_ps order --------------------------------------------
   float val[RM][16];
-  if constexpr (CW == 8) {
-#pragma unroll
-    for (int m = 0; m < RM; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        val[m][r] = ((acc[m][0][r] + acc[m][4][r]) + (acc[m][1][r] + acc[m][5][r])) +
-                    ((acc[m][2][r] + acc[m][6][r]) + (acc[m][3][r] + acc[m][7][r]));
-  } else {
+  {
     // partial tiles in LDS [wc][wh][m][r][lane]: CW = 4: s_{2wh} + s_{2wh+1}; CW = 2: s_wh
     constexpr int PS = RM * 16 * 64;  // floats of one wave's partial tile
 #pragma unroll
@@ -302,7 +288,7 @@ hipError_t mfma_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
   dim3 grid((cols + per - 1) / per, (a.rows + 16 * RM - 1) / (16 * RM), EPI == kEpiSwigluPair ? 1 : a.nmat);
   const size_t ring = static_cast<size_t>(2) * 16 * RM * kFRS * sizeof(float);
-  const size_t red = CW == 8 ? 0 : static_cast<size_t>(4) * RM * 16 * 64 * sizeof(float);
+  const size_t red = static_cast<size_t>(4) * RM * 16 * 64 * sizeof(float);
   k_mfma_f<EPI, RM, CW><<<grid, 256, ring > red ? ring : red, s>>>(a, act);
   return hipGetLastError();
 }
