@@ -369,13 +369,20 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     run_gemm(c, ga, act, st);
     tend(c);
   }
-  // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150)
-  tbeg(c, kRkMixer);
-  if (segs)
-    MMF_HIP(launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H, trace_dev != nullptr, st));
-  else
-    MMF_HIP(launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state, trace_dev != nullptr, st));
-  tend(c);
+  // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150). Independent streams
+  // without a trace: the step runs inside the g_norm prologue below (kPreMixSwish), which
+  // reports hipErrorNotSupported, launching nothing, where its float4 form does not apply.
+  const bool mix_in_prologue = stream_state && !segs && !trace_dev;
+  auto run_mixer = [&]() -> hipError_t {
+    tbeg(c, kRkMixer);
+    const hipError_t e = segs ? launch_mixer_segs(ib, fb, scan, rb, state, L.lb, segs, nseg, rows, H,
+                                                  trace_dev != nullptr, st)
+                              : launch_mixer(ib, fb, scan, rb, state, L.lb, rows, H, stream_state,
+                                             trace_dev != nullptr, st);
+    tend(c);
+    return e;
+  };
+  if (!mix_in_prologue) MMF_HIP(run_mixer());
   if (trace_dev) {
     const size_t n = static_cast<size_t>(rows) * H * sizeof(float);
     MMF_HIP(hipMemcpyAsync(trace_dev + 0 * rows * H, ib, n, hipMemcpyDeviceToDevice, st));
@@ -397,9 +404,29 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.normw[0] = proj_of(c, L.proj[3]).d.normw;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
-    tbeg(c, kRkPrologue);
-    MMF_HIP(launch_prologue(mode, pa, act, st));
-    tend(c);
+    bool done = false;
+    if (mix_in_prologue) {
+      PrologueArgs pm = pa;
+      pm.pre = kPreMixSwish;
+      pm.x2 = ib;
+      pm.mix_f = fb;
+      pm.mix_state = state;
+      pm.mix_lb = L.lb;
+      tbeg(c, kRkPrologue);
+      const hipError_t e = launch_prologue(mode, pm, act, st);
+      tend(c);
+      if (e != hipErrorNotSupported) {
+        MMF_HIP(e);
+        done = true;
+      } else {
+        MMF_HIP(run_mixer());
+      }
+    }
+    if (!done) {
+      tbeg(c, kRkPrologue);
+      MMF_HIP(launch_prologue(mode, pa, act, st));
+      tend(c);
+    }
     GemmArgs ga = gemm_args(c, &L.proj[3], 1, rows, mode, m.frac);
     ga.epi = kEpiAdd;
     ga.add = h;

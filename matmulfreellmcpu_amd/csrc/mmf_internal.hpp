@@ -143,17 +143,25 @@ struct ActBuf {
 };
 
 // Stage kinds of the row prologue (what happens before the BitLinear's own RMSNorm).
-enum PreKind : int { kPreNone = 0, kPreNorm = 1, kPreSwish = 2 };
+// kPreMixSwish: kPreSwish whose x2 is computed in the prologue by the recurrence step of
+// independent streams (launch_mixer's stream_state form, hgrn_model.cpp:109-150): x2 holds
+// the i projection, mix_f the f projection, and mix_state [rows, K] is updated in place.
+enum PreKind : int { kPreNone = 0, kPreNorm = 1, kPreSwish = 2, kPreMixSwish = 3 };
 
 struct PrologueArgs {
   const float* x;      // [rows, K]
-  const float* x2;     // kPreSwish: recurrence output rows [rows, K]
+  const float* x2;     // kPreSwish: recurrence output rows [rows, K]; kPreMixSwish: i rows
   const float* pre_w;  // stage-1 norm weight
   const float* normw[3];
   int na;
   PreKind pre;
   float eps, qs;
+  const float* mix_f;  // kPreMixSwish: f projection rows [rows, K]
+  float* mix_state;    // kPreMixSwish: recurrent state [rows, K], read and updated
+  const float* mix_lb; // kPreMixSwish: lower bounds [K] or null
 };
+// kPreMixSwish runs only in the float4 prologue: it returns hipErrorNotSupported, launching
+// nothing, where that does not apply (the caller then runs launch_mixer and kPreSwish).
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s);
 
 // Integer codes [rows, K] (int16-range, as int32) -> planes (TernaryBackend path).

@@ -234,19 +234,20 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
 template <int MODE, int PRE, int NA, int MAXV, bool PW, int BT>
 __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
-  constexpr int NV = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
-  constexpr int IX2 = 1, IPW = (PRE == kPreSwish) ? 2 : 1, INW = 1 + (PRE == kPreSwish ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
+  constexpr bool SW = PRE == kPreSwish || PRE == kPreMixSwish, MIX = PRE == kPreMixSwish;
+  constexpr int NV = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
+  constexpr int IX2 = 1, IPW = SW ? 2 : 1, INW = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
   const int row = xcd_row(blockIdx.x);
   if (row >= act.rows) return;
   const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
   const int LS = lds_stride(Lc);
   float* X = smem;
   // second LDS row only for silu(x2) (g_norm); the normed values never go through LDS
-  float* S = (PRE == kPreSwish) ? X + 8 * LS + 8 : X;
+  float* S = SW ? X + 8 * LS + 8 : X;
   float* red = S + 8 * LS + 8;
   const float* src[NV];
   src[0] = a.x + static_cast<size_t>(row) * K;
-  if (PRE == kPreSwish) src[IX2] = a.x2 + static_cast<size_t>(row) * K;
+  if (SW) src[IX2] = a.x2 + static_cast<size_t>(row) * K;
   if (PRE != kPreNone) src[IPW] = a.pre_w;
 #pragma unroll
   for (int i = 0; i < NA; ++i) src[INW + i] = a.normw[i];
@@ -254,7 +255,7 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   // so L2-resident, are read in the pass that uses them (fewer registers per thread, more
   // rows resident per CU) or, with PW (a few rows: the launch is one row's latency), loaded
   // at entry with the row, so that no pass waits for a memory round trip of its own.
-  constexpr int NX = 1 + (PRE == kPreSwish ? 1 : 0);
+  constexpr int NX = 1 + (SW ? 1 : 0);
   constexpr int NWV = PW ? NV - NX : 1;
   float4 v[NX][MAXV];
   float4 wv[NWV][PW ? MAXV : 1];
@@ -270,6 +271,20 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
         wv[wi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[NX + wi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  // kPreMixSwish: the f projection and the state of the row, with the inputs
+  float4 fv[MIX ? MAXV : 1], sv[MIX ? MAXV : 1], lv[MIX ? MAXV : 1];
+  if constexpr (MIX) {
+    const float4* f4 = reinterpret_cast<const float4*>(a.mix_f + static_cast<size_t>(row) * K);
+    const float4* s4 = reinterpret_cast<const float4*>(a.mix_state + static_cast<size_t>(row) * K);
+    const float4* l4 = reinterpret_cast<const float4*>(a.mix_lb);
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+      const int k4 = threadIdx.x + j * blockDim.x;
+      fv[j] = k4 < K4 ? f4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      sv[j] = k4 < K4 ? s4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      lv[j] = (l4 && k4 < K4) ? l4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   auto wt = [&](int vi, int k4, int j) {
     if constexpr (PW) return wv[vi - NX][j];
     else return reinterpret_cast<const float4*>(src[vi])[k4];
@@ -280,11 +295,35 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   for (int j = 0; j < MAXV; ++j) {
     const int k4 = threadIdx.x + j * blockDim.x;
     if (k4 >= K4) continue;
+    if constexpr (MIX) {
+      // the recurrence step of k_mixer (stream_state), element for element; the swiglu and
+      // sigmoid tail rule counts over all rows x K elements
+      const size_t e0 = static_cast<size_t>(row) * K + 4 * k4;
+      const size_t body = (static_cast<size_t>(act.rows) * K) & ~static_cast<size_t>(7);
+      const float4 lbv = lv[j];
+      float st[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
-      X[p] = el(v[0][j], c);
-      if (PRE == kPreSwish) S[p] = silu_of(el(v[IX2][j], c), k >= K8);
+      for (int c = 0; c < 4; ++c) {
+        const bool tail = e0 + c >= body;
+        float f = sigmoid_of(el(fv[j], c), tail);
+        if (a.mix_lb) f = __builtin_fmaf(1.0f - el(lbv, c), f, el(lbv, c));
+        const float in = swiglu_of(el(v[IX2][j], c), 1.0f - f, tail);
+        st[c] = __builtin_fmaf(f, el(sv[j], c), in);
+      }
+      reinterpret_cast<float4*>(a.mix_state + static_cast<size_t>(row) * K)[k4] = make_float4(st[0], st[1], st[2], st[3]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
+        X[p] = el(v[0][j], c);
+        S[p] = silu_of(st[c], k >= K8);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
+        X[p] = el(v[0][j], c);
+        if (SW) S[p] = silu_of(el(v[IX2][j], c), k >= K8);
+      }
     }
   }
   const int L32 = (Lc + 31) / 32 * 32;
@@ -303,7 +342,7 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
       for (int c = 0; c < 4; ++c) {
         const int p = act_pos(4 * k4 + c, K8, LS);
         float x = (X[p] * r1) * el(w, c);
-        if (PRE == kPreSwish) x = x * S[p];
+        if (SW) x = x * S[p];
         X[p] = x;
       }
     }
@@ -1194,6 +1233,7 @@ static hipError_t prologue4_mode(const PrologueArgs& a, ActBuf& act, size_t lds,
   if (a.pre == kPreNorm && a.na == 3) return prologue4_inst<MODE, kPreNorm, 3>(a, act, lds, s);
   if (a.pre == kPreNorm && a.na == 1) return prologue4_inst<MODE, kPreNorm, 1>(a, act, lds, s);
   if (a.pre == kPreSwish && a.na == 1) return prologue4_inst<MODE, kPreSwish, 1>(a, act, lds, s);
+  if (a.pre == kPreMixSwish && a.na == 1) return prologue4_inst<MODE, kPreMixSwish, 1>(a, act, lds, s);
   if (a.pre == kPreNone && a.na == 1) return prologue4_inst<MODE, kPreNone, 1>(a, act, lds, s);
   if (a.pre == kPreNone && a.na == 3) return prologue4_inst<MODE, kPreNone, 3>(a, act, lds, s);
   return hipErrorNotSupported;
@@ -1204,10 +1244,15 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);
   const size_t lds = (2 * rowf + 16) * sizeof(float);
-  const size_t lds4 = ((a.pre == kPreSwish ? 2 : 1) * rowf + 16) * sizeof(float);  // k_prologue4
+  const bool sw = a.pre == kPreSwish || a.pre == kPreMixSwish;
+  const size_t lds4 = ((sw ? 2 : 1) * rowf + 16) * sizeof(float);  // k_prologue4
   bool fast = act.K % 4 == 0 && act.K / 4 <= 7 * 256 && aligned16(a.x) && (a.na == 1 || a.na == 3);
   if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
-  if (a.pre == kPreSwish) fast = fast && aligned16(a.x2);
+  if (sw) fast = fast && aligned16(a.x2);
+  if (a.pre == kPreMixSwish) {
+    fast = fast && a.na == 1 && aligned16(a.mix_f) && aligned16(a.mix_state) && (!a.mix_lb || aligned16(a.mix_lb));
+    if (!fast) return hipErrorNotSupported;
+  }
   for (int i = 0; i < a.na; ++i) fast = fast && aligned16(a.normw[i]);
   if (fast) {
     hipError_t e = hipErrorNotSupported;

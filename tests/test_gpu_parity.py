@@ -264,10 +264,14 @@ def test_forward_float_long_prompt(blobs, oracle):
     e.close()
 
 
+@pytest.mark.parametrize("name", ["small", "odd"])
 @pytest.mark.parametrize("mode", [FLOAT, FIXED])
-def test_serve_matches_oracle(blobs, oracle, mode):
+def test_serve_matches_oracle(blobs, oracle, name, mode):
+    """Serving steps of 5 streams; the recurrence step runs inside the g_norm prologue.
+    "odd" (hidden 100): the last 4 of the 5 x 100 mixer elements take the scalar tail."""
     from matmulfreellmcpu_amd import Engine, read_blob
-    blob = read_blob(blobs("small"))
+    print(f"serve blob={name} mode={mode}", flush=True)
+    blob = read_blob(blobs(name))
     om = oracle.model(blob)
     rng = np.random.default_rng(9)
     V = blob.config.vocab_size
