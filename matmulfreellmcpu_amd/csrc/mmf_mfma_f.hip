@@ -43,6 +43,7 @@ namespace mmf {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kFRS = 8 * 16 + 4;  // LDS floats per staged row (8 chains x 16 positions, padded)
 // register sets of chunk loads in flight: a 16-row tile's chunk is ~0.5 us of matrix work
@@ -273,6 +274,133 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
 }
 
+// 32-row x 64-column tiles on v_mfma_f32_32x32x1_2b_f32 (the two blocks are the two 32-column
+// halves; accumulator r of lane l is block r / 16, row 8 ((r % 16) / 4) + 4 (l / 32) + r % 4,
+// column l % 32), 2 chains per wave as in k_mfma_f<., 1, 2>: for launches with enough 16-row
+// tiles that each wave's longer instructions pay (the serving steps' i/f/g and gate/up GEMMs).
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f32w(GemmArgs a, ActBuf act) {
+  constexpr bool PAIR = EPI == kEpiSwigluPair;
+  constexpr int NC = 2, S = 3;
+  extern __shared__ float smem[];
+  const int z = blockIdx.z;
+  const ProjDev& P = a.p[z];
+  const Geom& g = P.g;
+  const int Lc = act.Lc, Wc = g.Wc;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row0 = blockIdx.y * 32;
+  const int am = (act.na > 1) ? z : 0;
+  const int N = g.N, Nh = N / 2;
+  int n, cbase;
+  bool nok;
+  if (PAIR) {
+    cbase = blockIdx.x * 32;  // gate columns cbase + lane % 32 (block 0), up partners N/2 later (block 1)
+    const int c = cbase + (lane & 31);
+    nok = c < Nh;
+    n = (lane < 32) ? c : Nh + c;
+  } else {
+    cbase = blockIdx.x * 64;
+    n = cbase + lane;
+    nok = n < N;
+  }
+  const int jc[NC] = {wv, wv + 4};
+  const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
+  const int ri = lane & 31;
+  const bool rok = row0 + ri < a.rows;
+  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride();
+  auto load = [&](int c, float4 (&v)[NC][4], uint32_t (&w)[NC]) {
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq)
+        v[q][tq] = rok ? *reinterpret_cast<const float4*>(yrow + jc[q] * Lc + 16 * c + 4 * tq)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
+    }
+  };
+  v32f acc[NC];
+#pragma unroll
+  for (int q = 0; q < NC; ++q) acc[q] = v32f{};
+  float4 ar[S][NC][4];
+  uint32_t wr[S][NC];
+#pragma unroll
+  for (int u = 0; u < S; ++u)
+    if (u < Wc) load(u, ar[u], wr[u]);
+  for (int c0 = 0; c0 < Wc; c0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int c = c0 + u;
+      if (c >= Wc) break;
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int q = 0; q < NC; ++q) {
+            const float4 v = ar[u][q][tq];
+            const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+            acc[q] = __builtin_amdgcn_mfma_f32_32x32x1f32(y, code_f(wr[u][q], 4 * tq + tt), acc[q], 0, 0, 0);
+          }
+      if (c + S < Wc) load(c + S, ar[u], wr[u]);
+    }
+  }
+  // s_w = a_w + a_{w+4} per wave through LDS [w][r][lane]; wave 0: (s0 + s1) + (s2 + s3)
+#pragma unroll
+  for (int r = 0; r < 32; ++r) smem[(wv * 32 + r) * 64 + lane] = acc[0][r] + acc[1][r];
+  __syncthreads();
+  if (wv != 0) return;
+  constexpr int PS = 32 * 64;
+  float val[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const float* rp = smem + r * 64 + lane;
+    val[r] = (rp[0] + rp[PS]) + (rp[2 * PS] + rp[3 * PS]);
+  }
+  auto finish = [&](float sum, int o, int row) {
+    const float* yt = act.y + (static_cast<size_t>(am) * act.rows + row) * act.ystride() + 8 * Lc;
+    for (int t = 0; t < g.ntail; ++t) {
+      const int8_t wt = P.tail[o * 8 + t];
+      if (wt > 0) sum += yt[t];
+      else if (wt < 0) sum -= yt[t];
+    }
+    return sum * P.inv_scale_w;
+  };
+  const int col = lane & 31, rq = 4 * (lane >> 5);
+  if (PAIR) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + 8 * (r >> 2) + rq + (r & 3);
+      const int c = cbase + col;
+      if (row >= a.rows || c >= Nh) continue;
+      const float vg = finish(val[r], c, row), vu = finish(val[r + 16], Nh + c, row);
+      const size_t e = static_cast<size_t>(row) * Nh + c;
+      a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int rr = r & 15;
+      const int row = row0 + 8 * (rr >> 2) + rq + (rr & 3);
+      const int o = cbase + 32 * (r >> 4) + col;
+      if (row >= a.rows || o >= N) continue;
+      const float v = finish(val[r], o, row);
+      const size_t e = static_cast<size_t>(row) * N + o;
+      a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
+    }
+  }
+}
+
+template <int EPI>
+hipError_t mfma_f32w_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const Geom& g = a.p[0].g;
+  const int per = EPI == kEpiSwigluPair ? 32 : 64;
+  const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
+  dim3 grid((cols + per - 1) / per, (a.rows + 31) / 32, EPI == kEpiSwigluPair ? 1 : a.nmat);
+  k_mfma_f32w<EPI><<<grid, 256, 4 * 32 * 64 * sizeof(float), s>>>(a, act);
+  return hipGetLastError();
+}
+
 template <int EPI, int RM, int CW>
 long mfma_f_blocks(const GemmArgs& a) {
   const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW / 2);
@@ -293,10 +421,13 @@ hipError_t mfma_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 32 x 128 block tiles while that leaves at least 1024 blocks (four per CU), else 16 x 64
+// 32 x 128 block tiles while that leaves at least 1024 blocks (four per CU); else 32 x 64
+// tiles of the 32x32 instruction while there would be at least 384 16-row tiles (1.5 per
+// CU: 64 x 2560 x 7680 37 against 42 us, 64 x 2560 x 13824 58 against 76 us), else 16 x 64
 template <int EPI>
 hipError_t mfma_f_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   if (mfma_f_blocks<EPI, 2, 4>(a) >= 1024) return mfma_f_inst<EPI, 2, 4>(a, act, s);
+  if (mfma_f_blocks<EPI, 1, 2>(a) >= 384) return mfma_f32w_inst<EPI>(a, act, s);
   return mfma_f_inst<EPI, 1, 2>(a, act, s);
 }
 

@@ -249,6 +249,21 @@ def test_forward_logits(blobs, oracle, mode):
     e.close()
 
 
+def test_forward_float_mid_prompt(blobs, oracle):
+    """600-token float forward on hidden 1024: every GEMM kind runs on the 32 x 64 tiles of
+    the 32x32 matrix-core instruction (store, residual add, swiglu pair, ragged last tile)."""
+    from matmulfreellmcpu_amd import Engine, read_blob
+    print("forward float mid prompt", flush=True)
+    blob = read_blob(blobs("wide"))
+    om = oracle.model(blob)
+    ids = np.random.default_rng(19).integers(3, blob.config.vocab_size, 600)
+    want = om.forward(ids, FLOAT)
+    e = Engine(0)
+    e.load_blob(blob, FLOAT)
+    assert_bitexact(e.forward(ids), want, "mid-prompt forward logits")
+    e.close()
+
+
 def test_forward_float_long_prompt(blobs, oracle):
     """6144-token float forward: every GEMM kind (i/f/g store, o and down residual add, the
     gate/up swiglu pair) runs on 32 x 128 matrix-core tiles; all logits bit for bit."""
@@ -360,10 +375,11 @@ def test_serve_stacked_matches_oracle(blobs, oracle, mode):
     e.close()
 
 
-@pytest.mark.parametrize("mode", [FIXED, INT8])
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
 def test_serve_kgroups_matches_oracle(blobs, oracle, mode):
     """Serving steps of 56 streams whose MLP gate GEMM (6144 columns) runs as K-groups with
-    the swiglu-pair epilogue after the LDS reduction."""
+    the swiglu-pair epilogue after the LDS reduction (integer modes), or on 32 x 64 tiles of
+    the 32x32 fp32 matrix-core instruction (float)."""
     from matmulfreellmcpu_amd import Engine, read_blob
     blob = read_blob(blobs("wide"))
     om = oracle.model(blob)
