@@ -69,23 +69,26 @@ __device__ __forceinline__ float rstd_of(float ss, int n, float eps) {
 // Sequential reference lane sums (simd.hpp:69-89) over a zero-padded chain-transposed LDS
 // vector whose rows are LS floats apart and zero up to a multiple of 32, in two halves so
 // other waves can work while wave 0 runs the chains: chain_begin -- thread j < 8 sums row j
-// with FMAs in order, 32 values per batch, the next batch loading while the current one is
+// with FMAs in order, 4U values per batch, the next batch loading while the current one is
 // summed (the zeros add exact zeros); chain_end (after a barrier) -- hsum + the tail.
+// U float4 per batch (4U values; rows are zero to a multiple of 32, so U = 4 or 8).
+template <int U = 8>
 __device__ inline void chain_begin(const float* X, int Lc, int LS, float* red) {
+  static_assert(U == 4 || U == 8, "batches of 16 or 32 values");
   if (threadIdx.x < 8) {
     const float4* c = reinterpret_cast<const float4*>(X + threadIdx.x * LS);
-    const int nbat = (Lc + 31) / 32;
+    const int nbat = (Lc + 4 * U - 1) / (4 * U);
     float a = 0.0f;
-    float4 A[8], B[8];
+    float4 A[U], B[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) A[u] = c[u];
+    for (int u = 0; u < U; ++u) A[u] = c[u];
     for (int b = 0; b < nbat; b += 2) {
       const bool more = b + 1 < nbat;
       if (more)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) B[u] = c[8 * (b + 1) + u];
+        for (int u = 0; u < U; ++u) B[u] = c[U * (b + 1) + u];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < U; ++u) {
         a = __builtin_fmaf(A[u].x, A[u].x, a);
         a = __builtin_fmaf(A[u].y, A[u].y, a);
         a = __builtin_fmaf(A[u].z, A[u].z, a);
@@ -94,9 +97,9 @@ __device__ inline void chain_begin(const float* X, int Lc, int LS, float* red) {
       if (more) {
         if (b + 2 < nbat)
 #pragma unroll
-          for (int u = 0; u < 8; ++u) A[u] = c[8 * (b + 2) + u];
+          for (int u = 0; u < U; ++u) A[u] = c[U * (b + 2) + u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
           a = __builtin_fmaf(B[u].x, B[u].x, a);
           a = __builtin_fmaf(B[u].y, B[u].y, a);
           a = __builtin_fmaf(B[u].z, B[u].z, a);

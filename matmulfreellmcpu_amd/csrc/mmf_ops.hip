@@ -26,8 +26,9 @@ __device__ __forceinline__ int act_pos(int k, int K8, int LS) {
 
 // Reference sumsq (simd.hpp:69-89) of a padded chain-transposed vector in LDS: every
 // thread gets the result. `red` is 8 floats of LDS.
+template <int U = 8>
 __device__ float block_sumsq(const float* X, int Lc, int LS, int ntail, float* red) {
-  chain_begin(X, Lc, LS, red);
+  chain_begin<U>(X, Lc, LS, red);
   __syncthreads();
   const float s = chain_end(X, LS, ntail, red);
   __syncthreads();
@@ -231,9 +232,19 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
 // row (x, the gate input x2, the stage-1 weight, the NA BitLinear norm weights) is loaded
 // as float4 at entry -- one memory round trip -- and each thread then works on exactly the
 // elements it loaded. Arithmetic and order are those of k_prologue.
+// The 256-thread prologues of long row ranges fit 64 VGPRs (8 waves per SIMD: 8 rows resident
+// per CU, so 2048 rows run in one round) with 16-value chain batches; the recurrence and
+// the wide swish forms would spill there and keep the default.
+template <int PRE, int MAXV, int BT>
+constexpr bool prologue_eight_waves() {
+  return BT == 256 && PRE != kPreMixSwish && !(PRE == kPreSwish && MAXV > 3);
+}
+
 template <int MODE, int PRE, int NA, int MAXV, bool PW, int BT>
-__global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
+__global__ __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(prologue_eight_waves<PRE, MAXV, BT>() ? 8 : 1)))
+void k_prologue4(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
+  constexpr int CU = prologue_eight_waves<PRE, MAXV, BT>() ? 4 : 8;  // float4 per chain batch
   constexpr bool SW = PRE == kPreSwish || PRE == kPreMixSwish, MIX = PRE == kPreMixSwish;
   constexpr int NV = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
   constexpr int IX2 = 1, IPW = SW ? 2 : 1, INW = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
@@ -332,7 +343,7 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
   for (int t = nt + threadIdx.x; t < 8; t += blockDim.x) X[8 * LS + t] = 0.0f;
   __syncthreads();
   if (PRE != kPreNone) {
-    const float r1 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+    const float r1 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
       const int k4 = threadIdx.x + j * blockDim.x;
@@ -348,7 +359,7 @@ __global__ __launch_bounds__(BT) void k_prologue4(PrologueArgs a, ActBuf act) {
     }
     __syncthreads();
   }
-  const float r2 = rstd_of(block_sumsq(X, Lc, LS, nt, red), K, a.eps);
+  const float r2 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
   // Each thread keeps the BitLinear-normed values of its own elements in registers and
   // writes them (or their codes) straight to their chain-transposed positions: no staging
   // row, no extra pass.
