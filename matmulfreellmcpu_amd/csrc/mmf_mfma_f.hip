@@ -23,16 +23,16 @@
 // GEMV path: the word (group n / 16, chunk c, output n % 16, chain j) holds the 16 codes of
 // chain j at t = 16c .. 16c + 15, one v_bfe_i32 + v_cvt_f32_i32 per code.
 //
-// Tiling: RM 16-row subtiles per wave share each decoded weight; the 8 chains of a tile are
-// split over 8 / CW waves of a block (CW chains each), so the accumulators (RM x CW x 16
-// registers) stay within 128 and two waves fit per SIMD:
-//   RM = 2, CW = 4 (long row ranges, prefill): a block is 32 rows x 128 columns; the wave
-//           pair of a column group runs chains {0, 4, 1, 5} and {2, 6, 3, 7};
-//   RM = 1, CW = 2 (a few dozen rows, serving steps): a block is 16 rows x 64 columns, wave
-//           w runs chains w and w + 4, so the launch has 4x the waves per column.
-// Each wave adds its chains in pairs (a_j + a_{j+4}, the first level of hsum_ps), and the
-// wave of the column group with the first chains adds the other partial tiles through LDS in
-// the remaining order.
+// Three tilings, chosen by how many tiles a launch has (mfma_f_epi):
+//   k_mfma_f (long row ranges, prefill): a block is 32 rows x 128 columns. Each wave has two
+//     16-row subtiles that share each decoded weight, and 4 of the 8 chains: the wave pair of
+//     a column group runs chains {0, 4, 1, 5} and {2, 6, 3, 7}, 128 accumulator registers,
+//     two waves per SIMD. The activation tile is staged through LDS.
+//   k_mfma_f32w (mid-size launches: the serving steps' i/f/g and gate/up GEMMs): 32 x 64
+//     tiles of the 32x32x1 instruction, 2 chains per wave, operands straight to registers.
+//   k_mfma_f1 (narrow launches: the serving steps' o/down GEMMs): 16 x 64 tiles, one chain
+//     per wave, 8 waves per tile, operands straight to registers.
+// The waves add their chains in the hsum_ps order, through LDS across waves.
 // Epilogues: store, residual add, and the MLP pair (wave columns 0..31 gate outputs c0 ..
 // c0+31, columns 32..63 their up partners N/2 later: swiglu in registers).
 #include "mmf_device.hpp"
@@ -46,17 +46,12 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kFRS = 8 * 16 + 4;  // LDS floats per staged row (8 chains x 16 positions, padded)
-// register sets of chunk loads in flight: a 16-row tile's chunk is ~0.5 us of matrix work
-// (2 chains per wave), short against a load from HBM or another XCD's writes (the serving
-// steps stream every layer's weights), so those tiles keep more chunks in flight
-template <int CW> constexpr int f_stages() { return CW == 2 ? 3 : 2; }
 
 template <int EPI, int RM, int CW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f(GemmArgs a, ActBuf act) {
-  static_assert(CW != 2 || RM == 1, "two chains per wave: one 16-row subtile");
-  static_assert(CW == 2 || CW == 4, "the 8 chains of a tile are split over 2 or 4 waves");
+  static_assert(RM == 2 && CW == 4, "32 x 128 block tiles: two 16-row subtiles, 4 chains per wave");
   constexpr bool PAIR = EPI == kEpiSwigluPair;
-  constexpr int NC = CW, TR = 16 * RM, S = f_stages<CW>(), BUFF = TR * kFRS, WH = 8 / CW, WCOL = 4 / WH;
+  constexpr int NC = CW, TR = 16 * RM, S = 2, BUFF = TR * kFRS, WH = 8 / CW, WCOL = 4 / WH;
   extern __shared__ float smem[];
   const int z = blockIdx.z;
   const ProjDev& P = a.p[z];
@@ -83,10 +78,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
   int jc[NC];
 #pragma unroll
-  for (int q = 0; q < NC; ++q) {
-    if (CW == 4) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
-    else jc[q] = wh + 4 * q;                               // {wh, wh+4}
-  }
+  for (int q = 0; q < NC; ++q) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
   const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
   auto load_w = [&](int c, uint32_t (&w)[NC]) {
 #pragma unroll
@@ -116,114 +108,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
     for (int q = 0; q < NC; ++q) acc[m][q] = v16f{};
   const int ri = lane & 15;  // this lane's A row within a subtile
-  if constexpr (CW == 2) {
-    // Each wave's two chains are its own: no activation is shared between the waves of the
-    // block, so every wave loads its operands straight into registers (S chunks in flight)
-    // and runs without barriers. Lanes l, l + 16, l + 32, l + 48 read the same row.
-    const bool rok = row0 + ri < a.rows;
-    const float* yrow = ybase + static_cast<size_t>(ri) * act.ystride();
-    auto load_a = [&](int c, float4 (&v)[NC][4]) {
+  // S register sets in flight: set u holds the activations and weights of the chunks
+  // c = u (mod S). Chunk c's activations are loaded at the top of iteration c - S, written to
+  // LDS slot (c & 1) at the bottom of iteration c - 1; its weights are loaded at the bottom of
+  // iteration c - S and used in iteration c. The loop body is unrolled S times so that every
+  // set index is a compile-time constant.
+  float4 yr[S][NL];
+  uint32_t wr[S][NC];
 #pragma unroll
-      for (int q = 0; q < NC; ++q)
-#pragma unroll
-        for (int tq = 0; tq < 4; ++tq)
-          v[q][tq] = rok ? *reinterpret_cast<const float4*>(yrow + jc[q] * Lc + 16 * c + 4 * tq)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    float4 ar[S][NC][4];
-    uint32_t wr[S][NC];
-#pragma unroll
-    for (int u = 0; u < S; ++u)
-      if (u < Wc) {
-        load_a(u, ar[u]);
-        load_w(u, wr[u]);
-      }
-    for (int c0 = 0; c0 < Wc; c0 += S) {
-#pragma unroll
-      for (int u = 0; u < S; ++u) {
-        const int c = c0 + u;
-        if (c >= Wc) break;
-#pragma unroll
-        for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-            for (int q = 0; q < NC; ++q) {
-              const float4 v = ar[u][q][tq];
-              const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
-              acc[0][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(wr[u][q], 4 * tq + tt), acc[0][q], 0, 0, 0);
-            }
-        if (c + S < Wc) {
-          load_a(c + S, ar[u]);
-          load_w(c + S, wr[u]);
-        }
-      }
+  for (int u = 0; u < S; ++u)
+    if (u < Wc) {
+      load_y(u, yr[u]);
+      load_w(u, wr[u]);
     }
-  } else {
-    // S register sets in flight: set u holds the activations and weights of the chunks
-    // c = u (mod S). Chunk c's activations are loaded at the top of iteration c - S, written to
-    // LDS slot (c & 1) at the bottom of iteration c - 1; its weights are loaded at the bottom of
-    // iteration c - S and used in iteration c. The loop body is unrolled S times so that every
-    // set index is a compile-time constant.
-    float4 yr[S][NL];
-    uint32_t wr[S][NC];
-  #pragma unroll
-    for (int u = 0; u < S; ++u)
-      if (u < Wc) {
-        load_y(u, yr[u]);
-        load_w(u, wr[u]);
-      }
-  #pragma unroll
-    for (int h = 0; h < NL; ++h) *reinterpret_cast<float4*>(smem + ls_off[h]) = yr[0][h];
-    __syncthreads();
-    for (int c0 = 0; c0 < Wc; c0 += S) {
-  #pragma unroll
-      for (int u = 0; u < S; ++u) {
-        const int c = c0 + u;
-        if (c >= Wc) break;
-        const float* yb = smem + (c & 1) * BUFF + ri * kFRS;
-        if (c + S < Wc) load_y(c + S, yr[u]);
-  #pragma unroll
-        for (int tq = 0; tq < 4; ++tq) {
-          float4 av[RM][NC];
-  #pragma unroll
-          for (int m = 0; m < RM; ++m)
-  #pragma unroll
-            for (int q = 0; q < NC; ++q) av[m][q] = *reinterpret_cast<const float4*>(yb + 16 * m * kFRS + jc[q] * 16 + 4 * tq);
-  #pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-  #pragma unroll
-            for (int q = 0; q < NC; ++q) {
-              const float b = code_f(wr[u][q], 4 * tq + tt);
-  #pragma unroll
-              for (int m = 0; m < RM; ++m) {
-                const float y = tt == 0 ? av[m][q].x : tt == 1 ? av[m][q].y : tt == 2 ? av[m][q].z : av[m][q].w;
-                acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, b, acc[m][q], 0, 0, 0);
-              }
+#pragma unroll
+  for (int h = 0; h < NL; ++h) *reinterpret_cast<float4*>(smem + ls_off[h]) = yr[0][h];
+  __syncthreads();
+  for (int c0 = 0; c0 < Wc; c0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int c = c0 + u;
+      if (c >= Wc) break;
+      const float* yb = smem + (c & 1) * BUFF + ri * kFRS;
+      if (c + S < Wc) load_y(c + S, yr[u]);
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq) {
+        float4 av[RM][NC];
+#pragma unroll
+        for (int m = 0; m < RM; ++m)
+#pragma unroll
+          for (int q = 0; q < NC; ++q) av[m][q] = *reinterpret_cast<const float4*>(yb + 16 * m * kFRS + jc[q] * 16 + 4 * tq);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+          for (int q = 0; q < NC; ++q) {
+            const float b = code_f(wr[u][q], 4 * tq + tt);
+#pragma unroll
+            for (int m = 0; m < RM; ++m) {
+              const float y = tt == 0 ? av[m][q].x : tt == 1 ? av[m][q].y : tt == 2 ? av[m][q].z : av[m][q].w;
+              acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, b, acc[m][q], 0, 0, 0);
             }
           }
         }
-        if (c + 1 < Wc) {
-  #pragma unroll
-          for (int h = 0; h < NL; ++h)
-            *reinterpret_cast<float4*>(smem + ((c + 1) & 1) * BUFF + ls_off[h]) = yr[(u + 1) % S][h];
-        }
-        if (c + S < Wc) load_w(c + S, wr[u]);
-        __syncthreads();
       }
+      if (c + 1 < Wc) {
+#pragma unroll
+        for (int h = 0; h < NL; ++h)
+          *reinterpret_cast<float4*>(smem + ((c + 1) & 1) * BUFF + ls_off[h]) = yr[(u + 1) % S][h];
+      }
+      if (c + S < Wc) load_w(c + S, wr[u]);
+      __syncthreads();
     }
   }
   // ---- chain reduction in the hsum_ps order --------------------------------------------
   float val[RM][16];
   {
-    // partial tiles in LDS [wc][wh][m][r][lane]: CW = 4: s_{2wh} + s_{2wh+1}; CW = 2: s_wh
+    // partial tiles in LDS [wc][wh][m][r][lane]: s_{2wh} + s_{2wh+1} (s_j = a_j + a_{j+4})
     constexpr int PS = RM * 16 * 64;  // floats of one wave's partial tile
 #pragma unroll
     for (int m = 0; m < RM; ++m)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = (CW == 4) ? (acc[m][0][r] + acc[m][1][r]) + (acc[m][2][r] + acc[m][3][r])
-                                  : acc[m][0][r] + acc[m][1][r];
+        const float p = (acc[m][0][r] + acc[m][1][r]) + (acc[m][2][r] + acc[m][3][r]);
         smem[(wc * WH + wh) * PS + (m * 16 + r) * 64 + lane] = p;
       }
     __syncthreads();
@@ -234,7 +180,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int o = (m * 16 + r) * 64;
-        val[m][r] = (CW == 4) ? rp[o] + rp[PS + o] : (rp[o] + rp[PS + o]) + (rp[2 * PS + o] + rp[3 * PS + o]);
+        val[m][r] = rp[o] + rp[PS + o];
       }
   }
   // ---- tails, scale, epilogue ----------------------------------------------------------
@@ -391,6 +337,123 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
 }
 
+// 16-row x 64-column tiles with one chain per wave: 8 waves (512 threads) per tile, each
+// loading its operands straight into registers (3 chunks in flight, no barrier until the
+// reduction), for the narrow launches (the serving steps' o/down GEMMs: 64 x 2560 x 2560 in
+// 21 against 25 us with two chains per wave, 64 x 6912 x 2560 in 48 against 59 us). Wave 0
+// adds the 8 chain tiles through LDS in the hsum_ps order.
+template <int EPI>
+__global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
+  constexpr bool PAIR = EPI == kEpiSwigluPair;
+  constexpr int S = 3;
+  extern __shared__ float smem[];
+  const int z = blockIdx.z;
+  const ProjDev& P = a.p[z];
+  const Geom& g = P.g;
+  const int Lc = act.Lc, Wc = g.Wc;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's chain
+  const int row0 = blockIdx.y * 16;
+  const int am = (act.na > 1) ? z : 0;
+  const int N = g.N, Nh = N / 2;
+  int n, cbase;
+  bool nok;
+  if (PAIR) {
+    cbase = blockIdx.x * 32;
+    const int c = cbase + (lane & 31);
+    nok = c < Nh;
+    n = (lane < 32) ? c : Nh + c;
+  } else {
+    cbase = blockIdx.x * 64;
+    n = cbase + lane;
+    nok = n < N;
+  }
+  const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8 + j;
+  const int ri = lane & 15;
+  const bool rok = row0 + ri < a.rows;
+  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride() + j * Lc;
+  auto load = [&](int c, float4 (&v)[4], uint32_t& w) {
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq)
+      v[tq] = rok ? *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq) : make_float4(0.f, 0.f, 0.f, 0.f);
+    w = nok ? wrow[static_cast<size_t>(c) * 128] : 0u;
+  };
+  v16f acc = v16f{};
+  float4 ar[S][4];
+  uint32_t wr[S];
+#pragma unroll
+  for (int u = 0; u < S; ++u)
+    if (u < Wc) load(u, ar[u], wr[u]);
+  for (int c0 = 0; c0 < Wc; c0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int c = c0 + u;
+      if (c >= Wc) break;
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const float4 v = ar[u][tq];
+          const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+          acc = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(wr[u], 4 * tq + tt), acc, 0, 0, 0);
+        }
+      if (c + S < Wc) load(c + S, ar[u], wr[u]);
+    }
+  }
+  constexpr int PS = 16 * 64;  // floats of one chain's tile in LDS [j][r][lane]
+#pragma unroll
+  for (int r = 0; r < 16; ++r) smem[j * PS + r * 64 + lane] = acc[r];
+  __syncthreads();
+  if (j != 0) return;
+  float val[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float* p = smem + r * 64 + lane;
+    val[r] = ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
+  }
+  auto finish = [&](float sum, int o, int row) {
+    const float* yt = act.y + (static_cast<size_t>(am) * act.rows + row) * act.ystride() + 8 * Lc;
+    for (int t = 0; t < g.ntail; ++t) {
+      const int8_t wt = P.tail[o * 8 + t];
+      if (wt > 0) sum += yt[t];
+      else if (wt < 0) sum -= yt[t];
+    }
+    return sum * P.inv_scale_w;
+  };
+  const int col = lane & 15, rq = 4 * (lane >> 4);
+  if (PAIR) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int row = row0 + rq + (r & 3);
+      const int c = cbase + 16 * (r >> 2) + col;
+      if (row >= a.rows || c >= Nh) continue;
+      const float vg = finish(val[r], c, row), vu = finish(val[r + 8], Nh + c, row);
+      const size_t e = static_cast<size_t>(row) * Nh + c;
+      a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + rq + (r & 3);
+      const int o = cbase + 16 * (r >> 2) + col;
+      if (row >= a.rows || o >= N) continue;
+      const float v = finish(val[r], o, row);
+      const size_t e = static_cast<size_t>(row) * N + o;
+      a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
+    }
+  }
+}
+
+template <int EPI>
+hipError_t mfma_f1_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  const Geom& g = a.p[0].g;
+  const int per = EPI == kEpiSwigluPair ? 32 : 64;
+  const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
+  dim3 grid((cols + per - 1) / per, (a.rows + 15) / 16, EPI == kEpiSwigluPair ? 1 : a.nmat);
+  k_mfma_f1<EPI><<<grid, 512, 8 * 16 * 64 * sizeof(float), s>>>(a, act);
+  return hipGetLastError();
+}
+
 template <int EPI>
 hipError_t mfma_f32w_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Geom& g = a.p[0].g;
@@ -424,11 +487,12 @@ hipError_t mfma_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
 // 32 x 128 block tiles while that leaves at least 1024 blocks (four per CU); else 32 x 64
 // tiles of the 32x32 instruction while there would be at least 384 16-row tiles (1.5 per
 // CU: 64 x 2560 x 7680 37 against 42 us, 64 x 2560 x 13824 58 against 76 us), else 16 x 64
+// tiles with one chain per wave
 template <int EPI>
 hipError_t mfma_f_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   if (mfma_f_blocks<EPI, 2, 4>(a) >= 1024) return mfma_f_inst<EPI, 2, 4>(a, act, s);
   if (mfma_f_blocks<EPI, 1, 2>(a) >= 384) return mfma_f32w_inst<EPI>(a, act, s);
-  return mfma_f_inst<EPI, 1, 2>(a, act, s);
+  return mfma_f1_inst<EPI>(a, act, s);
 }
 
 }  // namespace
