@@ -29,7 +29,7 @@
 //     a column group runs chains {0, 4, 1, 5} and {2, 6, 3, 7}, 128 accumulator registers,
 //     two waves per SIMD. The activation tile is staged through LDS.
 //   k_mfma_f32w (mid-size launches: the serving steps' i/f/g and gate/up GEMMs): 32 x 64
-//     tiles of the 32x32x1 instruction, 2 chains per wave, operands straight to registers.
+//     tiles of the 32x32x1 instruction, one chain per wave, operands straight to registers.
 //   k_mfma_f1 (narrow launches: the serving steps' o/down GEMMs): 16 x 64 tiles, one chain
 //     per wave, 8 waves per tile, operands straight to registers.
 // The waves add their chains in the hsum_ps order, through LDS across waves.
@@ -222,19 +222,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 
 // 32-row x 64-column tiles on v_mfma_f32_32x32x1_2b_f32 (the two blocks are the two 32-column
 // halves; accumulator r of lane l is block r / 16, row 8 ((r % 16) / 4) + 4 (l / 32) + r % 4,
-// column l % 32), 2 chains per wave as in k_mfma_f<., 1, 2>: for launches with enough 16-row
-// tiles that each wave's longer instructions pay (the serving steps' i/f/g and gate/up GEMMs).
+// column l % 32), one chain per wave, 8 waves (512 threads) per tile, operands straight to
+// registers: for launches with enough 16-row tiles that each wave's longer instructions pay
+// (the serving steps' i/f/g and gate/up GEMMs: 64 x 2560 x 7680 in 33 us, 64 x 2560 x 13824
+// in 58 us, against 42 and 76 us on 16-row tiles with two chains per wave).
 template <int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f32w(GemmArgs a, ActBuf act) {
+__global__ __launch_bounds__(512) void k_mfma_f32w(GemmArgs a, ActBuf act) {
   constexpr bool PAIR = EPI == kEpiSwigluPair;
-  constexpr int NC = 2, S = 3;
+  constexpr int S = 3;
   extern __shared__ float smem[];
   const int z = blockIdx.z;
   const ProjDev& P = a.p[z];
   const Geom& g = P.g;
   const int Lc = act.Lc, Wc = g.Wc;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's chain
   const int row0 = blockIdx.y * 32;
   const int am = (act.na > 1) ? z : 0;
   const int N = g.N, Nh = N / 2;
@@ -250,26 +252,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     n = cbase + lane;
     nok = n < N;
   }
-  const int jc[NC] = {wv, wv + 4};
-  const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
+  const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8 + j;
   const int ri = lane & 31;
   const bool rok = row0 + ri < a.rows;
-  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride();
-  auto load = [&](int c, float4 (&v)[NC][4], uint32_t (&w)[NC]) {
+  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride() + j * Lc;
+  auto load = [&](int c, float4 (&v)[4], uint32_t& w) {
 #pragma unroll
-    for (int q = 0; q < NC; ++q) {
-#pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
-        v[q][tq] = rok ? *reinterpret_cast<const float4*>(yrow + jc[q] * Lc + 16 * c + 4 * tq)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-      w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
-    }
+    for (int tq = 0; tq < 4; ++tq)
+      v[tq] = rok ? *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq) : make_float4(0.f, 0.f, 0.f, 0.f);
+    w = nok ? wrow[static_cast<size_t>(c) * 128] : 0u;
   };
-  v32f acc[NC];
-#pragma unroll
-  for (int q = 0; q < NC; ++q) acc[q] = v32f{};
-  float4 ar[S][NC][4];
-  uint32_t wr[S][NC];
+  v32f acc = v32f{};
+  float4 ar[S][4];
+  uint32_t wr[S];
 #pragma unroll
   for (int u = 0; u < S; ++u)
     if (u < Wc) load(u, ar[u], wr[u]);
@@ -281,28 +276,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq)
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-          for (int q = 0; q < NC; ++q) {
-            const float4 v = ar[u][q][tq];
-            const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
-            acc[q] = __builtin_amdgcn_mfma_f32_32x32x1f32(y, code_f(wr[u][q], 4 * tq + tt), acc[q], 0, 0, 0);
-          }
+        for (int tt = 0; tt < 4; ++tt) {
+          const float4 v = ar[u][tq];
+          const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+          acc = __builtin_amdgcn_mfma_f32_32x32x1f32(y, code_f(wr[u], 4 * tq + tt), acc, 0, 0, 0);
+        }
       if (c + S < Wc) load(c + S, ar[u], wr[u]);
     }
   }
-  // s_w = a_w + a_{w+4} per wave through LDS [w][r][lane]; wave 0: (s0 + s1) + (s2 + s3)
-#pragma unroll
-  for (int r = 0; r < 32; ++r) smem[(wv * 32 + r) * 64 + lane] = acc[0][r] + acc[1][r];
-  __syncthreads();
-  if (wv != 0) return;
+  // chain tiles through LDS [j][r][lane]; wave 0 adds them in the hsum_ps order
   constexpr int PS = 32 * 64;
-  float val[32];
 #pragma unroll
-  for (int r = 0; r < 32; ++r) {
-    const float* rp = smem + r * 64 + lane;
-    val[r] = (rp[0] + rp[PS]) + (rp[2 * PS] + rp[3 * PS]);
-  }
+  for (int r = 0; r < 32; ++r) smem[j * PS + r * 64 + lane] = acc[r];
+  __syncthreads();
+  if (j != 0) return;
+  // each output's 8 chain values are added where it is stored (no 32-value array live)
+  auto hsum = [&](int r) {
+    const float* p = smem + r * 64 + lane;
+    return ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
+  };
   auto finish = [&](float sum, int o, int row) {
     const float* yt = act.y + (static_cast<size_t>(am) * act.rows + row) * act.ystride() + 8 * Lc;
     for (int t = 0; t < g.ntail; ++t) {
@@ -314,34 +306,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   };
   const int col = lane & 31, rq = 4 * (lane >> 5);
   if (PAIR) {
-#pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + 8 * (r >> 2) + rq + (r & 3);
       const int c = cbase + col;
       if (row >= a.rows || c >= Nh) continue;
-      const float vg = finish(val[r], c, row), vu = finish(val[r + 16], Nh + c, row);
+      const float vg = finish(hsum(r), c, row), vu = finish(hsum(r + 16), Nh + c, row);
       const size_t e = static_cast<size_t>(row) * Nh + c;
       a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
     }
   } else {
-#pragma unroll
     for (int r = 0; r < 32; ++r) {
       const int rr = r & 15;
       const int row = row0 + 8 * (rr >> 2) + rq + (rr & 3);
       const int o = cbase + 32 * (r >> 4) + col;
       if (row >= a.rows || o >= N) continue;
-      const float v = finish(val[r], o, row);
+      const float v = finish(hsum(r), o, row);
       const size_t e = static_cast<size_t>(row) * N + o;
       a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
     }
   }
 }
 
-// 16-row x 64-column tiles with one chain per wave: 8 waves (512 threads) per tile, each
-// loading its operands straight into registers (3 chunks in flight, no barrier until the
-// reduction), for the narrow launches (the serving steps' o/down GEMMs: 64 x 2560 x 2560 in
-// 21 against 25 us with two chains per wave, 64 x 6912 x 2560 in 48 against 59 us). Wave 0
-// adds the 8 chain tiles through LDS in the hsum_ps order.
 template <int EPI>
 __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
   constexpr bool PAIR = EPI == kEpiSwigluPair;
@@ -460,7 +445,7 @@ hipError_t mfma_f32w_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const int per = EPI == kEpiSwigluPair ? 32 : 64;
   const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
   dim3 grid((cols + per - 1) / per, (a.rows + 31) / 32, EPI == kEpiSwigluPair ? 1 : a.nmat);
-  k_mfma_f32w<EPI><<<grid, 256, 4 * 32 * 64 * sizeof(float), s>>>(a, act);
+  k_mfma_f32w<EPI><<<grid, 512, 8 * 32 * 64 * sizeof(float), s>>>(a, act);
   return hipGetLastError();
 }
 
