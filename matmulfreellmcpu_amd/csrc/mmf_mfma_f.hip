@@ -4,36 +4,30 @@
 // runs acc_j = fma(y_k, w_k, acc_j) over k = j + 8t in t order, the lanes are summed in the
 // hsum_ps order ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), and the K % 8 tail is added after.
 // With w_k in {-1, 0, +1} the product y_k * w_k is exact, so fma(y, w, acc) is the single
-// rounding of acc + y*w. v_mfma_f32_16x16x1_4b_f32 computes D = C + A*B per element with
-// one product (K = 1), so a chain of these instructions on one accumulator, fed the chain's
-// positions in t order, reproduces acc_j bit for bit (denormals included). Each chain is
-// its own accumulator tile, so the instruction order across chains is free, and the 8
-// chains give 8 independent accumulators to keep the matrix core busy.
+// rounding of acc + y*w. The fp32 matrix ops with one product per element (K = 1:
+// v_mfma_f32_32x32x1_2b_f32, v_mfma_f32_16x16x1_4b_f32) compute D = C + A*B, so a chain of
+// them on one accumulator, fed the chain's positions in t order, reproduces acc_j bit for bit
+// (denormals included). Each chain is its own accumulator tile, run by its own wave: 8 waves
+// per tile, wave j running chain j, and wave 0 adds the 8 chain tiles through LDS in the
+// hsum_ps order where each output is stored.
 //
-// Instruction layout (4 blocks of 16 x 16 x 1): lane l supplies A = y[row l % 16] and
-// B = w[column l] of block l / 16; accumulator r of lane l is block r / 4, row
-// 4 * (l / 16) + r % 4, column l % 16. Here all four blocks take the same 16 rows and
-// lane l's B is column n0 + l (four 16-column blocks side by side), so a wave computes a
-// 16-row x 64-column tile per instruction and position.
+// Operands go straight to registers, 3 chunks of 16 chain positions in flight per wave (no
+// wave shares another's activations, so there is no LDS staging and no barrier until the
+// reduction): lane l reads 4 positions of its row's chain per float4 load. Activations are
+// the fp32 chain rows of the prologue (row r, chain j, position t at y[r * (8 Lc + 8) +
+// j * Lc + t]). Weights are the 2-bit slabs of the GEMV path: the word (group n / 16, chunk
+// c, output n % 16, chain j) holds the 16 codes of chain j at t = 16c .. 16c + 15, one
+// v_bfe_i32 + v_cvt_f32_i32 per code. A wave issues a matrix op only about every 70 cycles
+// whatever its number of accumulators, so one chain per wave (the most waves per tile)
+// measured fastest at every size.
 //
-// Operands. Activations are the fp32 chain rows of the prologue (row r, chain j, position
-// t at y[r * (8 Lc + 8) + j * Lc + t]); a block stages the 16 rows x 8 chains x 16 positions
-// of one chunk in one of two LDS slots (loaded several chunks ahead into register sets), and each
-// lane reads 4 positions of one chain per ds_read_b128. Weights are the 2-bit slabs of the
-// GEMV path: the word (group n / 16, chunk c, output n % 16, chain j) holds the 16 codes of
-// chain j at t = 16c .. 16c + 15, one v_bfe_i32 + v_cvt_f32_i32 per code.
-//
-// Three tilings, chosen by how many tiles a launch has (mfma_f_epi):
-//   k_mfma_f (long row ranges, prefill): a block is 32 rows x 128 columns. Each wave has two
-//     16-row subtiles that share each decoded weight, and 4 of the 8 chains: the wave pair of
-//     a column group runs chains {0, 4, 1, 5} and {2, 6, 3, 7}, 128 accumulator registers,
-//     two waves per SIMD. The activation tile is staged through LDS.
-//   k_mfma_f32w (mid-size launches: the serving steps' i/f/g and gate/up GEMMs): 32 x 64
-//     tiles of the 32x32x1 instruction, one chain per wave, operands straight to registers.
-//   k_mfma_f1 (narrow launches: the serving steps' o/down GEMMs): 16 x 64 tiles, one chain
-//     per wave, 8 waves per tile, operands straight to registers.
-// The waves add their chains in the hsum_ps order, through LDS across waves.
-// Epilogues: store, residual add, and the MLP pair (wave columns 0..31 gate outputs c0 ..
+// Two tilings, chosen by how many tiles a launch has (mfma_f_epi):
+//   k_mfma_f32w: 32 x 64 tiles of the 32x32x1 instruction (2048 MACs per op: half the ops
+//     per wave of two 16-row tiles), from 384 16-row tiles on (prefill, the serving steps'
+//     i/f/g and gate/up GEMMs);
+//   k_mfma_f1: 16 x 64 tiles of the 16x16x1 instruction (4 blocks of 16 columns side by
+//     side, all with the same 16 rows) for narrower launches (the serving steps' o/down).
+// Epilogues: store, residual add, and the MLP pair (B columns 0..31 gate outputs c0 ..
 // c0+31, columns 32..63 their up partners N/2 later: swiglu in registers).
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
@@ -44,181 +38,6 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
-
-constexpr int kFRS = 8 * 16 + 4;  // LDS floats per staged row (8 chains x 16 positions, padded)
-
-template <int EPI, int RM, int CW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_mfma_f(GemmArgs a, ActBuf act) {
-  static_assert(RM == 2 && CW == 4, "32 x 128 block tiles: two 16-row subtiles, 4 chains per wave");
-  constexpr bool PAIR = EPI == kEpiSwigluPair;
-  constexpr int NC = CW, TR = 16 * RM, S = 2, BUFF = TR * kFRS, WH = 8 / CW, WCOL = 4 / WH;
-  extern __shared__ float smem[];
-  const int z = blockIdx.z;
-  const ProjDev& P = a.p[z];
-  const Geom& g = P.g;
-  const int Lc = act.Lc, Wc = g.Wc;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wh = wv % WH, wc = wv / WH;
-  const int row0 = blockIdx.y * TR;
-  const int am = (act.na > 1) ? z : 0;
-  const int N = g.N, Nh = N / 2;
-  // this lane's B column (weight row) and the wave's first output column
-  int n, cbase;
-  bool nok;
-  if (PAIR) {
-    cbase = (blockIdx.x * WCOL + wc) * 32;
-    const int c = cbase + (lane & 31);
-    nok = c < Nh;
-    n = (lane < 32) ? c : Nh + c;
-  } else {
-    cbase = (blockIdx.x * WCOL + wc) * 64;
-    n = cbase + lane;
-    nok = n < N;
-  }
-  int jc[NC];
-#pragma unroll
-  for (int q = 0; q < NC; ++q) jc[q] = 2 * wh + (q >> 1) + 4 * (q & 1);  // {2wh, 2wh+4, 2wh+1, 2wh+5}
-  const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8;
-  auto load_w = [&](int c, uint32_t (&w)[NC]) {
-#pragma unroll
-    for (int q = 0; q < NC; ++q) w[q] = nok ? wrow[static_cast<size_t>(c) * 128 + jc[q]] : 0u;
-  };
-  // activation tile loads: TR rows x 8 chains x 4 float4 per chunk, 2 RM per thread
-  const float* ybase = act.y + (static_cast<size_t>(am) * act.rows + row0) * act.ystride();
-  const int nrows = min(TR, a.rows - row0);
-  constexpr int NL = 2 * RM;
-  int ge_off[NL], ls_off[NL];
-  bool ge_ok[NL];
-#pragma unroll
-  for (int h = 0; h < NL; ++h) {
-    const int e = tid + 256 * h, r = e >> 5, ch = (e >> 2) & 7, f4 = e & 3;
-    ge_ok[h] = r < nrows;
-    ge_off[h] = r * static_cast<int>(act.ystride()) + ch * Lc + 4 * f4;
-    ls_off[h] = r * kFRS + ch * 16 + 4 * f4;
-  }
-  auto load_y = [&](int c, float4 (&v)[NL]) {
-#pragma unroll
-    for (int h = 0; h < NL; ++h)
-      v[h] = ge_ok[h] ? *reinterpret_cast<const float4*>(ybase + ge_off[h] + 16 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  v16f acc[RM][NC];
-#pragma unroll
-  for (int m = 0; m < RM; ++m)
-#pragma unroll
-    for (int q = 0; q < NC; ++q) acc[m][q] = v16f{};
-  const int ri = lane & 15;  // this lane's A row within a subtile
-  // S register sets in flight: set u holds the activations and weights of the chunks
-  // c = u (mod S). Chunk c's activations are loaded at the top of iteration c - S, written to
-  // LDS slot (c & 1) at the bottom of iteration c - 1; its weights are loaded at the bottom of
-  // iteration c - S and used in iteration c. The loop body is unrolled S times so that every
-  // set index is a compile-time constant.
-  float4 yr[S][NL];
-  uint32_t wr[S][NC];
-#pragma unroll
-  for (int u = 0; u < S; ++u)
-    if (u < Wc) {
-      load_y(u, yr[u]);
-      load_w(u, wr[u]);
-    }
-#pragma unroll
-  for (int h = 0; h < NL; ++h) *reinterpret_cast<float4*>(smem + ls_off[h]) = yr[0][h];
-  __syncthreads();
-  for (int c0 = 0; c0 < Wc; c0 += S) {
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int c = c0 + u;
-      if (c >= Wc) break;
-      const float* yb = smem + (c & 1) * BUFF + ri * kFRS;
-      if (c + S < Wc) load_y(c + S, yr[u]);
-#pragma unroll
-      for (int tq = 0; tq < 4; ++tq) {
-        float4 av[RM][NC];
-#pragma unroll
-        for (int m = 0; m < RM; ++m)
-#pragma unroll
-          for (int q = 0; q < NC; ++q) av[m][q] = *reinterpret_cast<const float4*>(yb + 16 * m * kFRS + jc[q] * 16 + 4 * tq);
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-          for (int q = 0; q < NC; ++q) {
-            const float b = code_f(wr[u][q], 4 * tq + tt);
-#pragma unroll
-            for (int m = 0; m < RM; ++m) {
-              const float y = tt == 0 ? av[m][q].x : tt == 1 ? av[m][q].y : tt == 2 ? av[m][q].z : av[m][q].w;
-              acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x1f32(y, b, acc[m][q], 0, 0, 0);
-            }
-          }
-        }
-      }
-      if (c + 1 < Wc) {
-#pragma unroll
-        for (int h = 0; h < NL; ++h)
-          *reinterpret_cast<float4*>(smem + ((c + 1) & 1) * BUFF + ls_off[h]) = yr[(u + 1) % S][h];
-      }
-      if (c + S < Wc) load_w(c + S, wr[u]);
-      __syncthreads();
-    }
-  }
-  // ---- chain reduction in the hsum_ps order --------------------------------------------
-  float val[RM][16];
-  {
-    // partial tiles in LDS [wc][wh][m][r][lane]: s_{2wh} + s_{2wh+1} (s_j = a_j + a_{j+4})
-    constexpr int PS = RM * 16 * 64;  // floats of one wave's partial tile
-#pragma unroll
-    for (int m = 0; m < RM; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = (acc[m][0][r] + acc[m][1][r]) + (acc[m][2][r] + acc[m][3][r]);
-        smem[(wc * WH + wh) * PS + (m * 16 + r) * 64 + lane] = p;
-      }
-    __syncthreads();
-    if (wh != 0) return;
-    const float* rp = smem + wc * WH * PS + lane;
-#pragma unroll
-    for (int m = 0; m < RM; ++m)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int o = (m * 16 + r) * 64;
-        val[m][r] = rp[o] + rp[PS + o];
-      }
-  }
-  // ---- tails, scale, epilogue ----------------------------------------------------------
-  const int col = lane & 15, rq = 4 * (lane >> 4);
-  auto finish = [&](float s, int o, int row) {
-    const float* yt = act.y + (static_cast<size_t>(am) * act.rows + row) * act.ystride() + 8 * Lc;
-    for (int t = 0; t < g.ntail; ++t) {
-      const int8_t wt = P.tail[o * 8 + t];
-      if (wt > 0) s += yt[t];
-      else if (wt < 0) s -= yt[t];
-    }
-    return s * P.inv_scale_w;
-  };
-#pragma unroll
-  for (int m = 0; m < RM; ++m) {
-    if (PAIR) {
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int row = row0 + 16 * m + rq + (r & 3);
-        const int c = cbase + 16 * (r >> 2) + col;
-        if (row >= a.rows || c >= Nh) continue;
-        const float vg = finish(val[m][r], c, row), vu = finish(val[m][r + 8], Nh + c, row);
-        const size_t e = static_cast<size_t>(row) * Nh + c;
-        a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = row0 + 16 * m + rq + (r & 3);
-        const int o = cbase + 16 * (r >> 2) + col;
-        if (row >= a.rows || o >= N) continue;
-        const float v = finish(val[m][r], o, row);
-        const size_t e = static_cast<size_t>(row) * N + o;
-        a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
-      }
-    }
-  }
-}
 
 // 32-row x 64-column tiles on v_mfma_f32_32x32x1_2b_f32 (the two blocks are the two 32-column
 // halves; accumulator r of lane l is block r / 16, row 8 ((r % 16) / 4) + 4 (l / 32) + r % 4,
@@ -390,12 +209,11 @@ __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
   for (int r = 0; r < 16; ++r) smem[j * PS + r * 64 + lane] = acc[r];
   __syncthreads();
   if (j != 0) return;
-  float val[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
+  // each output's 8 chain values are added where it is stored
+  auto hsum = [&](int r) {
     const float* p = smem + r * 64 + lane;
-    val[r] = ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
-  }
+    return ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
+  };
   auto finish = [&](float sum, int o, int row) {
     const float* yt = act.y + (static_cast<size_t>(am) * act.rows + row) * act.ystride() + 8 * Lc;
     for (int t = 0; t < g.ntail; ++t) {
@@ -407,22 +225,20 @@ __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
   };
   const int col = lane & 15, rq = 4 * (lane >> 4);
   if (PAIR) {
-#pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int row = row0 + rq + (r & 3);
       const int c = cbase + 16 * (r >> 2) + col;
       if (row >= a.rows || c >= Nh) continue;
-      const float vg = finish(val[r], c, row), vu = finish(val[r + 8], Nh + c, row);
+      const float vg = finish(hsum(r), c, row), vu = finish(hsum(r + 8), Nh + c, row);
       const size_t e = static_cast<size_t>(row) * Nh + c;
       a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
     }
   } else {
-#pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = row0 + rq + (r & 3);
       const int o = cbase + 16 * (r >> 2) + col;
       if (row >= a.rows || o >= N) continue;
-      const float v = finish(val[r], o, row);
+      const float v = finish(hsum(r), o, row);
       const size_t e = static_cast<size_t>(row) * N + o;
       a.out[z][e] = (EPI == kEpiAdd) ? a.add[e] + v : v;
     }
@@ -449,34 +265,20 @@ hipError_t mfma_f32w_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int EPI, int RM, int CW>
-long mfma_f_blocks(const GemmArgs& a) {
-  const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW / 2);
+// 16 x 64 tiles of a launch (16 x 32 gate columns with their up partners for the pair)
+template <int EPI>
+long mfma_f_tiles16(const GemmArgs& a) {
+  const int per = EPI == kEpiSwigluPair ? 32 : 64;
   const int cols = EPI == kEpiSwigluPair ? a.p[0].g.N / 2 : a.p[0].g.N;
-  return static_cast<long>((cols + per - 1) / per) * ((a.rows + 16 * RM - 1) / (16 * RM)) *
-         (EPI == kEpiSwigluPair ? 1 : a.nmat);
+  return static_cast<long>((cols + per - 1) / per) * ((a.rows + 15) / 16) * (EPI == kEpiSwigluPair ? 1 : a.nmat);
 }
 
-template <int EPI, int RM, int CW>
-hipError_t mfma_f_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
-  const Geom& g = a.p[0].g;
-  const int per = (EPI == kEpiSwigluPair ? 32 : 64) * (CW / 2);
-  const int cols = EPI == kEpiSwigluPair ? g.N / 2 : g.N;
-  dim3 grid((cols + per - 1) / per, (a.rows + 16 * RM - 1) / (16 * RM), EPI == kEpiSwigluPair ? 1 : a.nmat);
-  const size_t ring = static_cast<size_t>(2) * 16 * RM * kFRS * sizeof(float);
-  const size_t red = static_cast<size_t>(4) * RM * 16 * 64 * sizeof(float);
-  k_mfma_f<EPI, RM, CW><<<grid, 256, ring > red ? ring : red, s>>>(a, act);
-  return hipGetLastError();
-}
 
-// 32 x 128 block tiles while that leaves at least 1024 blocks (four per CU); else 32 x 64
-// tiles of the 32x32 instruction while there would be at least 384 16-row tiles (1.5 per
-// CU: 64 x 2560 x 7680 37 against 42 us, 64 x 2560 x 13824 58 against 76 us), else 16 x 64
-// tiles with one chain per wave
+// 32 x 64 tiles of the 32x32 instruction while there would be at least 384 16-row tiles (1.5
+// per CU), else 16 x 64 tiles
 template <int EPI>
 hipError_t mfma_f_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
-  if (mfma_f_blocks<EPI, 2, 4>(a) >= 1024) return mfma_f_inst<EPI, 2, 4>(a, act, s);
-  if (mfma_f_blocks<EPI, 1, 2>(a) >= 384) return mfma_f32w_inst<EPI>(a, act, s);
+  if (mfma_f_tiles16<EPI>(a) >= 384) return mfma_f32w_inst<EPI>(a, act, s);
   return mfma_f1_inst<EPI>(a, act, s);
 }
 
