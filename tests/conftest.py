@@ -67,7 +67,7 @@ def blobs(tmp_path_factory):
             make_blob(p, vocab=4096, hidden=256, layers=4, inter=704, seed=11, random_norms=True, random_lb=True)
         elif name == "wide":  # MLP gate matrix of 48 column tiles: the K-group GEMM at <= 64 rows
             make_blob(p, vocab=1024, hidden=1024, layers=2, inter=3072, seed=21, random_norms=True, random_lb=True)
-        elif name == "tall":  # long prompts: 32 x 128 float matrix-core tiles in every GEMM kind
+        elif name == "tall":  # long prompts: 32 x 64 float matrix-core tiles in every GEMM kind
             make_blob(p, vocab=256, hidden=768, layers=1, inter=528, seed=31, random_norms=True, random_lb=True)
         elif name == "odd":  # hidden not a multiple of 8 or 16 (tails everywhere)
             make_blob(p, vocab=1000, hidden=100, layers=2, inter=208, seed=13, random_norms=True, random_lb=True)

@@ -100,9 +100,9 @@ def test_bitlinear_op_kgroups(eng, oracle, rows, K, N, mode):
 @pytest.mark.parametrize("rows,K,N", [(16, 64, 64), (64, 1024, 2560), (100, 1031, 333), (1030, 523, 2048),
                                       (1030, 523, 8192), (2048, 256, 4008)])
 def test_bitlinear_op_float_mfma(eng, oracle, rows, K, N):
-    """Float mode on the fp32 matrix cores: 32 x 128 block tiles (4 chains per wave, the last
-    two shapes) and 16 x 64 tiles (2 chains per wave), the chains' partial tiles added in LDS;
-    ragged rows and columns, K tails."""
+    """Float mode on the fp32 matrix cores, one reference lane chain per wave: 32 x 64 tiles
+    of the 32x32 instruction (the last three shapes) and 16 x 64 tiles of the 16x16 one (the
+    first three), the chain tiles added in LDS; ragged rows and columns, K tails."""
     print(f"bitlinear float mfma rows={rows} K={K} N={N}", flush=True)
     rng = np.random.default_rng(rows * 3 + K + N)
     x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
@@ -266,7 +266,8 @@ def test_forward_float_mid_prompt(blobs, oracle):
 
 def test_forward_float_long_prompt(blobs, oracle):
     """6144-token float forward: every GEMM kind (i/f/g store, o and down residual add, the
-    gate/up swiglu pair) runs on 32 x 128 matrix-core tiles; all logits bit for bit."""
+    gate/up swiglu pair) runs on the 32 x 64 matrix-core tiles with hidden 768 and a K of
+    528 for down_proj; all logits bit for bit."""
     from matmulfreellmcpu_amd import Engine, read_blob
     print("forward float long prompt", flush=True)
     blob = read_blob(blobs("tall"))
