@@ -87,6 +87,17 @@ int mmf_bitlinear(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps,
  * equal shapes sharing the input x; bit-identical to k mmf_bitlinear calls. */
 int mmf_bitlinear_cluster(mmf_ctx* ctx, const int* proj_ids, int k, int mode, int frac_bits,
                           float eps, const float* x, float* const* outs, size_t rows);
+/* mmf_bitlinear without any device allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, results and errors as mmf_bitlinear; its
+ * scratch (the activation codes and split-K partials of the call) lives in a static device
+ * array of MMF_NOALLOC_SCRATCH_BYTES bytes, one per GPU, held until the process ends. A call
+ * whose scratch would exceed it fails with MMF_ERR_ARG before launching anything (split the
+ * rows over several calls). Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (from contexts with different streams, or other threads) race. */
+#define MMF_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mmf_bitlinear_noalloc(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps, const float* x,
+                          float* out, size_t rows, int32_t* acc);
 /* The integer input of a FixedQ510 BitLinear, for an external TernaryBackend: the RMSNorm
  * y = (x * rstd) * normw (bitlinear.cpp:62-70) and its Q5.10 codes (simd.hpp:162-187) as int32
  * codes [rows, K] (frac_bits fractional bits). dev pointers. */

@@ -63,6 +63,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_proj_shape": (i, [_vp, i, C.POINTER(_sz), C.POINTER(_sz)]),
         "mmf_ternary_matmul": (i, [_vp, i, _vp, _vp, _sz]),
         "mmf_bitlinear": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
+        "mmf_bitlinear_noalloc": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
         "mmf_bitlinear_cluster": (i, [_vp, C.POINTER(i), i, i, i, C.c_float, _vp, C.POINTER(_vp), _sz]),
         "mmf_rmsnorm": (i, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_float]),
         "mmf_swiglu": (i, [_vp, _vp, _vp, _vp, _sz]),
@@ -171,6 +172,11 @@ class Engine:
 
     def bitlinear(self, pid, x, out, rows, mode=FLOAT, frac_bits=10, eps=1e-6, acc=None):
         self._chk(self.lib.mmf_bitlinear(self.h, pid, mode, frac_bits, eps, _ptr(x), _ptr(out), rows, _ptr(acc)))
+
+    def bitlinear_noalloc(self, pid, x, out, rows, mode=FLOAT, frac_bits=10, eps=1e-6, acc=None):
+        """mmf_bitlinear with its scratch in the library's static device array (no allocation)."""
+        self._chk(self.lib.mmf_bitlinear_noalloc(self.h, pid, mode, frac_bits, eps, _ptr(x), _ptr(out), rows,
+                                                 _ptr(acc)))
 
     def bitlinear_cluster(self, pids, x, outs, rows, mode=FLOAT, frac_bits=10, eps=1e-6):
         k = len(pids)

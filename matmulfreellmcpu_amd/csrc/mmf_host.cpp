@@ -13,6 +13,7 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -246,7 +247,8 @@ void tend(mmf_ctx* c) {
 }
 
 // ---- activation buffers ---------------------------------------------------------------
-ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, int rows, int na) {
+// Geometry of the activations of `rows` rows for na projections, no buffers attached.
+ActBuf act_shape(const Geom& g, int rows, int na) {
   ActBuf a;
   a.Lc = g.Lc;
   a.K = g.K;
@@ -255,13 +257,28 @@ ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, 
   a.ntail = g.ntail;
   a.rows = rows;
   a.na = na;
-  const size_t nr = static_cast<size_t>(rows) * na;
+  return a;
+}
+
+// Bytes of the buffers y, q, ct, sa that `mode` uses for the activations a (0 if unused).
+void act_bytes(Mode mode, const ActBuf& a, size_t out[4]) {
+  const size_t nr = static_cast<size_t>(a.rows) * a.na;
+  out[0] = mode == kFloat ? nr * a.ystride() * sizeof(float) : 0;
+  out[1] = mode == kFloat ? 0 : 2 * static_cast<size_t>(a.na) * a.qplane();
+  out[2] = mode == kFloat ? 0 : nr * 8 * sizeof(int32_t);
+  out[3] = mode == kFloat ? 0 : nr * sizeof(float);
+}
+
+ActBuf make_act(DBuf& y, DBuf& q, DBuf& ct, DBuf& sa, Mode mode, const Geom& g, int rows, int na) {
+  ActBuf a = act_shape(g, rows, na);
+  size_t b[4];
+  act_bytes(mode, a, b);
   if (mode == kFloat) {
-    a.y = y.as<float>(nr * a.ystride());
+    a.y = static_cast<float*>(y.get(b[0]));
   } else {
-    a.q = q.as<int8_t>(2 * static_cast<size_t>(na) * a.qplane());
-    a.ct = ct.as<int32_t>(nr * 8);
-    a.sa = sa.as<float>(nr);
+    a.q = static_cast<int8_t*>(q.get(b[1]));
+    a.ct = static_cast<int32_t*>(ct.get(b[2]));
+    a.sa = static_cast<float*>(sa.get(b[3]));
   }
   return a;
 }
@@ -763,6 +780,31 @@ void clear_key(mmf_ctx* c, Model& m) {
 // =========================================================================================
 extern "C" {
 
+// Scratch of mmf_bitlinear_noalloc. Each GPU holds its own copy at its own address; host
+// code never passes the array's name to a kernel (on the host it is only a stand-in for the
+// symbol): it uses the device address that hipGetSymbolAddress returned for that GPU.
+static __device__ __align__(256) unsigned char scratch[MMF_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};  // device address of `scratch` per device, once resolved
+
+// Resolves the device address of `scratch` on `device`, which must be current. Called by
+// mmf_create once per device.
+hipError_t resolve_scratch(int device) {
+  if (device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[device]) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  g_scratch_dev[device] = p;
+  return hipSuccess;
+}
+}  // namespace
+
 int mmf_create(mmf_ctx** out, int device) {
   if (!out) return MMF_ERR_ARG;
   *out = nullptr;
@@ -786,6 +828,13 @@ int mmf_create(mmf_ctx** out, int device) {
   c->prop = prop;
   if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
     g_create_err = "stream creation failed";
+    delete c;
+    return MMF_ERR_HIP;
+  }
+  const hipError_t se = resolve_scratch(device);
+  if (se != hipSuccess) {
+    g_create_err = std::string("device address of the no-alloc scratch: ") + hipGetErrorString(se);
+    (void)hipStreamDestroy(c->stream);
     delete c;
     return MMF_ERR_HIP;
   }
@@ -886,19 +935,60 @@ int mmf_ternary_matmul(mmf_ctx* c, int id, const int32_t* x, int32_t* acc, size_
   });
 }
 
+// A fixed device region that one call carves its scratch from (mmf_bitlinear_noalloc).
+struct FixedScratch {
+  char* base;
+  size_t cap;
+};
+
+// fs == nullptr: the activations and the split-K partials live in the context's grow-only
+// buffers; otherwise in fs, and nothing is allocated (sizes beyond fs->cap are refused
+// before any launch).
 static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac, float eps, const float* x,
-                           float* const* outs, size_t rows, int32_t* acc) {
+                           float* const* outs, size_t rows, int32_t* acc, const FixedScratch* fs = nullptr) {
   if (k < 1 || k > 3) fail(MMF_ERR_ARG, "cluster size must be 1..3");
   if (mode < 0 || mode > 2) fail(MMF_ERR_ARG, "invalid mode");
   if (frac < 0 || frac > 30) fail(MMF_ERR_ARG, "invalid frac_bits");
   if (rows == 0) return;
+  if (rows > (1u << 24)) fail(MMF_ERR_ARG, "too many rows");
+  if (!x) fail(MMF_ERR_ARG, "null input");
+  for (int z = 0; z < k; ++z)
+    if (!outs[z]) fail(MMF_ERR_ARG, "null output");
   const Proj& p0 = proj_of(c, ids[0]);
   for (int z = 0; z < k; ++z) {
     const Proj& p = proj_of(c, ids[z]);
     if (p.d.g.N != p0.d.g.N || p.d.g.K != p0.d.g.K) fail(MMF_ERR_ARG, "cluster projections differ in shape");
     if (!p.d.normw) fail(MMF_ERR_ARG, "projection registered without a norm weight");
   }
-  ActBuf act = make_act(c->opy, c->opq, c->opct, c->opsa, static_cast<Mode>(mode), p0.d.g, static_cast<int>(rows), k);
+  const Mode md = static_cast<Mode>(mode);
+  GemmArgs ga = gemm_args(c, ids, k, static_cast<int>(rows), md, frac);
+  for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
+  ga.acc[0] = acc;
+  const size_t wsb = gemm_workspace_bytes(ga);
+  ActBuf act;
+  if (!fs) {
+    act = make_act(c->opy, c->opq, c->opct, c->opsa, md, p0.d.g, static_cast<int>(rows), k);
+    ga.ws = wsb ? static_cast<int32_t*>(c->gws.get(wsb)) : nullptr;
+  } else {
+    act = act_shape(p0.d.g, static_cast<int>(rows), k);
+    size_t b[5];
+    act_bytes(md, act, b);
+    b[4] = wsb;
+    size_t off[5], end = 0;
+    for (int i = 0; i < 5; ++i) {
+      off[i] = end;
+      end = (end + b[i] + 255) / 256 * 256;
+    }
+    if (end > fs->cap)
+      fail(MMF_ERR_ARG, "bitlinear needs " + std::to_string(end) + " bytes of scratch for " + std::to_string(rows) +
+                            " rows of this projection, more than the " + std::to_string(fs->cap) +
+                            " bytes of the static scratch: split the rows over several calls");
+    act.y = b[0] ? reinterpret_cast<float*>(fs->base + off[0]) : nullptr;
+    act.q = b[1] ? reinterpret_cast<int8_t*>(fs->base + off[1]) : nullptr;
+    act.ct = b[2] ? reinterpret_cast<int32_t*>(fs->base + off[2]) : nullptr;
+    act.sa = b[3] ? reinterpret_cast<float*>(fs->base + off[3]) : nullptr;
+    ga.ws = wsb ? reinterpret_cast<int32_t*>(fs->base + off[4]) : nullptr;
+  }
   PrologueArgs pa{};
   pa.x = x;
   pa.pre = kPreNone;
@@ -907,13 +997,10 @@ static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac
   pa.eps = eps;
   pa.qs = static_cast<float>(1u << frac);
   tbeg(c, kRkPrologue);
-  MMF_HIP(launch_prologue(static_cast<Mode>(mode), pa, act, c->stream));
+  MMF_HIP(launch_prologue(md, pa, act, c->stream));
   tend(c);
-  GemmArgs ga = gemm_args(c, ids, k, static_cast<int>(rows), static_cast<Mode>(mode), frac);
-  for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
-  ga.acc[0] = acc;
   tbeg(c, kRkGemmIFG);
-  run_gemm(c, ga, act, c->stream);
+  MMF_HIP(launch_gemm(ga, act, c->stream));
   tend(c);
 }
 
@@ -996,6 +1083,20 @@ double time_graph_runs(mmf_ctx* c, int warmup, int reps, F&& f) {
 int mmf_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out, size_t rows,
                   int32_t* acc) {
   return guard(c, [&] { bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, acc); });
+}
+
+int mmf_bitlinear_noalloc(mmf_ctx* c, int id, int mode, int frac, float eps, const float* x, float* out,
+                          size_t rows, int32_t* acc) {
+  return guard(c, [&] {
+    void* p = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_scratch_mu);
+      p = c->device < kMaxDevices ? g_scratch_dev[c->device] : nullptr;
+    }
+    if (!p) fail(MMF_ERR_STATE, "no-alloc scratch not resolved on this device");
+    const FixedScratch fs{static_cast<char*>(p), MMF_NOALLOC_SCRATCH_BYTES};
+    bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, acc, &fs);
+  });
 }
 
 int mmf_bitlinear_cluster(mmf_ctx* c, const int* ids, int k, int mode, int frac, float eps, const float* x,
