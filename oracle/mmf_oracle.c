@@ -7,6 +7,7 @@
  */
 #include "mmf_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -35,12 +36,17 @@ float mo_sumsq(const float* x, size_t n) {
 }
 
 /* ternary_dot_f32 (simd.hpp:92-122): 8 lanes acc = fma(y, (float)w, acc), hsum, then the
- * scalar tail as signed adds. */
+ * scalar tail as signed adds. The 8 lane chains are one 8-wide vector: each lane is the
+ * same single-rounding fma as fmaf, the vector form only converts the weights 8 at a time. */
 float mo_ternary_dot_f32(const float* y, const int8_t* w, size_t n) {
-  float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float a[8];
   size_t k = 0;
-  for (; k + 8 <= n; k += 8)
-    for (int j = 0; j < 8; ++j) a[j] = fmaf(y[k + j], (float)w[k + j], a[j]);
+  __m256 acc = _mm256_setzero_ps();
+  for (; k + 8 <= n; k += 8) {
+    const __m256 wv = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i*)(w + k))));
+    acc = _mm256_fmadd_ps(_mm256_loadu_ps(y + k), wv, acc);
+  }
+  _mm256_storeu_ps(a, acc);
   float s = mo_hsum8(a);
   for (; k < n; ++k) {
     if (w[k] > 0) s += y[k];
@@ -439,7 +445,7 @@ void mo_forward(const mo_model* m, int mode, int frac, const int64_t* ids, size_
 
 void mo_generate_serve(const mo_model* m, int mode, int frac, const int64_t* flat,
                        const size_t* lens, size_t B, size_t new_tokens, int64_t eos_id,
-                       int64_t* out, size_t cap_per, size_t* out_len) {
+                       int64_t* out, size_t cap_per, size_t* out_len, float* state_out) {
   const size_t H = m->H, L = m->L, V = m->V;
   float* st = (float*)calloc(L * B * H, sizeof(float));
   char* done = (char*)calloc(B, 1);
@@ -473,5 +479,6 @@ void mo_generate_serve(const mo_model* m, int mode, int frac, const int64_t* fla
     }
     if (all_done) break;
   }
+  if (state_out) memcpy(state_out, st, L * B * H * sizeof(float));
   free(st); free(done); free(lg); free(h);
 }

@@ -102,7 +102,7 @@ void mo_forward(const mo_model* m, int mode, int frac_bits, const int64_t* ids, 
  * out[b * cap_per + j]; out_len[b]. */
 void mo_generate_serve(const mo_model* m, int mode, int frac_bits, const int64_t* flat,
                        const size_t* lens, size_t B, size_t new_tokens, int64_t eos_id,
-                       int64_t* out, size_t cap_per, size_t* out_len);
+                       int64_t* out, size_t cap_per, size_t* out_len, float* state_out);
 
 /* Greedy argmax, first index wins ties (hgrn_model.cpp:270-273). */
 size_t mo_argmax(const float* v, size_t n);

@@ -87,7 +87,7 @@ class Oracle:
                                   C.c_size_t, C.c_int64, _i64p, _fp, _fp]
         L.mo_forward.argtypes = [C.POINTER(MoModel), C.c_int, C.c_int, _i64p, C.c_size_t, _fp]
         L.mo_generate_serve.argtypes = [C.POINTER(MoModel), C.c_int, C.c_int, _i64p, _szp,
-                                        C.c_size_t, C.c_size_t, C.c_int64, _i64p, C.c_size_t, _szp]
+                                        C.c_size_t, C.c_size_t, C.c_int64, _i64p, C.c_size_t, _szp, _fp]
         L.mo_argmax.restype = C.c_size_t
         L.mo_argmax.argtypes = [_fp, C.c_size_t]
 
@@ -245,17 +245,21 @@ class OracleModel:
         self.o.lib.mo_forward(C.byref(self.m), mode, frac_bits, _p(ids, _i64p), ids.size, _p(lg, _fp))
         return lg
 
-    def generate_serve(self, prompts, new_tokens, mode=FLOAT, frac_bits=10, eos_id=-1):
+    def generate_serve(self, prompts, new_tokens, mode=FLOAT, frac_bits=10, eos_id=-1, want_state=False):
+        """Id stream per stream; with want_state also the final recurrent state [L, B, H]."""
         flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int64) for p in prompts]))
         lens = np.array([len(p) for p in prompts], np.uintp)
         B = len(prompts)
         cap = int(lens.max()) + max(new_tokens, 1)
         out = np.zeros((B, cap), np.int64)
         out_len = np.zeros(B, np.uintp)
+        c = self.cfg
+        st = np.empty((c.num_hidden_layers, B, c.hidden_size), np.float32) if want_state else None
         self.o.lib.mo_generate_serve(C.byref(self.m), mode, frac_bits, _p(flat, _i64p),
                                      _p(lens, _szp), B, new_tokens, eos_id, _p(out, _i64p), cap,
-                                     _p(out_len, _szp))
-        return [out[b, :int(out_len[b])].copy() for b in range(B)]
+                                     _p(out_len, _szp), _p(st, _fp))
+        streams = [out[b, :int(out_len[b])].copy() for b in range(B)]
+        return (streams, st) if want_state else streams
 
     def trace(self, ids, mode=FLOAT, frac_bits=10):
         """Stateful prefill layer by layer: (h [L,T,H], state [L,H], internals [L,5,T,H])."""

@@ -73,6 +73,10 @@ def blobs(tmp_path_factory):
             make_blob(p, vocab=1000, hidden=100, layers=2, inter=208, seed=13, random_norms=True, random_lb=True)
         elif name == "s0":
             make_blob(p, preset="s0", seed=1234)
+        elif name == "h2048":  # the 1.3B widths (hidden 2048, intermediate 5632, vocab 32000), 2 layers
+            make_blob(p, vocab=32000, hidden=2048, layers=2, inter=5632, seed=41, random_norms=True, random_lb=True)
+        elif name == "h2560":  # the 2.7B widths (hidden 2560, intermediate 6912, vocab 32000), 2 layers
+            make_blob(p, vocab=32000, hidden=2560, layers=2, inter=6912, seed=43, random_norms=True, random_lb=True)
         else:
             raise KeyError(name)
         out[name] = p
