@@ -53,9 +53,14 @@ class Model {
 
   const Config& config() const { return cfg_; }
 
-  // The reference's backend injection (model.hpp:74-79). This engine runs the ternary
-  // projections on the GPU itself, so nullptr (the default) and a HipTernaryBackend are
-  // accepted and change nothing; any other backend is rejected with std::runtime_error.
+  // The reference's backend injection (model.hpp:74-79, hgrn_model.cpp:40-78). The backend is
+  // borrowed and must outlive the Model, as must the Weights. nullptr (the default) and a
+  // HipTernaryBackend keep the projections on this engine's GPU kernels. Any other backend
+  // receives the integer matmul of every FixedQ510 projection (tags
+  // model.layers.{l}.{i,f,g,o,gate,down}_proj and lm_head; proj_ids maps a tag to the
+  // backend's proj_id, -1 when absent): the GPU computes the RMSNorm and Q5.10 codes, the
+  // backend the accumulators (batch_size() rows per call; the i/f/g cluster through
+  // matmul_seq), the GPU dequantises and goes on. Float mode never uses the backend.
   void set_backend(TernaryBackend* be, std::unordered_map<std::string, int> proj_ids);
 
   // Recurrent state [num_hidden_layers][streams][hidden_size] after the last call.
@@ -64,11 +69,22 @@ class Model {
   mmf_ctx* context() const { return ctx_; }
 
  private:
+  // the external integer matmul (mmf_model_set_matmul) that forwards to backend_
+  static int backend_matmul(void* self, int layer, int proj, int k, const std::int32_t* codes, std::int32_t* acc,
+                            std::size_t K, std::size_t N, std::size_t rows);
+  void run_backend(int layer, int proj, int k, const std::int32_t* codes, std::int32_t* acc, std::size_t K,
+                   std::size_t N, std::size_t rows);
+  void check_call(int rc, const char* what);
+
   mmf_ctx* ctx_ = nullptr;
+  const Weights& w_;
   Config cfg_;
   ActQuant aq_;
   int frac_bits_;
   std::size_t streams_ = 1;
+  TernaryBackend* backend_ = nullptr;
+  std::unordered_map<std::string, int> proj_ids_;
+  std::string backend_error_;
 };
 
 }  // namespace mmfree

@@ -7,7 +7,8 @@
 //   x carries int16-range Q5.10 codes stored as int32; proj_id addresses resident weights
 //   (-1 = use the wq pointer); matmul_batch_chunked reports every column exactly once;
 //   matmul_seq's default is serial and bit-identical to k matmul_batch calls.
-// The MI355X implementation is HipTernaryBackend (mmfree/hip_backend.hpp).
+// The MI355X implementation is HipTernaryBackend (mmfree/hip_backend.hpp); CpuBackend
+// below is the host-CPU one.
 #pragma once
 
 #include <cstddef>
@@ -55,6 +56,28 @@ struct TernaryBackend {
   }
 
   virtual ~TernaryBackend() = default;
+};
+
+// The host-CPU backend (reference: ternary_backend.hpp:96-103): each output is the exact
+// integer sum of its row, outputs spread over OpenMP threads when the program is built
+// with OpenMP. Integer sums do not depend on their order, so the accumulators are the
+// same for any thread count. Sums wrap at 32 bits like the reference's SIMD adds (real
+// shapes never reach that: |code| <= 32768 and N <= 65536).
+struct CpuBackend final : TernaryBackend {
+  void matmul(int /*proj_id*/, const std::int32_t* x, std::int32_t* acc, const std::int8_t* wq, std::size_t N,
+              std::size_t M) override {
+    const std::ptrdiff_t outs = static_cast<std::ptrdiff_t>(M);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (std::ptrdiff_t o = 0; o < outs; ++o) {
+      const std::int8_t* w = wq + static_cast<std::size_t>(o) * N;
+      std::uint32_t s = 0;
+      for (std::size_t n = 0; n < N; ++n)
+        s += static_cast<std::uint32_t>(x[n]) * static_cast<std::uint32_t>(static_cast<std::int32_t>(w[n]));
+      acc[o] = static_cast<std::int32_t>(s);
+    }
+  }
 };
 
 }  // namespace mmfree

@@ -69,6 +69,12 @@ int mmf_download(mmf_ctx* ctx, void* host, const void* dev, size_t bytes);
  * (ternary_backend.hpp:26-31: proj_id addresses resident weights). */
 int mmf_proj_register(mmf_ctx* ctx, const int8_t* wq, size_t N, size_t K, float scale_w,
                       const float* normw, int* proj_id);
+/* Replace the weights of a registered projection with wq [N, K] of its registered shape
+ * (host memory, ternary int8): the seam's "the weights at wq now" contract of proj_id -1
+ * (ternary_backend.hpp:26-31) for a caller whose buffer now holds other weights. Scale and
+ * norm weight are kept. On MMF_ERR_ARG (a weight outside {-1, 0, +1}) the projection's
+ * weights are undefined until the next successful update. */
+int mmf_proj_update(mmf_ctx* ctx, int proj_id, const int8_t* wq);
 /* Shape of a registered projection. */
 int mmf_proj_shape(mmf_ctx* ctx, int proj_id, size_t* N, size_t* K);
 
@@ -133,6 +139,25 @@ int mmf_model_tensor(mmf_ctx* ctx, const char* name, int dtype, const size_t* sh
                      const void* data);
 int mmf_model_finalize(mmf_ctx* ctx, int mode, int frac_bits);
 int mmf_model_config(mmf_ctx* ctx, mmf_config* cfg);
+
+/* External integer matmul of the model's FixedQ510 projections: Model::set_backend with a
+ * TernaryBackend that is not this engine's (model.hpp:74-79, hgrn_model.cpp:40-78; the split
+ * of bitlinear.cpp:39-94 and bitlinear_cluster, :119-160). While fn is set (NULL clears it),
+ * every FixedQ510 projection of the model -- prefill, serving steps, generate, forward, trace
+ * -- computes its RMSNorm and Q5.10 codes on the device and calls
+ *     fn(user, layer, proj, k, codes, acc, K, N, rows)
+ * on the calling thread with host arrays: codes [k][rows][K] (int16-range codes as int32, in
+ * element order), to be answered with acc [k][rows][N], acc[j][r][o] = sum_n
+ * codes[j][r][n] * wq_j[o][n] (wrapping int32). proj is 0..5 for i, f, g, o, gate (N = 2I,
+ * the gate and up halves), down of `layer`, or 6 with layer -1 for the lm_head; k is 3 for
+ * the i/f/g cluster (proj 0, 1, 2), else 1. A non-zero return fails the model call with
+ * MMF_ERR_ARG. The accumulators are dequantised and consumed on the device as the built-in
+ * matmul's would be, so the results equal the built-in path's for a correct fn. Float and
+ * Int8Absmax projections ignore fn (the reference's float path has no backend, kernels.hpp
+ * :37-40). The timing entry points refuse to run while fn is set. */
+typedef int (*mmf_matmul_fn)(void* user, int layer, int proj, int k, const int32_t* codes, int32_t* acc,
+                             size_t K, size_t N, size_t rows);
+int mmf_model_set_matmul(mmf_ctx* ctx, mmf_matmul_fn fn, void* user);
 
 /* Greedy Model::generate (model.hpp:44-50, hgrn_model.cpp:249-347), decode loop on the
  * device. Writes the id stream (prompt + generated) to out (capacity cap) and its length to

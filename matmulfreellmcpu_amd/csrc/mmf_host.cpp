@@ -123,6 +123,12 @@ struct Model {
   hipGraphExec_t step_graph = nullptr;
   size_t step_B = 0;
   uint64_t step_epoch = 0;
+  // external integer matmul of the FixedQ510 projections (mmf_model_set_matmul)
+  mmf_matmul_fn ext_fn = nullptr;
+  void* ext_user = nullptr;
+  DBuf ext_codes, ext_acc;
+  std::vector<int32_t> ext_hcodes, ext_hacc;
+  bool ext_on() const { return ext_fn && mode == kFixed; }
 };
 
 // Optional per-launch timing of the row path: an event pair around each launch, summed
@@ -303,6 +309,35 @@ GemmArgs gemm_args(mmf_ctx* c, const int* ids, int n, int rows, Mode mode, int f
   return a;
 }
 
+// One projection group of the model: the built-in GEMM, or, with an external integer matmul
+// set in FixedQ510, codes to the host, the caller's accumulators back, and the same
+// dequantisation and output stage on the device (layer/proj as mmf_model_set_matmul names
+// them).
+void proj_gemm(mmf_ctx* c, Model& m, GemmArgs& ga, const ActBuf& act, hipStream_t st, int layer, int proj) {
+  if (!m.ext_on()) {
+    run_gemm(c, ga, act, st);
+    return;
+  }
+  const size_t k = ga.nmat, rows = ga.rows, K = act.K, N = ga.p[0].g.N;
+  int32_t* dcodes = m.ext_codes.as<int32_t>(k * rows * K);
+  int32_t* dacc = m.ext_acc.as<int32_t>(k * rows * N);
+  m.ext_hcodes.resize(k * rows * K);
+  m.ext_hacc.assign(k * rows * N, 0);
+  MMF_HIP(launch_planes_to_codes(act, kFixed, dcodes, st));
+  MMF_HIP(hipMemcpyAsync(m.ext_hcodes.data(), dcodes, k * rows * K * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  MMF_HIP(hipStreamSynchronize(st));
+  const int rc = m.ext_fn(m.ext_user, layer, proj, static_cast<int>(k), m.ext_hcodes.data(), m.ext_hacc.data(), K, N,
+                          rows);
+  if (rc != 0)
+    fail(MMF_ERR_ARG, "external matmul of layer " + std::to_string(layer) + " projection " + std::to_string(proj) +
+                          " failed (" + std::to_string(rc) + ")");
+  MMF_HIP(hipMemcpyAsync(dacc, m.ext_hacc.data(), k * rows * N * sizeof(int32_t), hipMemcpyHostToDevice, st));
+  ga.ws = dacc;
+  MMF_HIP(launch_acc_epilogue(ga, act, st));
+  // the host arrays are reused by the next projection: wait for the upload
+  MMF_HIP(hipStreamSynchronize(st));
+}
+
 // ---- model helpers -------------------------------------------------------------------
 Model& model_of(mmf_ctx* c) {
   if (!c->model.finalized) fail(MMF_ERR_STATE, "no model: call mmf_model_begin/tensor/finalize first");
@@ -383,7 +418,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.out[1] = fb;
     ga.out[2] = gb;
     tbeg(c, kRkGemmIFG);
-    run_gemm(c, ga, act, st);
+    proj_gemm(c, m, ga, act, st, l, 0);
     tend(c);
   }
   // gate, lower bound, swiglu, recurrence (hgrn_model.cpp:109-150). Independent streams
@@ -449,7 +484,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.add = h;
     ga.out[0] = resid;
     tbeg(c, kRkGemmO);
-    run_gemm(c, ga, act, st);
+    proj_gemm(c, m, ga, act, st, l, 3);
     tend(c);
   }
   // mlp_norm -> gate_proj -> swiglu (hgrn_model.cpp:167-185)
@@ -472,7 +507,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.out[0] = zb;
     ga.swiglu_n = rows * I;
     tbeg(c, kRkGemmGate);
-    run_gemm(c, ga, act, st);
+    proj_gemm(c, m, ga, act, st, l, 4);
     tend(c);
   }
   // down_proj -> h = resid + d (hgrn_model.cpp:187-194)
@@ -494,7 +529,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     ga.add = resid;
     ga.out[0] = h;
     tbeg(c, kRkGemmDown);
-    run_gemm(c, ga, act, st);
+    proj_gemm(c, m, ga, act, st, l, 5);
     tend(c);
   }
 }
@@ -516,7 +551,7 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   MMF_HIP(launch_prologue(mode, pa, act, c->stream));
   GemmArgs ga = gemm_args(c, &m.lm, 1, rows, mode, m.frac);
   ga.out[0] = logits;
-  run_gemm(c, ga, act, c->stream);
+  proj_gemm(c, m, ga, act, c->stream, -1, 6);
 }
 
 int lm_grid(const Model& m) {
@@ -773,6 +808,40 @@ void clear_key(mmf_ctx* c, Model& m) {
   MMF_HIP(hipMemsetAsync(m.hist_pos.p, 0, sizeof(int32_t), c->stream));
 }
 
+// Greedy B=1 decode on the row kernels, one launch sequence per token (the path while an
+// external matmul is set: it runs on the host, which the captured single-row decode graph
+// cannot call). hlast: the prompt's last hidden row; appends the generated ids to out.
+void generate_rows(mmf_ctx* c, Model& m, const float* hlast, size_t new_tokens, int64_t eos_id, int64_t* out,
+                   size_t& len, mmf_token_cb cb, void* user) {
+  const size_t H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+  RowScratch& s = m.rs;
+  float* lg = s.logits.as<float>(V);
+  int64_t* am = s.am.as<int64_t>(1);
+  int64_t* d = s.ids.as<int64_t>(1);
+  auto head = [&](const float* x) {
+    lm_rows(c, m, 1, x, lg);
+    MMF_HIP(launch_argmax_rows(lg, 1, static_cast<int>(V), am, c->stream));
+    int64_t t = 0;
+    MMF_HIP(hipMemcpyAsync(&t, am, sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+    return t;
+  };
+  int64_t t = head(hlast);
+  for (size_t k = 0; k < new_tokens; ++k) {
+    if (k > 0) {
+      MMF_HIP(hipMemcpyAsync(d, &t, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+      float* h = s.h.as<float>(H);
+      MMF_HIP(launch_embed(m.emb, d, h, 1, static_cast<int>(H), c->stream));
+      for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
+        layer_rows(c, m, static_cast<int>(l), 1, h, static_cast<float*>(m.state.p) + l * H, true, nullptr);
+      t = head(h);
+    }
+    out[len++] = t;
+    if (cb) cb(user, t);
+    if (t == eos_id) break;
+  }
+}
+
 }  // namespace
 
 // =========================================================================================
@@ -851,13 +920,14 @@ void mmf_destroy(mmf_ctx* c) {
   for (auto& kv : c->model.tensors)
     if (kv.second.p) (void)hipFree(kv.second.p);
   Model& m = c->model;
-  for (DBuf* b : {&m.h, &m.resid, &m.g, &m.recur, &m.z, &m.logits, &m.key, &m.hist, &m.hist_pos, &m.state})
+  for (DBuf* b : {&m.h, &m.resid, &m.g, &m.recur, &m.z, &m.logits, &m.key, &m.hist, &m.hist_pos, &m.state, &m.embT,
+                  &m.normT, &m.ext_codes, &m.ext_acc})
     b->release();
   RowScratch& s = m.rs;
   for (DBuf* b : {&s.ids, &s.h, &s.resid, &s.i, &s.f, &s.g, &s.recur, &s.scan, &s.z, &s.logits, &s.state0, &s.am,
-                  &s.acty, &s.actq, &s.actct, &s.actsa})
+                  &s.acty, &s.actq, &s.actct, &s.actsa, &s.segs})
     b->release();
-  for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate}) b->release();
+  for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate, &c->gws}) b->release();
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -911,6 +981,22 @@ int mmf_proj_register(mmf_ctx* c, const int8_t* wq, size_t N, size_t K, float sc
     void* raw = c->raw.get(N * K);
     MMF_HIP(hipMemcpyAsync(raw, wq, N * K, hipMemcpyHostToDevice, c->stream));
     *proj_id = register_proj(c, static_cast<const int8_t*>(raw), N, K, scale_w, normw, nullptr);
+  });
+}
+
+int mmf_proj_update(mmf_ctx* c, int id, const int8_t* wq) {
+  return guard(c, [&] {
+    if (!wq) fail(MMF_ERR_ARG, "null argument");
+    const Proj& P = proj_of(c, id);
+    const Geom& g = P.d.g;
+    const size_t NK = static_cast<size_t>(g.N) * g.K;
+    void* raw = c->raw.get(NK);
+    MMF_HIP(hipMemcpyAsync(raw, wq, NK, hipMemcpyHostToDevice, c->stream));
+    const hipError_t e = launch_pack(static_cast<const int8_t*>(raw), g, const_cast<uint32_t*>(P.d.pk),
+                                     const_cast<int8_t*>(P.d.tail), const_cast<int32_t*>(P.d.rowsum), c->stream);
+    if (e == hipErrorInvalidValue) fail(MMF_ERR_ARG, "projection weights must be ternary (-1, 0, +1)");
+    MMF_HIP(e);
+    MMF_HIP(launch_pack_mfma(P.d.pk, g, P.d.pair != 0, const_cast<uint32_t*>(P.d.pkm), c->stream));
   });
 }
 
@@ -1304,6 +1390,11 @@ int mmf_model_generate(mmf_ctx* c, const int64_t* ids, size_t n, size_t new_toke
       if (out_len) *out_len = len;
       return;
     }
+    if (m.ext_on()) {  // the external matmul runs on the host: one row step at a time
+      generate_rows(c, m, h + (n - 1) * m.cfg.hidden_size, new_tokens, eos_id, out, len, cb, user);
+      if (out_len) *out_len = len;
+      return;
+    }
     MMF_HIP(launch_to_chain(h + (n - 1) * m.cfg.hidden_size, static_cast<float*>(m.h.p), 1,
                             static_cast<int>(m.cfg.hidden_size), m.gH.Lc, c->stream));
     lm_single(c, m, static_cast<float*>(m.h.p), nullptr, true);
@@ -1438,7 +1529,9 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
       lm_rows(c, m, static_cast<int>(B), h, lg);
       MMF_HIP(launch_argmax_rows(lg, static_cast<int>(B), static_cast<int>(V), am, c->stream));
     };
-    if (m.step_graph && m.step_B == B && m.step_epoch == dbuf_epoch.load()) {
+    if (m.ext_on()) {  // the external matmul runs on the host: no graph
+      work();
+    } else if (m.step_graph && m.step_B == B && m.step_epoch == dbuf_epoch.load()) {
       MMF_HIP(hipGraphLaunch(m.step_graph, c->stream));
     } else {
       work();
@@ -1459,6 +1552,14 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
     if (logits) MMF_HIP(hipMemcpyAsync(logits, lg, B * V * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     if (argmax) MMF_HIP(hipMemcpyAsync(argmax, am, B * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
     MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_model_set_matmul(mmf_ctx* c, mmf_matmul_fn fn, void* user) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    m.ext_fn = fn;
+    m.ext_user = fn ? user : nullptr;
   });
 }
 
@@ -1507,6 +1608,7 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
   return guard(c, [&] {
     Model& m = model_of(c);
     if (reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid reps");
+    if (m.ext_on()) fail(MMF_ERR_STATE, "timing runs the built-in kernels: clear the external matmul first");
     if (m.streams != 1) reset_state(c, m, 1);
     if (m.hist_cap < static_cast<size_t>(warmup + reps) + 1) {
       m.hist.as<int64_t>(warmup + reps + 1);
@@ -1609,6 +1711,7 @@ int mmf_model_time_prefill(mmf_ctx* c, const int64_t* ids, size_t T, int warmup,
   return guard(c, [&] {
     Model& m = model_of(c);
     if (!ids || T == 0 || reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid prompt/reps");
+    if (m.ext_on()) fail(MMF_ERR_STATE, "timing runs the built-in kernels: clear the external matmul first");
     if (m.streams != 1) reset_state(c, m, 1);
     const int H = static_cast<int>(m.cfg.hidden_size);
     auto f = [&] {

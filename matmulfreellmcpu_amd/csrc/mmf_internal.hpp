@@ -166,6 +166,9 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
 
 // Integer codes [rows, K] (int16-range, as int32) -> planes (TernaryBackend path).
 hipError_t launch_codes_to_planes(const int32_t* x, ActBuf& act, hipStream_t s);
+// The inverse: planes (and tail codes) of act's na projections -> int32 codes
+// [na][rows][K] in natural element order, for an external integer matmul.
+hipError_t launch_planes_to_codes(const ActBuf& act, Mode mode, int32_t* codes, hipStream_t s);
 
 enum EpiKind : int { kEpiStore = 0, kEpiAdd = 1, kEpiSwigluPair = 2 };
 
@@ -185,11 +188,17 @@ struct GemmArgs {
   // of exact int32 sums in ws, reduced in split order by a second kernel
   int ksplit;
   int32_t* ws;
+  // launch_acc_epilogue: ws holds complete accumulators [nmat][rows][N] (tails and the
+  // Q5.10 bias included, as an external integer matmul returns them)
+  bool ext_acc;
 };
 // Dispatches the integer modes to the matrix-core kernel (mmf_mfma.hip) from
 // mfma_min_rows() rows on, everything else to the dot-product kernel.
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s);
+// Dequantisation and output stage (a.epi) of complete integer accumulators a.ws
+// [nmat][rows][N] (integer modes): what the GEMM's epilogue does after its own matmul.
+hipError_t launch_acc_epilogue(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 // Float mode on the fp32 matrix cores (mmf_mfma_f.hip), bit-exact with the FMA chains;
 // used from float_mfma_min_rows() rows on when mfma_f_ok(a).
 bool mfma_f_ok(const GemmArgs& a);

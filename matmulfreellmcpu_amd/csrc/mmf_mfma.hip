@@ -475,10 +475,13 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   const float* const addp = a.add;
   const int8_t* const tailp = W.tail;
   const int32_t* const rsum = W.rowsum;
-  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = W.g.ntail, ksplit = a.ksplit, nmat = a.nmat;
+  // complete accumulators (ext_acc) already hold the tail products and the Q5.10 bias
+  const int bias = a.ext_acc ? 0 : 1;
+  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = bias ? W.g.ntail : 0, ksplit = a.ksplit,
+            nmat = a.nmat;
   const float invf = a.inv_fixed[z], scw = W.scale_w;
   MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rsum), "s"(rawacc), "s"(swn), "s"(ntail),
-          "s"(ksplit), "s"(nmat), "s"(invf), "s"(scw));
+          "s"(ksplit), "s"(nmat), "s"(invf), "s"(scw), "s"(bias));
   for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < n;
        e += static_cast<size_t>(gridDim.x) * blockDim.x) {
     const int row = static_cast<int>(e / Nout), o0 = static_cast<int>(e % Nout);
@@ -499,7 +502,7 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) s += pv[u];
       }
-      if (MODE == kFixed) s += 128 * rsum[o];
+      if (MODE == kFixed && bias) s += 128 * rsum[o];
       if (ntail) {
         const int32_t* ct = act.ct + ar * 8;
         int32_t tw[8], tc[8];
@@ -663,6 +666,32 @@ size_t gemm_workspace_bytes(const GemmArgs& a) {
 
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   return a.mode == kFixed ? mfma_mode<kFixed>(a, act, s) : mfma_mode<kInt8>(a, act, s);
+}
+
+template <int MODE, int EPI>
+static hipError_t acc_epi_inst(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  GemmArgs b = a;
+  b.ksplit = 1;
+  b.ext_acc = true;
+  const int Nout = EPI == kEpiSwigluPair ? a.p[0].g.N / 2 : a.p[0].g.N;
+  const size_t n = static_cast<size_t>(a.rows) * Nout;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 4096));
+  k_splitk_epi<MODE, EPI><<<dim3(blocks, 1, EPI == kEpiSwigluPair ? 1 : a.nmat), 256, 0, s>>>(b, act);
+  return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t acc_epi_mode(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  switch (a.epi) {
+    case kEpiSwigluPair: return acc_epi_inst<MODE, kEpiSwigluPair>(a, act, s);
+    case kEpiAdd: return acc_epi_inst<MODE, kEpiAdd>(a, act, s);
+    default: return acc_epi_inst<MODE, kEpiStore>(a, act, s);
+  }
+}
+
+hipError_t launch_acc_epilogue(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
+  if (a.mode == kFloat || !a.ws || a.rows <= 0) return hipErrorInvalidValue;
+  return a.mode == kFixed ? acc_epi_mode<kFixed>(a, act, s) : acc_epi_mode<kInt8>(a, act, s);
 }
 
 }  // namespace mmf

@@ -463,6 +463,24 @@ __global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
     act.ct[static_cast<size_t>(row) * 8 + t] = (t < act.ntail) ? xr[act.K8 + t] : 0;
 }
 
+// planes -> int32 codes [na][rows][K] in natural element order (the inverse of k_codes, for
+// an external TernaryBackend): FixedQ510 code = 256 * hi + lo + 128, Int8Absmax code = the
+// plane-0 byte; the tail codes come from ct. One block per (row, projection).
+__global__ void k_planes_to_codes(ActBuf act, int mode, int32_t* __restrict__ codes) {
+  const int row = xcd_row(blockIdx.x), ai = blockIdx.y, Lc = act.Lc;
+  if (row >= act.rows) return;
+  const int8_t* q = act.q + act.qoff(ai, 0, row, 0);
+  const size_t lop = act.qplane();
+  const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+  int32_t* out = codes + ar * act.K;
+  for (int k = threadIdx.x; k < act.K8; k += blockDim.x) {
+    const size_t o = ActBuf::qpos((k & 7) * Lc + (k >> 3));
+    const int hi = q[o];
+    out[k] = mode == kFixed ? hi * 256 + static_cast<int>(q[lop + o]) + 128 : hi;
+  }
+  for (int t = threadIdx.x; t < act.ntail; t += blockDim.x) out[act.K8 + t] = act.ct[ar * 8 + t];
+}
+
 // ------------------------------------------------------------------------------------
 // Ternary GEMM over row tiles. Block = 16 outputs x 8 chains; R rows per block; the
 // activations of one chunk of MW words per chain are staged in LDS for all R rows.
@@ -1285,6 +1303,12 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
 
 hipError_t launch_codes_to_planes(const int32_t* x, ActBuf& act, hipStream_t s) {
   k_codes<<<row_grid(act.rows), 256, 0, s>>>(x, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_planes_to_codes(const ActBuf& act, Mode mode, int32_t* codes, hipStream_t s) {
+  if (mode == kFloat || act.na < 1 || act.na > 3) return hipErrorInvalidValue;
+  k_planes_to_codes<<<dim3(row_grid(act.rows), act.na), 256, 0, s>>>(act, mode, codes);
   return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "content_hash.hpp"
 #include "mmfree_hip.h"
 
 namespace mmfree {
@@ -27,7 +28,7 @@ int HipTernaryBackend::register_projection(const std::int8_t* wq, std::size_t N,
   int id = -1;
   // the seam's wq is [M outputs, N inputs]; the C ABI names them (N, K)
   check(ctx_, mmf_proj_register(ctx_, wq, M, N, 1.0f, nullptr, &id), "mmf_proj_register");
-  by_ptr_[{wq, N, M}] = id;
+  by_ptr_[{wq, N, M}] = Resident{id, detail::content_hash(wq, N * M)};
   return id;
 }
 
@@ -39,7 +40,15 @@ int HipTernaryBackend::resolve(int proj_id, const std::int8_t* wq, std::size_t N
     return proj_id;
   }
   auto it = by_ptr_.find({wq, N, M});
-  return it != by_ptr_.end() ? it->second : register_projection(wq, N, M);
+  if (it == by_ptr_.end()) return register_projection(wq, N, M);
+  // the weights at wq now: a buffer refilled with other weights (or another blob mapped at the
+  // same address) replaces the resident copy in place
+  const std::uint64_t h = detail::content_hash(wq, N * M);
+  if (h != it->second.hash) {
+    check(ctx_, mmf_proj_update(ctx_, it->second.id, wq), "mmf_proj_update");
+    it->second.hash = h;
+  }
+  return it->second.id;
 }
 
 void HipTernaryBackend::ensure(std::size_t xbytes, std::size_t accbytes) {

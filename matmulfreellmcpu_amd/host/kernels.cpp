@@ -19,6 +19,7 @@
 #include <tuple>
 #include <vector>
 
+#include "content_hash.hpp"
 #include "mmfree/hip_backend.hpp"
 #include "mmfree_hip.h"
 
@@ -29,11 +30,7 @@ void check(mmf_ctx* c, int rc, const char* what) {
   if (rc != MMF_OK) throw std::runtime_error(std::string(what) + ": " + mmf_last_error(c));
 }
 
-std::uint64_t fnv(const void* p, std::size_t n, std::uint64_t h = 1469598103934665603ull) {
-  const unsigned char* b = static_cast<const unsigned char*>(p);
-  for (std::size_t i = 0; i < n; ++i) h = (h ^ b[i]) * 1099511628211ull;
-  return h;
-}
+using detail::content_hash;
 
 struct DevMem {
   mmf_ctx* c;
@@ -58,9 +55,9 @@ struct Default {
   }
   ~Default() { mmf_destroy(c); }
   int proj(const int8_t* wq, std::size_t N, std::size_t K, float scale_w, const float* normw) {
-    std::uint64_t h = fnv(wq, N * K);
-    h = fnv(&scale_w, sizeof scale_w, h);
-    h = fnv(normw, K * sizeof(float), h);
+    std::uint64_t h = content_hash(wq, N * K);
+    h = content_hash(&scale_w, sizeof scale_w, h);
+    h = content_hash(normw, K * sizeof(float), h);
     auto key = std::make_tuple(static_cast<const void*>(wq), N, K, h);
     auto it = projs.find(key);
     if (it != projs.end()) return it->second;
@@ -140,7 +137,42 @@ void bitlinear_cluster(float* const* outs, const float* x, const float* const* n
                        const float* scale_w, int k, std::size_t rows, std::size_t in_dim, std::size_t out_dim, float eps,
                        int frac_bits, TernaryBackend* be, const int* proj_ids) {
   if (k <= 0 || !rows) return;
-  if (foreign(be) || k > 3) {  // the reference's equivalence: k bitlinear calls (kernels.hpp:46-50)
+  const std::size_t K = in_dim, N = out_dim;
+  if (foreign(be)) {
+    // the reference's cluster over the seam (bitlinear.cpp:119-160): every projection's codes
+    // from the GPU, then per chunk of batch_size() rows one matmul_seq whose produce hands
+    // over projection j's codes and whose consume dequantises its accumulators
+    std::vector<std::int32_t> q(static_cast<std::size_t>(k) * rows * K);
+    {
+      Default& d = dflt();
+      std::lock_guard<std::mutex> lk(d.mu);
+      DevMem dx(d.c, rows * K * 4, x), dq(d.c, rows * K * 4);
+      for (int j = 0; j < k; ++j) {
+        DevMem dw(d.c, K * 4, norm_weights[j]);
+        check(d.c,
+              mmf_bitlinear_codes(d.c, dx.as<float>(), dw.as<float>(), dq.as<int32_t>(), rows, K, eps, frac_bits),
+              "mmf_bitlinear_codes");
+        dq.get(q.data() + static_cast<std::size_t>(j) * rows * K, rows * K * 4);
+      }
+    }
+    std::vector<int> ids(k, -1);
+    if (proj_ids) ids.assign(proj_ids, proj_ids + k);
+    const float qs = static_cast<float>(1u << frac_bits);
+    const std::size_t B = std::max<std::size_t>(1, be->batch_size());
+    for (std::size_t r0 = 0; r0 < rows; r0 += B) {
+      const std::size_t bn = std::min(B, rows - r0);
+      be->matmul_seq(
+          ids.data(), wqs, k,
+          [&](int j, std::int32_t* xq) { std::copy_n(q.data() + (j * rows + r0) * K, bn * K, xq); },
+          [&](int j, const std::int32_t* acc) {
+            const float inv_fixed = 1.0f / (qs * scale_w[j]);
+            for (std::size_t e = 0; e < bn * N; ++e) outs[j][r0 * N + e] = static_cast<float>(acc[e]) * inv_fixed;
+          },
+          K, N, bn);
+    }
+    return;
+  }
+  if (k > 3) {  // the reference's equivalence: k bitlinear calls (kernels.hpp:46-50)
     for (int j = 0; j < k; ++j)
       bitlinear(outs[j], x, norm_weights[j], wqs[j], scale_w[j], rows, in_dim, out_dim, eps, nullptr,
                 ActQuant::FixedQ510, frac_bits, be, proj_ids ? proj_ids[j] : -1);
@@ -148,7 +180,6 @@ void bitlinear_cluster(float* const* outs, const float* x, const float* const* n
   }
   Default& d = dflt();
   std::lock_guard<std::mutex> lk(d.mu);
-  const std::size_t K = in_dim, N = out_dim;
   std::vector<int> ids(k);
   for (int j = 0; j < k; ++j) ids[j] = d.proj(wqs[j], N, K, scale_w[j], norm_weights[j]);
   DevMem dx(d.c, rows * K * 4, x);

@@ -78,20 +78,21 @@ void trampoline(void* user, std::int64_t id) { (*static_cast<const std::function
 
 }  // namespace
 
-Model::Model(const Weights& w, ActQuant aq, int frac_bits) : cfg_(w.config()), aq_(aq), frac_bits_(frac_bits) {
+Model::Model(const Weights& w, ActQuant aq, int frac_bits)
+    : w_(w), cfg_(w.config()), aq_(aq), frac_bits_(frac_bits) {
   const int rc = mmf_create(&ctx_, device_index());
   if (rc != MMF_OK) throw std::runtime_error(std::string("mmfree: ") + mmf_last_error(nullptr));
   try {
     mmf_config c{cfg_.vocab_size, cfg_.hidden_size, cfg_.num_hidden_layers, cfg_.intermediate_size,
                  cfg_.use_lower_bound ? 1 : 0, cfg_.rms_norm_eps};
-    check(ctx_, mmf_model_begin(ctx_, &c), "mmf_model_begin");
+    check_call(mmf_model_begin(ctx_, &c), "mmf_model_begin");
     for (const std::string& name : w.names()) {
       const TensorRef& t = w.get(name);
-      check(ctx_, mmf_model_tensor(ctx_, name.c_str(), t.is_int8 ? 1 : 0, t.shape.data(), static_cast<int>(t.shape.size()),
+      check_call(mmf_model_tensor(ctx_, name.c_str(), t.is_int8 ? 1 : 0, t.shape.data(), static_cast<int>(t.shape.size()),
                                    t.data),
             "mmf_model_tensor");
     }
-    check(ctx_, mmf_model_finalize(ctx_, mode_of(aq), frac_bits), "mmf_model_finalize");
+    check_call(mmf_model_finalize(ctx_, mode_of(aq), frac_bits), "mmf_model_finalize");
   } catch (...) {
     mmf_destroy(ctx_);
     ctx_ = nullptr;
@@ -102,17 +103,97 @@ Model::Model(const Weights& w, ActQuant aq, int frac_bits) : cfg_(w.config()), a
 Model::~Model() { mmf_destroy(ctx_); }
 
 void Model::set_backend(TernaryBackend* be, std::unordered_map<std::string, int> proj_ids) {
-  (void)proj_ids;
-  if (be && !dynamic_cast<HipTernaryBackend*>(be))
-    throw std::runtime_error(
-        "mmfree: this Model runs the ternary projections on the GPU; a CPU/FPGA TernaryBackend "
-        "can be used with the operator functions (bitlinear) instead");
+  // a HipTernaryBackend runs the same kernels this Model already uses: nothing to route
+  const bool external = be && !dynamic_cast<HipTernaryBackend*>(be);
+  check_call(mmf_model_set_matmul(ctx_, external ? &Model::backend_matmul : nullptr, external ? this : nullptr),
+        "mmf_model_set_matmul");
+  backend_ = external ? be : nullptr;
+  proj_ids_ = std::move(proj_ids);
+}
+
+// Called by the engine for each FixedQ510 projection group while an external backend is set.
+// Exceptions must not cross the C ABI: the message is kept and rethrown by check_call.
+int Model::backend_matmul(void* self, int layer, int proj, int k, const std::int32_t* codes, std::int32_t* acc,
+                          std::size_t K, std::size_t N, std::size_t rows) {
+  Model* m = static_cast<Model*>(self);
+  try {
+    m->run_backend(layer, proj, k, codes, acc, K, N, rows);
+    return 0;
+  } catch (const std::exception& e) {
+    m->backend_error_ = e.what();
+  } catch (...) {
+    m->backend_error_ = "TernaryBackend threw a non-standard exception";
+  }
+  return 1;
+}
+
+// The reference's calls into the seam (bitlinear.cpp:39-94, :119-160): rows in chunks of
+// batch_size(); one matmul_batch_chunked per chunk for a single projection, one matmul_seq
+// per chunk for the i/f/g cluster. codes [k][rows][K] and acc [k][rows][N] are contiguous,
+// so a chunk's rows are handed over in place.
+void Model::run_backend(int layer, int proj, int k, const std::int32_t* codes, std::int32_t* acc, std::size_t K,
+                        std::size_t N, std::size_t rows) {
+  static const char* const kProj[6] = {"i_proj", "f_proj", "g_proj", "o_proj", "gate_proj", "down_proj"};
+  if (k < 1 || k > 3 || proj < 0 || proj + k > (proj == 6 ? 7 : 6))
+    throw std::runtime_error("mmfree: invalid projection group from the engine");
+  int ids[3];
+  const std::int8_t* wqs[3];
+  for (int j = 0; j < k; ++j) {
+    const std::string tag =
+        proj == 6 ? std::string("lm_head") : "model.layers." + std::to_string(layer) + "." + kProj[proj + j];
+    const TensorRef& wq = w_.get(tag + ".wq");
+    if (wq.shape.size() != 2 || wq.shape[0] != N || wq.shape[1] != K)
+      throw std::runtime_error("mmfree: " + tag + ".wq does not have the projection's shape");
+    wqs[j] = wq.i8();
+    auto it = proj_ids_.find(tag);
+    ids[j] = it == proj_ids_.end() ? -1 : it->second;
+  }
+  const std::size_t B = std::max<std::size_t>(1, backend_->batch_size());
+  std::vector<char> seen;
+  for (std::size_t r0 = 0; r0 < rows; r0 += B) {
+    const std::size_t bn = std::min(B, rows - r0);
+    if (k == 1) {
+      // every column must be reported exactly once (ternary_backend.hpp contract)
+      seen.assign(N, 0);
+      bool bad = false;
+      backend_->matmul_batch_chunked(ids[0], codes + r0 * K, acc + r0 * N, wqs[0], K, N, bn,
+                                     [&](std::size_t col0, std::size_t ncols) {
+                                       if (col0 > N || ncols > N - col0) {
+                                         bad = true;
+                                         return;
+                                       }
+                                       for (std::size_t o = col0; o < col0 + ncols; ++o) bad |= seen[o]++ != 0;
+                                     });
+      if (bad || std::count(seen.begin(), seen.end(), 1) != static_cast<std::ptrdiff_t>(N))
+        throw std::runtime_error("mmfree: the TernaryBackend did not report every column exactly once");
+    } else {
+      backend_->matmul_seq(
+          ids, wqs, k,
+          [&](int j, std::int32_t* xq) {
+            std::copy_n(codes + (static_cast<std::size_t>(j) * rows + r0) * K, bn * K, xq);
+          },
+          [&](int j, const std::int32_t* a) {
+            std::copy_n(a, bn * N, acc + (static_cast<std::size_t>(j) * rows + r0) * N);
+          },
+          K, N, bn);
+    }
+  }
+}
+
+void Model::check_call(int rc, const char* what) {
+  if (rc == MMF_OK) return;
+  if (!backend_error_.empty()) {
+    std::string e;
+    e.swap(backend_error_);
+    throw std::runtime_error(e);
+  }
+  check(ctx_, rc, what);
 }
 
 void Model::forward(const std::int64_t* ids, std::size_t T, std::vector<float>& logits) {
   MMFREE_PROFILE("forward");
   logits.assign(T * cfg_.vocab_size, 0.0f);
-  check(ctx_, mmf_model_forward(ctx_, ids, T, logits.data()), "mmf_model_forward");
+  check_call(mmf_model_forward(ctx_, ids, T, logits.data()), "mmf_model_forward");
 }
 
 std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, std::size_t new_tokens,
@@ -124,11 +205,10 @@ std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, 
     MMFREE_PROFILE("generate");
     std::vector<std::int64_t> out(ids.size() + new_tokens);
     std::size_t len = 0;
-    check(ctx_,
-          mmf_model_generate(ctx_, ids.data(), ids.size(), new_tokens, eos_id, out.data(), out.size(), &len,
-                             on_token ? &trampoline : nullptr,
-                             on_token ? const_cast<void*>(static_cast<const void*>(&on_token)) : nullptr),
-          "mmf_model_generate");
+    check_call(mmf_model_generate(ctx_, ids.data(), ids.size(), new_tokens, eos_id, out.data(), out.size(), &len,
+                                  on_token ? &trampoline : nullptr,
+                                  on_token ? const_cast<void*>(static_cast<const void*>(&on_token)) : nullptr),
+               "mmf_model_generate");
     out.resize(len);
     return out;
   }
@@ -137,17 +217,17 @@ std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, 
   std::vector<float> lg(V);
   std::vector<std::size_t> cand;
   std::mt19937_64 rng(samp.seed);
-  check(ctx_, mmf_model_reset(ctx_, 1), "mmf_model_reset");
+  check_call(mmf_model_reset(ctx_, 1), "mmf_model_reset");
   {
     MMFREE_PROFILE("prefill");
-    check(ctx_, mmf_model_prefill(ctx_, 0, ids.data(), ids.size(), lg.data(), nullptr), "mmf_model_prefill");
+    check_call(mmf_model_prefill(ctx_, 0, ids.data(), ids.size(), lg.data(), nullptr), "mmf_model_prefill");
   }
   if (new_tokens == 0) return stream;
   for (std::size_t step = 0; step < new_tokens; ++step) {
     if (step > 0) {
       MMFREE_PROFILE("decode");
       const std::int64_t t = stream.back();
-      check(ctx_, mmf_model_step(ctx_, &t, lg.data(), nullptr), "mmf_model_step");
+      check_call(mmf_model_step(ctx_, &t, lg.data(), nullptr), "mmf_model_step");
     }
     std::int64_t t;
     {
@@ -177,7 +257,7 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
   std::vector<char> done(B, 0);
   std::vector<float> lg(greedy ? 0 : B * V);
   std::vector<std::int64_t> am(B);
-  check(ctx_, mmf_model_reset(ctx_, B), "mmf_model_reset");
+  check_call(mmf_model_reset(ctx_, B), "mmf_model_reset");
   streams_ = B;
   // all prompts prefilled together (the same states and first tokens as the reference's
   // stream-by-stream prefill), then the first-token callbacks in stream order, each stream
@@ -190,7 +270,7 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
       cat.insert(cat.end(), prompts[b].begin(), prompts[b].end());
       lens[b] = prompts[b].size();
     }
-    check(ctx_, mmf_model_prefill_streams(ctx_, B, cat.data(), lens.data(), greedy ? nullptr : lg.data(), am.data()),
+    check_call(mmf_model_prefill_streams(ctx_, B, cat.data(), lens.data(), greedy ? nullptr : lg.data(), am.data()),
           "mmf_model_prefill_streams");
   }
   for (std::size_t b = 0; b < B; ++b) {
@@ -205,7 +285,7 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
     for (std::size_t b = 0; b < B; ++b) tok[b] = streams[b].back();
     {
       MMFREE_PROFILE("decode");
-      check(ctx_, mmf_model_step(ctx_, tok.data(), greedy ? nullptr : lg.data(), am.data()), "mmf_model_step");
+      check_call(mmf_model_step(ctx_, tok.data(), greedy ? nullptr : lg.data(), am.data()), "mmf_model_step");
     }
     bool all_done = true;
     for (std::size_t b = 0; b < B; ++b) {

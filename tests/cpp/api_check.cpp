@@ -3,13 +3,17 @@
 // Reads raw inputs written by the test into DIR, writes raw outputs back:
 //   bitlinear (Float / FixedQ510 / Int8Absmax, norm_out, FixedQ510 through an external
 //   TernaryBackend and through HipTernaryBackend), rmsnorm, swiglu, hgrn_scan,
-//   rmsnorm_swishgate; Model::generate (sampled) and Model::generate_serve (greedy, sampled).
+//   rmsnorm_swishgate; Model::generate (sampled) and Model::generate_serve (greedy, sampled);
+//   Model::set_backend with a CpuBackend, a batching backend with a tag map and a throwing
+//   backend; HipTernaryBackend with one host weight buffer refilled between calls.
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
 #include <functional>
 #include <sstream>
+#include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "mmfree/hip_backend.hpp"
@@ -54,6 +58,48 @@ struct TestCpuBackend final : TernaryBackend {
   std::size_t batch_size() const override { return 3; }
 };
 
+// Batches 3 rows and reports each projection's columns in two ranges, the upper one first;
+// counts the calls and checks that the tag map's proj_ids arrive (lm_head -> 77,
+// layer 0 o_proj -> 5, every other tag -1).
+struct ChunkedBackend final : TernaryBackend {
+  std::size_t calls = 0, seq_calls = 0, lm_calls = 0, bad_ids = 0;
+  void matmul(int, const std::int32_t* x, std::int32_t* acc, const std::int8_t* wq, std::size_t N,
+              std::size_t M) override {
+    for (std::size_t o = 0; o < M; ++o) {
+      std::int64_t s = 0;
+      for (std::size_t n = 0; n < N; ++n) s += static_cast<std::int64_t>(x[n]) * wq[o * N + n];
+      acc[o] = static_cast<std::int32_t>(s);
+    }
+  }
+  std::size_t batch_size() const override { return 3; }
+  void matmul_batch_chunked(int proj_id, const std::int32_t* x, std::int32_t* acc, const std::int8_t* wq,
+                            std::size_t N, std::size_t M, std::size_t b,
+                            const std::function<void(std::size_t, std::size_t)>& on_cols) override {
+    ++calls;
+    if (proj_id == 77) ++lm_calls;
+    else if (proj_id != -1 && proj_id != 5) ++bad_ids;
+    matmul_batch(proj_id, x, acc, wq, N, M, b);
+    const std::size_t half = M / 2;
+    on_cols(half, M - half);
+    if (half) on_cols(0, half);
+  }
+  void matmul_seq(const int* proj_ids, const std::int8_t* const* wqs, int k,
+                  const std::function<void(int, std::int32_t*)>& produce,
+                  const std::function<void(int, const std::int32_t*)>& consume, std::size_t N, std::size_t M,
+                  std::size_t b) override {
+    ++seq_calls;
+    for (int j = 0; j < k; ++j)
+      if (proj_ids[j] != -1) ++bad_ids;
+    TernaryBackend::matmul_seq(proj_ids, wqs, k, produce, consume, N, M, b);
+  }
+};
+
+struct ThrowingBackend final : TernaryBackend {
+  void matmul(int, const std::int32_t*, std::int32_t*, const std::int8_t*, std::size_t, std::size_t) override {
+    throw std::runtime_error("backend failure");
+  }
+};
+
 int main(int argc, char** argv) {
   if (argc != 3) return 2;
   const std::string blob = argv[1], d = std::string(argv[2]) + "/";
@@ -76,6 +122,15 @@ int main(int argc, char** argv) {
   bitlinear(out.data(), x.data(), nw.data(), wq.data(), scale, rows, K, N, 1e-6f, nullptr, ActQuant::FixedQ510, 10,
             &cpu, -1);
   wr(d + "bl_fixed_cpube.f32", out);
+  {  // the i/f/g cluster over the seam: three scales, one weight matrix
+    const float* nws[3] = {nw.data(), nw.data(), nw.data()};
+    const std::int8_t* wqs[3] = {wq.data(), wq.data(), wq.data()};
+    const float scales[3] = {scale, 2.0f * scale, 0.5f * scale};
+    std::vector<float> cl(3 * rows * N);
+    float* outs[3] = {cl.data(), cl.data() + rows * N, cl.data() + 2 * rows * N};
+    bitlinear_cluster(outs, x.data(), nws, wqs, scales, 3, rows, K, N, 1e-6f, 10, &cpu, nullptr);
+    wr(d + "cluster_cpube.f32", cl);
+  }
   HipTernaryBackend hip(0);
   bitlinear(out.data(), x.data(), nw.data(), wq.data(), scale, rows, K, N, 1e-6f, nullptr, ActQuant::FixedQ510, 10,
             &hip, -1);
@@ -85,6 +140,14 @@ int main(int argc, char** argv) {
   hip.matmul_batch(-1, codes.data(), acc.data(), wq.data(), K, N, rows);
   wr(d + "hipbe_codes.i32", codes);
   wr(d + "hipbe_acc.i32", acc);
+  // one host buffer refilled with other weights between two proj_id -1 calls
+  std::vector<std::int8_t> wbuf = wq;
+  hip.matmul_batch(-1, codes.data(), acc.data(), wbuf.data(), K, N, rows);
+  wr(d + "hipbe_reuse_acc1.i32", acc);
+  for (std::size_t i = 0; i < wbuf.size(); ++i) wbuf[i] = static_cast<std::int8_t>((i * 7 + 3) % 3) - 1;
+  hip.matmul_batch(-1, codes.data(), acc.data(), wbuf.data(), K, N, rows);
+  wr(d + "hipbe_reuse_w2.i8", wbuf);
+  wr(d + "hipbe_reuse_acc2.i32", acc);
   std::vector<float> y(rows * K);
   rmsnorm(y.data(), x.data(), nw.data(), rows, K, 1e-6f);
   wr(d + "rmsnorm.f32", y);
@@ -131,6 +194,43 @@ int main(int argc, char** argv) {
     std::vector<std::int64_t> gcb;
     auto g = m.generate(prompts[0], 10, -1, Sampling{}, [&](std::int64_t t) { gcb.push_back(t); });
     wr_streams(d + "gen_" + tag + ".txt", {g, gcb});
+  }
+  // ---- Model::set_backend with backends that are not this engine's (FixedQ510) ----
+  {
+    Model m(w, ActQuant::FixedQ510);
+    CpuBackend cpub;
+    m.set_backend(&cpub, {});
+    wr_streams(d + "be_cpu_gen.txt", {m.generate(prompts[0], 10)});
+    wr_streams(d + "be_cpu_serve.txt", m.generate_serve(prompts, 6));
+    Sampling smp;
+    smp.temperature = 0.8f;
+    smp.top_k = 40;
+    smp.seed = 7;
+    wr_streams(d + "be_cpu_gen_sampled.txt", {m.generate(prompts[0], 12, -1, smp)});
+    std::vector<float> lg;
+    m.forward(prompts[0].data(), prompts[0].size(), lg);
+    wr(d + "be_cpu_forward.f32", lg);
+    // a backend that batches 3 rows, reports columns in two ranges out of order, and sees
+    // proj_ids from the tag map
+    ChunkedBackend chk;
+    std::unordered_map<std::string, int> ids{{"lm_head", 77}, {"model.layers.0.o_proj", 5}};
+    m.set_backend(&chk, ids);
+    wr_streams(d + "be_chunk_gen.txt", {m.generate(prompts[0], 10)});
+    std::printf("chunked backend: calls=%zu seq=%zu lm_head_ids=%zu bad_ids=%zu\n", chk.calls, chk.seq_calls,
+                chk.lm_calls, chk.bad_ids);
+    // back to the engine's own kernels
+    m.set_backend(nullptr, {});
+    wr_streams(d + "be_none_gen.txt", {m.generate(prompts[0], 10)});
+    // a backend whose matmul throws: the error reaches the caller
+    ThrowingBackend thr;
+    m.set_backend(&thr, {});
+    bool threw = false;
+    try {
+      m.generate(prompts[0], 4);
+    } catch (const std::runtime_error& e) {
+      threw = std::string(e.what()).find("backend failure") != std::string::npos;
+    }
+    std::printf("throwing backend: %s\n", threw ? "error propagated" : "NO ERROR");
   }
   std::printf("ok calls=%zu\n", cpu.calls);
   return 0;

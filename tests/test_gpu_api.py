@@ -192,7 +192,8 @@ def test_cpp_api(blobs, oracle, ref, tmp_path):
     (d / "prompts.txt").write_text("\n".join(" ".join(map(str, p)) for p in prompts) + "\n")
     blob = blobs("small")
     out = _run([API_CHECK, blob, str(d)], timeout=300)
-    assert out.startswith("ok")
+    lines = out.strip().splitlines()
+    assert lines[-1].startswith("ok"), out
 
     def f32(name, shape):
         return np.fromfile(d / name, np.float32).reshape(shape)
@@ -207,6 +208,17 @@ def test_cpp_api(blobs, oracle, ref, tmp_path):
     codes = np.fromfile(d / "hipbe_codes.i32", np.int32).reshape(rows, K)
     acc = np.fromfile(d / "hipbe_acc.i32", np.int32).reshape(rows, N)
     np.testing.assert_array_equal(acc, codes.astype(np.int64) @ wq.T.astype(np.int64))
+    # one host buffer refilled with other weights: the second call uses the new weights
+    w2 = np.fromfile(d / "hipbe_reuse_w2.i8", np.int8).reshape(N, K)
+    assert not np.array_equal(w2, wq)
+    np.testing.assert_array_equal(np.fromfile(d / "hipbe_reuse_acc1.i32", np.int32).reshape(rows, N),
+                                  codes.astype(np.int64) @ wq.T.astype(np.int64))
+    np.testing.assert_array_equal(np.fromfile(d / "hipbe_reuse_acc2.i32", np.int32).reshape(rows, N),
+                                  codes.astype(np.int64) @ w2.T.astype(np.int64))
+    cl = f32("cluster_cpube.f32", (3, rows, N))
+    for j, s in enumerate((scale, 2.0 * scale, 0.5 * scale)):
+        assert_bitexact(cl[j], oracle.bitlinear(x, nw, wq, float(np.float32(s)), 1e-6, FIXED)["out"],
+                        f"bitlinear_cluster through a CPU TernaryBackend, projection {j}")
     assert_bitexact(f32("rmsnorm.f32", (rows, K)), oracle.rmsnorm(x, nw, 1e-6), "rmsnorm")
     assert_bitexact(f32("swishgate.f32", (rows, K)), oracle.rmsnorm_swishgate(x, o2, nw, 1e-6), "swishgate")
     assert_bitexact(f32("swiglu.f32", (rows, K)), oracle.swiglu(x, o2), "swiglu")
@@ -235,3 +247,24 @@ def test_cpp_api(blobs, oracle, ref, tmp_path):
         np.testing.assert_array_equal(g, rm.generate(prompts[0], 10))
         np.testing.assert_array_equal(gcb, g[len(prompts[0]):])
         rm.close()
+
+    # Model::set_backend with backends that are not this engine's: every FixedQ510
+    # projection's integer matmul on the host backend, results equal to the reference Model
+    rm = ref.model(blob, FIXED)
+    want_gen = rm.generate(prompts[0], 10)
+    np.testing.assert_array_equal(_streams(d / "be_cpu_gen.txt")[0], want_gen)
+    for g, w in zip(_streams(d / "be_cpu_serve.txt"), rm.generate_serve(prompts, 6)):
+        np.testing.assert_array_equal(g, w)
+    np.testing.assert_array_equal(_streams(d / "be_cpu_gen_sampled.txt")[0],
+                                  rm.generate(prompts[0], 12, temperature=0.8, top_k=40, seed=7))
+    want_lg = rm.forward(prompts[0])
+    assert_bitexact(np.fromfile(d / "be_cpu_forward.f32", np.float32).reshape(want_lg.shape), want_lg,
+                    "forward logits through a CPU TernaryBackend")
+    rm.close()
+    np.testing.assert_array_equal(_streams(d / "be_chunk_gen.txt")[0], want_gen)
+    np.testing.assert_array_equal(_streams(d / "be_none_gen.txt")[0], want_gen)
+    chk = next(ln for ln in lines if ln.startswith("chunked backend:"))
+    counts = dict(kv.split("=") for kv in chk.split(":")[1].split())
+    assert int(counts["calls"]) > 0 and int(counts["seq"]) > 0 and int(counts["lm_head_ids"]) > 0, chk
+    assert counts["bad_ids"] == "0", chk
+    assert "throwing backend: error propagated" in lines, out
