@@ -1,12 +1,15 @@
 // mmfree/profile.hpp -- wall-clock op profiler (off by default).
-// Same interface as the reference's (cpp/include/mmfree/profile.hpp:20-73). Model wraps its
-// GPU calls in ScopedTimers (labels "prefill", "decode", "lm_head", "sample"); the per-kernel
-// breakdown comes from rocprofv3 or mmf_model_time_decode.
+// Same public interface as the reference's (cpp/include/mmfree/profile.hpp:20-73). Model
+// wraps its GPU calls in ScopedTimers (labels "generate", "prefill", "decode", "forward",
+// "sample"); the per-kernel breakdown comes from rocprofv3 or mmf_model_time_decode /
+// mmf_model_time_prefill.
 #pragma once
 
 #include <chrono>
+#include <cstddef>
 #include <cstdint>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace mmfree {
@@ -21,14 +24,17 @@ class Profiler {
   static Profiler& instance();
   void enable(bool on) { enabled_ = on; }
   bool enabled() const { return enabled_; }
-  void reset() { entries_.clear(); }
+  void reset();
   void add(const char* label, std::uint64_t ns);
+  // entries by total time, largest first (first-seen order among equal totals)
   std::vector<Entry> sorted() const;
-  std::uint64_t total_ns() const;
+  std::uint64_t total_ns() const { return total_; }
 
  private:
   bool enabled_ = false;
-  std::vector<Entry> entries_;
+  std::vector<Entry> entries_;                  // in first-seen order
+  std::unordered_map<std::string, std::size_t> slot_;  // label -> index into entries_
+  std::uint64_t total_ = 0;
 };
 
 class ScopedTimer {

@@ -159,6 +159,21 @@ typedef int (*mmf_matmul_fn)(void* user, int layer, int proj, int k, const int32
                              size_t K, size_t N, size_t rows);
 int mmf_model_set_matmul(mmf_ctx* ctx, mmf_matmul_fn fn, void* user);
 
+/* Device-time op profile of the model's kernels, for the Profiler / --profile breakdown
+ * (the reference times each op on the host: hgrn_model.cpp:88-189, bench.cpp:16-40).
+ * While on, every model launch is bracketed by events on the context's stream, the decode
+ * steps run launch by launch instead of from their captured graphs, and the timing entry
+ * points refuse to run. _read adds up the device time (microseconds) and launch count per
+ * op since the last read: MMF_PROF_NORM the row prologues (the model's RMSNorms and g_norm
+ * with each BitLinear's own norm and activation codes), MMF_PROF_MATMUL the BitLinear GEMMs
+ * and the fused single-row BitLinear kernels (norms, GEMV and epilogue), MMF_PROF_MIXER the
+ * gate math and recurrence of the row path, MMF_PROF_LM_HEAD the final norm and lm_head,
+ * MMF_PROF_EMBED the embedding gather. Measurement only. */
+enum { MMF_PROF_NORM = 0, MMF_PROF_MATMUL = 1, MMF_PROF_MIXER = 2, MMF_PROF_LM_HEAD = 3, MMF_PROF_EMBED = 4,
+       MMF_PROF_KINDS = 5 };
+int mmf_model_profile(mmf_ctx* ctx, int on);
+int mmf_model_profile_read(mmf_ctx* ctx, double* us, uint64_t* launches);
+
 /* Greedy Model::generate (model.hpp:44-50, hgrn_model.cpp:249-347), decode loop on the
  * device. Writes the id stream (prompt + generated) to out (capacity cap) and its length to
  * out_len. on_token (may be NULL) is called with each generated id, in order; eos_id < 0

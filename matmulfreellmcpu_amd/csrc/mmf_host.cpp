@@ -548,10 +548,14 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   pa.normw[0] = proj_of(c, m.lm).d.normw;
   pa.eps = m.cfg.rms_norm_eps;
   pa.qs = m.qs;
+  tbeg(c, kRkLM);
   MMF_HIP(launch_prologue(mode, pa, act, c->stream));
+  tend(c);
   GemmArgs ga = gemm_args(c, &m.lm, 1, rows, mode, m.frac);
   ga.out[0] = logits;
+  tbeg(c, kRkLM);
   proj_gemm(c, m, ga, act, c->stream, -1, 6);
+  tend(c);
 }
 
 int lm_grid(const Model& m) {
@@ -588,7 +592,9 @@ void lm_single(mmf_ctx* c, Model& m, const float* x, float* logits, bool want_ke
   a.pre_w = m.norm_wT;
   a.out = logits;
   if (!want_key) a.keys = nullptr;
+  tbeg(c, kRkLM);
   MMF_HIP(launch_decode(kLM, static_cast<Mode>(m.mode), a, c->stream));
+  tend(c);
 }
 
 // One kernel of the single-row decode step for stream 0. `full` = part of a real step:
@@ -650,7 +656,10 @@ void decode_one(mmf_ctx* c, Model& m, DecKind kind, size_t l, bool full = false)
       a.out = h;
       break;
   }
+  // each fused launch is one BitLinear group (with its norms and epilogue): timed as matmul
+  tbeg(c, kind == kIFG ? kRkGemmIFG : kind == kO ? kRkGemmO : kind == kGate ? kRkGemmGate : kRkGemmDown);
   MMF_HIP(launch_decode(kind, mode, a, c->stream));
+  tend(c);
 }
 
 void decode_launches(mmf_ctx* c, Model& m) {
@@ -691,6 +700,10 @@ hipGraphExec_t capture_graph(mmf_ctx* c, F&& f) {
 }
 
 void decode_step(mmf_ctx* c, Model& m) {
+  if (c->timer.on) {  // profiling: launch by launch, each between its own events
+    decode_launches(c, m);
+    return;
+  }
   if (graphs_enabled() && !m.graph_tried) {
     m.graph_tried = true;
     m.graph = capture_graph(c, [&] { decode_launches(c, m); });
@@ -831,7 +844,9 @@ void generate_rows(mmf_ctx* c, Model& m, const float* hlast, size_t new_tokens, 
     if (k > 0) {
       MMF_HIP(hipMemcpyAsync(d, &t, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
       float* h = s.h.as<float>(H);
+      tbeg(c, kRkOther);
       MMF_HIP(launch_embed(m.emb, d, h, 1, static_cast<int>(H), c->stream));
+      tend(c);
       for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
         layer_rows(c, m, static_cast<int>(l), 1, h, static_cast<float*>(m.state.p) + l * H, true, nullptr);
       t = head(h);
@@ -1522,14 +1537,16 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
     // embedding, all layers, final norm + lm_head, argmax: captured once per stream count
     // and replayed while no scratch buffer has moved (the first step runs them directly)
     auto work = [&] {
+      tbeg(c, kRkOther);
       MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
+      tend(c);
       for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
         layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H,
                    true, nullptr);
       lm_rows(c, m, static_cast<int>(B), h, lg);
       MMF_HIP(launch_argmax_rows(lg, static_cast<int>(B), static_cast<int>(V), am, c->stream));
     };
-    if (m.ext_on()) {  // the external matmul runs on the host: no graph
+    if (m.ext_on() || c->timer.on) {  // host matmul or per-launch profiling: no graph
       work();
     } else if (m.step_graph && m.step_B == B && m.step_epoch == dbuf_epoch.load()) {
       MMF_HIP(hipGraphLaunch(m.step_graph, c->stream));
@@ -1552,6 +1569,46 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
     if (logits) MMF_HIP(hipMemcpyAsync(logits, lg, B * V * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     if (argmax) MMF_HIP(hipMemcpyAsync(argmax, am, B * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream));
     MMF_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int mmf_model_profile(mmf_ctx* c, int on) {
+  return guard(c, [&] {
+    RowTimer& t = c->timer;
+    if (on && !t.on) {
+      t.used = 0;
+      t.kinds.clear();
+    }
+    t.on = on != 0;
+  });
+}
+
+int mmf_model_profile_read(mmf_ctx* c, double* us, uint64_t* launches) {
+  return guard(c, [&] {
+    RowTimer& t = c->timer;
+    double acc[MMF_PROF_KINDS] = {};
+    uint64_t n[MMF_PROF_KINDS] = {};
+    if (!t.kinds.empty()) {
+      MMF_HIP(hipStreamSynchronize(c->stream));
+      for (size_t i = 0; i < t.kinds.size(); ++i) {
+        float ms = 0.0f;
+        MMF_HIP(hipEventElapsedTime(&ms, t.pool[2 * i], t.pool[2 * i + 1]));
+        const int k = t.kinds[i];
+        const int op = k == kRkPrologue ? MMF_PROF_NORM
+                       : k == kRkMixer  ? MMF_PROF_MIXER
+                       : k == kRkLM     ? MMF_PROF_LM_HEAD
+                       : k == kRkOther  ? MMF_PROF_EMBED
+                                        : MMF_PROF_MATMUL;
+        acc[op] += 1000.0 * ms;
+        ++n[op];
+      }
+    }
+    t.used = 0;
+    t.kinds.clear();
+    for (int k = 0; k < MMF_PROF_KINDS; ++k) {
+      if (us) us[k] = acc[k];
+      if (launches) launches[k] = n[k];
+    }
   });
 }
 
@@ -1609,6 +1666,7 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
     Model& m = model_of(c);
     if (reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid reps");
     if (m.ext_on()) fail(MMF_ERR_STATE, "timing runs the built-in kernels: clear the external matmul first");
+    if (c->timer.on) fail(MMF_ERR_STATE, "timing while the op profile is on");
     if (m.streams != 1) reset_state(c, m, 1);
     if (m.hist_cap < static_cast<size_t>(warmup + reps) + 1) {
       m.hist.as<int64_t>(warmup + reps + 1);
@@ -1684,6 +1742,7 @@ int mmf_time_bitlinear(mmf_ctx* c, int id, int mode, int frac, float eps, const 
                        int warmup, int reps, double* total_us, double* prologue_us, double* gemm_us) {
   return guard(c, [&] {
     if (reps < 1 || warmup < 0 || rows == 0) fail(MMF_ERR_ARG, "invalid reps/rows");
+    if (c->timer.on) fail(MMF_ERR_STATE, "timing while the op profile is on");
     auto f = [&] { bitlinear_impl(c, &id, 1, mode, frac, eps, x, &out, rows, nullptr); };
     const double t = time_graph_runs(c, warmup, reps, f);
     if (total_us) *total_us = t;
@@ -1712,6 +1771,7 @@ int mmf_model_time_prefill(mmf_ctx* c, const int64_t* ids, size_t T, int warmup,
     Model& m = model_of(c);
     if (!ids || T == 0 || reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid prompt/reps");
     if (m.ext_on()) fail(MMF_ERR_STATE, "timing runs the built-in kernels: clear the external matmul first");
+    if (c->timer.on) fail(MMF_ERR_STATE, "timing while the op profile is on");
     if (m.streams != 1) reset_state(c, m, 1);
     const int H = static_cast<int>(m.cfg.hidden_size);
     auto f = [&] {
@@ -1719,8 +1779,8 @@ int mmf_model_time_prefill(mmf_ctx* c, const int64_t* ids, size_t T, int warmup,
       tbeg(c, kRkLM);
       MMF_HIP(launch_to_chain(h + (T - 1) * static_cast<size_t>(H), static_cast<float*>(m.h.p), 1, H, m.gH.Lc,
                               c->stream));
-      lm_single(c, m, static_cast<float*>(m.h.p), nullptr, true);
       tend(c);
+      lm_single(c, m, static_cast<float*>(m.h.p), nullptr, true);  // timed as kRkLM inside
     };
     const double t = time_runs(c, warmup, reps, f);
     if (total_us) *total_us = t;

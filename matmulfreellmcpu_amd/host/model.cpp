@@ -76,6 +76,32 @@ std::int64_t pick(const float* lg, std::size_t V, const Sampling& s, std::mt1993
 
 void trampoline(void* user, std::int64_t id) { (*static_cast<const std::function<void(std::int64_t)>*>(user))(id); }
 
+// While the Profiler is on, one model call's device time per op goes into it: the engine
+// brackets each launch with events (mmf_model_profile) and the totals are added under
+// these labels when the call ends, one Profiler call per launch.
+class DeviceOps {
+ public:
+  explicit DeviceOps(mmf_ctx* c) : c_(Profiler::instance().enabled() ? c : nullptr) {
+    if (c_ && mmf_model_profile(c_, 1) != MMF_OK) c_ = nullptr;
+  }
+  ~DeviceOps() {
+    if (!c_) return;
+    static const char* const kLabel[MMF_PROF_KINDS] = {"norm+quant", "matmul", "gate+scan", "lm_head", "embed"};
+    double us[MMF_PROF_KINDS];
+    std::uint64_t n[MMF_PROF_KINDS];
+    if (mmf_model_profile_read(c_, us, n) == MMF_OK)
+      for (int k = 0; k < MMF_PROF_KINDS; ++k)
+        for (std::uint64_t i = 0; i < n[k]; ++i)
+          Profiler::instance().add(kLabel[k], static_cast<std::uint64_t>(1000.0 * us[k] / n[k]));
+    mmf_model_profile(c_, 0);
+  }
+  DeviceOps(const DeviceOps&) = delete;
+  DeviceOps& operator=(const DeviceOps&) = delete;
+
+ private:
+  mmf_ctx* c_;
+};
+
 }  // namespace
 
 Model::Model(const Weights& w, ActQuant aq, int frac_bits)
@@ -191,7 +217,7 @@ void Model::check_call(int rc, const char* what) {
 }
 
 void Model::forward(const std::int64_t* ids, std::size_t T, std::vector<float>& logits) {
-  MMFREE_PROFILE("forward");
+  DeviceOps ops(ctx_);
   logits.assign(T * cfg_.vocab_size, 0.0f);
   check_call(mmf_model_forward(ctx_, ids, T, logits.data()), "mmf_model_forward");
 }
@@ -202,7 +228,7 @@ std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, 
   if (ids.empty()) throw std::runtime_error("mmfree: generate needs at least one prompt token");
   streams_ = 1;
   if (samp.temperature <= 0.0f) {  // greedy: the decode loop stays on the device
-    MMFREE_PROFILE("generate");
+    DeviceOps ops(ctx_);
     std::vector<std::int64_t> out(ids.size() + new_tokens);
     std::size_t len = 0;
     check_call(mmf_model_generate(ctx_, ids.data(), ids.size(), new_tokens, eos_id, out.data(), out.size(), &len,
@@ -212,20 +238,17 @@ std::vector<std::int64_t> Model::generate(const std::vector<std::int64_t>& ids, 
     out.resize(len);
     return out;
   }
+  DeviceOps ops(ctx_);
   const std::size_t V = cfg_.vocab_size;
   std::vector<std::int64_t> stream = ids;
   std::vector<float> lg(V);
   std::vector<std::size_t> cand;
   std::mt19937_64 rng(samp.seed);
   check_call(mmf_model_reset(ctx_, 1), "mmf_model_reset");
-  {
-    MMFREE_PROFILE("prefill");
-    check_call(mmf_model_prefill(ctx_, 0, ids.data(), ids.size(), lg.data(), nullptr), "mmf_model_prefill");
-  }
+  check_call(mmf_model_prefill(ctx_, 0, ids.data(), ids.size(), lg.data(), nullptr), "mmf_model_prefill");
   if (new_tokens == 0) return stream;
   for (std::size_t step = 0; step < new_tokens; ++step) {
     if (step > 0) {
-      MMFREE_PROFILE("decode");
       const std::int64_t t = stream.back();
       check_call(mmf_model_step(ctx_, &t, lg.data(), nullptr), "mmf_model_step");
     }
@@ -257,13 +280,13 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
   std::vector<char> done(B, 0);
   std::vector<float> lg(greedy ? 0 : B * V);
   std::vector<std::int64_t> am(B);
+  DeviceOps ops(ctx_);
   check_call(mmf_model_reset(ctx_, B), "mmf_model_reset");
   streams_ = B;
   // all prompts prefilled together (the same states and first tokens as the reference's
   // stream-by-stream prefill), then the first-token callbacks in stream order, each stream
   // sampling from its own generator (model.hpp:60-66, hgrn_model.cpp:412-428)
   {
-    MMFREE_PROFILE("prefill");
     std::vector<std::int64_t> cat;
     std::vector<std::size_t> lens(B);
     for (std::size_t b = 0; b < B; ++b) {
@@ -283,10 +306,7 @@ std::vector<std::vector<std::int64_t>> Model::generate_serve(
   std::vector<std::int64_t> tok(B);
   for (std::size_t step = 1; step < new_tokens; ++step) {
     for (std::size_t b = 0; b < B; ++b) tok[b] = streams[b].back();
-    {
-      MMFREE_PROFILE("decode");
-      check_call(mmf_model_step(ctx_, tok.data(), greedy ? nullptr : lg.data(), am.data()), "mmf_model_step");
-    }
+    check_call(mmf_model_step(ctx_, tok.data(), greedy ? nullptr : lg.data(), am.data()), "mmf_model_step");
     bool all_done = true;
     for (std::size_t b = 0; b < B; ++b) {
       if (done[b]) continue;

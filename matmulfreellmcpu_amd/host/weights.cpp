@@ -222,18 +222,23 @@ Weights::Weights(const std::string& path) {
       if (dt->str == "f32") esize = 4;
       else if (dt->str == "i8") { esize = 1; ref.is_int8 = true; }
       else throw std::runtime_error("weights: tensor " + kv.first + " has dtype " + dt->str);
+      // every product and sum below is checked: a crafted header must not wrap a size to a
+      // small number that passes the bounds check
+      const std::runtime_error too_big("weights: tensor " + kv.first + " does not fit the file");
       std::size_t numel = 1;
       for (const auto& d : sh->items) {
         ref.shape.push_back(as_size(d, kv.first + ".shape"));
-        numel *= ref.shape.back();
+        if (__builtin_mul_overflow(numel, ref.shape.back(), &numel)) throw too_big;
       }
-      const std::size_t nbytes = (ref.shape.empty() ? 0 : numel) * esize;
+      std::size_t nbytes = 0, start = 0, end = 0;
+      if (__builtin_mul_overflow(ref.shape.empty() ? 0 : numel, esize, &nbytes)) throw too_big;
       const std::size_t off = as_size(*of, kv.first + ".offset");
       if (const JVal* nb = m.at("nbytes"))
         if (as_size(*nb, kv.first + ".nbytes") != nbytes)
           throw std::runtime_error("weights: " + kv.first + " nbytes disagrees with its shape");
-      if (data_start + off < data_start || data_start + off + nbytes > size_)
-        throw std::runtime_error("weights: tensor " + kv.first + " does not fit the file");
+      if (__builtin_add_overflow(data_start, off, &start) || __builtin_add_overflow(start, nbytes, &end) ||
+          end > size_)
+        throw too_big;
       ref.data = bytes + data_start + off;
       if (tensors_.count(kv.first)) throw std::runtime_error("weights: duplicate tensor " + kv.first);
       tensors_.emplace(kv.first, std::move(ref));

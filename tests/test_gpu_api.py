@@ -161,7 +161,14 @@ def test_cli_bench_runs(blobs):
     _need(CLI)
     out = _run([CLI, "--blob", blobs("small"), "--ids", "5,6,7", "--gen", "8", "--bench", "--reps", "2",
                 "--mode", "float"])
-    assert "decode" in out
+    assert "decode" in out and "  threads:       1\n" in out
+    # --profile: the device time of the engine's kernels per op, in the reference's table
+    for extra in (["--bench", "--reps", "2"], []):
+        out = _run([CLI, "--blob", blobs("small"), "--ids", "5,6,7", "--gen", "8", "--mode", "fixed", "--profile"]
+                   + extra)
+        assert "op profile (" in out and "matmul (incl lm_head):" in out, out
+        ops = {ln.split()[0] for ln in out.splitlines() if ln.startswith("  ") and len(ln.split()) == 5}
+        assert {"matmul", "lm_head", "norm+quant", "embed"} <= ops, out
 
 
 # ---- 3. the C++ API ------------------------------------------------------------------------

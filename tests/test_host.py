@@ -7,6 +7,7 @@ import json
 import os
 import re
 import struct
+import subprocess
 
 import numpy as np
 import pytest
@@ -78,6 +79,25 @@ def test_blob_reader_validates(tmp_path):
     _write_blob(bad, wrongdt, 64)
     with pytest.raises(ValueError, match="dtype"):
         read_blob(bad)
+
+
+def test_cxx_weights_reject_overflowing_shapes(tmp_path):
+    """The C++ Weights loader (through mmfree-cli, which opens the blob before any device
+    work) refuses shapes whose byte size wraps around 64 bits, and offsets past the end."""
+    cli = os.path.join(ROOT, "matmulfreellmcpu_amd", "_lib", "mmfree-cli")
+    if not os.path.exists(cli):
+        pytest.skip("mmfree-cli not built")
+    cases = {
+        "wrap": {"dtype": "f32", "shape": [2 ** 33, 2 ** 31], "offset": 0, "nbytes": 0},
+        "wrap3": {"dtype": "i8", "shape": [2 ** 32, 2 ** 16, 2 ** 16], "offset": 0},
+        "offset": {"dtype": "f32", "shape": [2], "offset": 2 ** 52, "nbytes": 8},
+    }
+    for name, entry in cases.items():
+        p = str(tmp_path / f"{name}.mmfree")
+        _write_blob(p, {"config": {"vocab_size": 4, "hidden_size": 8}, "tensors": {"a": entry}}, 64)
+        r = subprocess.run([cli, "--blob", p, "--ids", "1,2", "--gen", "1"], capture_output=True, text=True,
+                           timeout=60)
+        assert r.returncode == 1 and "does not fit the file" in r.stderr, (name, r.returncode, r.stderr)
 
 
 def test_generator_is_deterministic_and_follows_the_recipe(tmp_path):
