@@ -17,29 +17,10 @@
 //    words per matrix, the epilogue operands, the prologue inputs -- is issued at entry;
 //  * every block recomputes the (order-exact) row norms of its input vector, so no
 //    grid-wide synchronisation is needed inside a launch.
-// A block is 16 outputs x 8 chains; thread (ol, j) sums chain j of output og*16+ol, which
-// is the reference's AVX2 lane j.
+// Thread (ol, j) of a matrix's 128 threads sums chain j of output og*16+ol, which is the
+// reference's AVX2 lane j (16 outputs x 8 chains per output group).
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
-
-// MMF_PHASE_TRACE (off by default): thread 0 of block 0 records wall_clock64() at the phase
-// boundaries of the decode kernel into mmf_phase_trace[kind][0..7]; thread 0 of the last
-// block records its entry and exit in [kind][8], [kind][9]. Read with mmf_debug_phase_trace.
-#ifdef MMF_PHASE_TRACE
-__device__ unsigned long long mmf_phase_trace[5][10];
-#define MMF_MARK(k, i)                                                                  \
-  do {                                                                                  \
-    if (blockIdx.x == 0 && threadIdx.x == 0) mmf_phase_trace[k][i] = wall_clock64();    \
-  } while (0)
-#define MMF_SPAN(k, first)                                                              \
-  do {                                                                                  \
-    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)                                \
-      mmf_phase_trace[k][(first) ? 8 : 9] = wall_clock64();                             \
-  } while (0)
-#else
-#define MMF_MARK(k, i) do {} while (0)
-#define MMF_SPAN(k, first) do {} while (0)
-#endif
 
 namespace mmf {
 
@@ -55,16 +36,27 @@ template <> struct KindTraits<kLM> { static constexpr int NM = 1, NA = 1, NP = 3
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int MODE, int KIND, int NV>
-__global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArgs a) {
+// A block is KS parts of NM * 128 threads. In every part, thread (mi, ol, j) sums chain j of
+// output ol of the block's group for matrix mi. What the parts do:
+//   kLM             part p takes the block's p-th output group (the groups a block strides
+//                   over run side by side);
+//   integer modes   part p sums words [p Wc / KS, (p + 1) Wc / KS) of every chain; the int32
+//                   partials meet in LDS (integer sums do not depend on their order);
+//   float           only part 0 runs the GEMV (a chain is one reference lane, in order); the
+//                   other parts share the loads, the normalisation and the encoding.
+template <int MODE, int KIND, int NV, int KS>
+__global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(DecArgs a) {
   constexpr int NM = KindTraits<KIND>::NM, NA = KindTraits<KIND>::NA, NP = KindTraits<KIND>::NP;
-  constexpr int BS = kBlock * NM;
+  constexpr int BM = kBlock * NM;  // threads of one part
+  constexpr int BS = BM * KS;
+  constexpr bool LMG = (KIND == kLM);                         // parts = output groups
+  constexpr bool KSPLIT = (MODE != kFloat) && !LMG && KS > 1;  // parts = word ranges
   extern __shared__ float smem[];
   // ---- kernel arguments ---------------------------------------------------------------------
   // Every field the launch uses is read here and pinned in scalar registers: the scalar loads
   // then issue back to back at entry and cost one round trip, instead of one dependent round
   // trip each where a field is first used (the compiler otherwise sinks them to their uses).
-  const int mis = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 7);  // wave's matrix
+  const int mis = __builtin_amdgcn_readfirstlane((static_cast<int>(threadIdx.x) >> 6) % (2 * NM) >> 1);  // wave's matrix
   const ProjDev& Pa = a.p[KIND == kIFG ? mis : 0];
   const Geom& g0 = a.p[0].g;
   const int gN = g0.N, gK = g0.K, Lc = g0.Lc, nt = g0.ntail, Wc = g0.Wc, gng = g0.ngroups;
@@ -114,30 +106,30 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   // different banks: float rows LS floats apart, int8 plane rows LQ bytes apart.
   const int L32 = (Lc + 31) / 32 * 32;  // rows zero-filled to whole 32-value chain batches
   const int LS = L32 + 4, WL = 8 * LS + 8, LQ = Lc + 16;
-  const int tid = threadIdx.x, mi = tid >> 7, lt = tid & 127, ol = lt >> 3, j = lt & 7;
+  const int tid = threadIdx.x, part = tid / BM, mi = (tid % BM) >> 7, lt = tid & 127, ol = lt >> 3, j = lt & 7;
   const int ai = (NA > 1) ? mi : 0;  // this thread's activation vector
   const int nout = (KIND == kGate) ? gN / 2 : gN;
   const int ngroups_out = (nout + kGroup - 1) / kGroup;
 
   float* X = smem;           // [WL] input row
   float* S = X + WL;         // [WL] kO: silu(recur)
-  float* red = S + WL;       // [16]
-  float* vals = red + 16;    // [NM][16] per-matrix results of the block's outputs
-  float* Y = vals + 48;      // float: NA x [WL]; int: NA x 2 planes x [8 LQ] bytes + tails + scales
+  float* red = S + WL;       // [32] chain partials, per-wave maxima and argmax keys
+  float* vals = red + 32;    // [KS][NM][16] per-part, per-matrix results of the block's outputs
+  float* Y = vals + 48 * KS; // float: NA x [WL]; int: NA x 2 planes x [8 LQ] bytes + tails + scales
   int8_t* Q = reinterpret_cast<int8_t*>(Y);
   int32_t* CT = reinterpret_cast<int32_t*>(Q + NA * 16 * LQ);
   float* SA = reinterpret_cast<float*>(CT + NA * 8);
   // [NM][G][Wc][128] all weight words of the block's G output groups, slab row layout
-  uint32_t* WX = (MODE == kFloat) ? reinterpret_cast<uint32_t*>(Y + NA * WL) : reinterpret_cast<uint32_t*>(SA + NA);
+  // (16-byte aligned: the weight copies write 16 bytes per lane)
+  uint32_t* WX = (MODE == kFloat) ? reinterpret_cast<uint32_t*>(Y + NA * WL)
+                                  : reinterpret_cast<uint32_t*>(SA + ((NA + 3) & ~3));
   const int G = awg;
 
   // ---- entry: issue every load that does not depend on the prologue --------------------
-  MMF_MARK(KIND, 0);
-  MMF_SPAN(KIND, true);
-  int og = blockIdx.x;
-  const int o0 = og * kGroup + ol;
   const int mrow = (KIND == kGate && mi == 1) ? gng / 2 : 0;  // gate: the up half
-  const bool epi = (mi == 0 && j == 0 && og < ngroups_out && o0 < nout);
+  // epilogue owners of the single-group kinds: part 0, matrix 0, lane j == 0
+  const int o0 = static_cast<int>(blockIdx.x) * kGroup + ol;
+  const bool epi = !LMG && part == 0 && mi == 0 && j == 0 && o0 < nout;
   const int po = epi ? ((o0 < aoK8) ? (o0 & 7) * aoLc + (o0 >> 3) : 8 * aoLc + (o0 - aoK8)) : 0;
   float e_lb = 0.0f, e_st = 0.0f, e_hin = 0.0f;
   if (epi) {
@@ -194,14 +186,19 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
       v[s][i] = (e < W4) ? reinterpret_cast<const float4*>(src[s])[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   // the weight words of the block's output groups (after the input, which the norms need
-  // first): straight into LDS, one dword per lane, in the slab row order
-  for (int gi = 0; gi < G; ++gi) {
-    const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
-    if (og_i >= ngroups_out) break;
-    const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * Wc * 128 + lt;
-    uint32_t* dx = WX + (mi * G + gi) * Wc * 128 + (lt & 64);  // this wave's 64 dwords of a row
-    for (int m = 0; m < Wc; ++m)
-      __builtin_amdgcn_global_load_lds(sx + m * 128, (lds_void*)(dx + m * 128), 4, 0, 0);
+  // first): straight into LDS in the slab order, 16 bytes per lane, so one instruction of a
+  // wave moves 1 KB (two slab rows); the 2 KS waves of a matrix take every 2 KS-th KB. A slab
+  // of an odd number of rows ends in half a KB, which lanes 32..63 skip.
+  {
+    const int nwords = Wc * 128, wv = part * 2 + (lt >> 6), lane = lt & 63;
+    for (int gi = 0; gi < G; ++gi) {
+      const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
+      if (og_i >= ngroups_out) break;
+      const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * nwords;
+      uint32_t* dx = WX + (mi * G + gi) * nwords;
+      for (int c = wv * 256; c < nwords; c += 512 * KS)
+        if (c + 4 * lane < nwords) __builtin_amdgcn_global_load_lds(sx + c + 4 * lane, (lds_void*)(dx + c), 16, 0, 0);
+    }
   }
   // LDS float4 index of each of this thread's global float4s
   int li[NV];
@@ -224,7 +221,6 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     X[jj * LS + Lc + (z - jj * (L32 - Lc))] = 0.0f;
   }
   __syncthreads();
-  MMF_MARK(KIND, 1);
 
   // ---- stage 1: the kernel's own pre-norm -------------------------------------------------
   if (KIND != kDown) {
@@ -249,11 +245,9 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     __syncthreads();
   }
   // ---- stage 2: BitLinear RMSNorm, activation encoding ------------------------------------
-  MMF_MARK(KIND, 2);
   chain_begin(X, Lc, LS, red);
   __syncthreads();
   const float r2 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
-  MMF_MARK(KIND, 3);
   constexpr int NW0 = NP - NA;  // first norm-weight source
 #pragma unroll
   for (int aa = 0; aa < NA; ++aa) {
@@ -328,31 +322,29 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
   if (G > 0) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS copies landed
   __syncthreads();
 
-  // ---- GEMV: each thread one chain of one matrix --------------------------------------------
-  MMF_MARK(KIND, 4);
-  unsigned long long best = 0ull;
-  for (int gi = 0; og < ngroups_out; og += gridDim.x, ++gi) {
-    float facc = 0.0f;
-    int32_t hacc = 0, lacc = 0;
-    // One word = 16 codes of chain j against 16 activations: act_of reads the activations
-    // from LDS, word_of runs the chain over them.
-    struct Act {
-      float4 f[MODE == kFloat ? 4 : 1];
-      uint4 h, l;
-    };
-    auto act_of = [&](int m) {
-      Act r;
-      if (MODE == kFloat) {
-        const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS + 16 * m);
+  // ---- GEMV: each thread one chain (or one chain's word range) of one matrix ----------------
+  // One word = 16 codes of chain j against 16 activations: act_of reads the activations from
+  // LDS, word_of runs the chain over them.
+  struct Act {
+    float4 f[MODE == kFloat ? 4 : 1];
+    uint4 h, l;
+  };
+  auto act_of = [&](int m) {
+    Act r;
+    if (MODE == kFloat) {
+      const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS + 16 * m);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) r.f[q] = yl[q];
-      } else {
-        const int8_t* ql = Q + ai * 16 * LQ + j * LQ + 16 * m;
-        r.h = *reinterpret_cast<const uint4*>(ql);
-        if (MODE == kFixed) r.l = *reinterpret_cast<const uint4*>(ql + 8 * LQ);
-      }
-      return r;
-    };
+      for (int q = 0; q < 4; ++q) r.f[q] = yl[q];
+    } else {
+      const int8_t* ql = Q + ai * 16 * LQ + j * LQ + 16 * m;
+      r.h = *reinterpret_cast<const uint4*>(ql);
+      if (MODE == kFixed) r.l = *reinterpret_cast<const uint4*>(ql + 8 * LQ);
+    }
+    return r;
+  };
+  // The chain sums of this thread over words [m0, m1) of group og (slot gi of the LDS copy):
+  // float in facc, integer planes in hacc / lacc.
+  auto gemv = [&](int og, int gi, int m0, int m1, float& facc, int32_t& hacc, int32_t& lacc) {
     auto word_of = [&](uint32_t w, const Act& x) {
       if (MODE == kFloat) {
         const float y[16] = {x.f[0].x, x.f[0].y, x.f[0].z, x.f[0].w, x.f[1].x, x.f[1].y, x.f[1].z, x.f[1].w,
@@ -367,8 +359,8 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
     };
     if (G > 0) {  // words in LDS: 4 at a time, all their reads issued before the chain
       const uint32_t* wl = WX + (mi * G + gi) * Wc * 128 + lt;
-      int m = 0;
-      for (; m + 4 <= Wc; m += 4) {
+      int m = m0;
+      for (; m + 4 <= m1; m += 4) {
         const uint32_t w0 = wl[m * 128], w1 = wl[(m + 1) * 128], w2 = wl[(m + 2) * 128], w3 = wl[(m + 3) * 128];
         const Act x0 = act_of(m), x1 = act_of(m + 1), x2 = act_of(m + 2), x3 = act_of(m + 3);
         word_of(w0, x0);
@@ -376,27 +368,27 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
         word_of(w2, x2);
         word_of(w3, x3);
       }
-      for (; m < Wc; ++m) word_of(wl[m * 128], act_of(m));
+      for (; m < m1; ++m) word_of(wl[m * 128], act_of(m));
     } else {  // LDS too small for the words: read them from global memory, 8 at a time
       const uint32_t* slab = pk + static_cast<size_t>(og + mrow) * Wc * 128 + lt;
       constexpr int U = 8;
-      for (int m0 = 0; m0 < Wc; m0 += U) {
+      for (int mb = m0; mb < m1; mb += U) {
         uint32_t w[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) w[u] = (m0 + u < Wc) ? slab[static_cast<size_t>(m0 + u) * 128] : 0u;
+        for (int u = 0; u < U; ++u) w[u] = (mb + u < m1) ? slab[static_cast<size_t>(mb + u) * 128] : 0u;
 #pragma unroll
         for (int u = 0; u < U; ++u)
-          if (m0 + u < Wc) word_of(w[u], act_of(m0 + u));
+          if (mb + u < m1) word_of(w[u], act_of(mb + u));
       }
     }
-
-    // reduce the 8 chains, add the tail, scale
-    MMF_MARK(KIND, 5);
-    const int o = og * kGroup + ol;
+  };
+  // The output value of output o of matrix mi (lane j == 0) from its chain sums: reduce the 8
+  // chains, add the tail, scale.
+  auto finish = [&](int o, float facc, int32_t sum) {
     const int oo = o + ((KIND == kGate && mi == 1) ? nout : 0);
     float val = 0.0f;
     if (MODE == kFloat) {
-      float s = hsum8_lanes(facc);
+      float s = facc;
       if (j == 0 && o < nout) {
         const float* yt = Y + ai * WL + 8 * LS;
         for (int t = 0; t < nt; ++t) {
@@ -406,30 +398,89 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
         }
       }
       val = s * pinv;
-    } else {
-      int32_t s = isum8_lanes(hacc);
-      if (MODE == kFixed) s = s * 256 + isum8_lanes(lacc);
-      if (j == 0 && o < nout) {
-        if (MODE == kFixed) s += 128 * prowsum[oo];
-        for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[oo * 8 + t]) * CT[ai * 8 + t];
-        val = (MODE == kFixed) ? static_cast<float>(s) * invfx
-                               : static_cast<float>(s) / (pscale * SA[ai]);
+    } else if (j == 0 && o < nout) {
+      int32_t s = sum;
+      if (MODE == kFixed) s += 128 * prowsum[oo];
+      for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[oo * 8 + t]) * CT[ai * 8 + t];
+      val = (MODE == kFixed) ? static_cast<float>(s) * invfx : static_cast<float>(s) / (pscale * SA[ai]);
+    }
+    return val;
+  };
+
+  if constexpr (LMG) {
+    // ---- lm_head: part p runs the block's groups p, p + KS, ... (slot gi); logits and keys
+    unsigned long long best = 0ull;
+    for (int gi = part, og = static_cast<int>(blockIdx.x) + part * static_cast<int>(gridDim.x); og < ngroups_out;
+         gi += KS, og += KS * static_cast<int>(gridDim.x)) {
+      float facc = 0.0f;
+      int32_t hacc = 0, lacc = 0;
+      gemv(og, gi, 0, Wc, facc, hacc, lacc);
+      const int o = og * kGroup + ol;
+      int32_t sum = 0;
+      if (MODE == kFloat) {
+        facc = hsum8_lanes(facc);
+      } else {
+        sum = isum8_lanes(hacc);
+        if (MODE == kFixed) sum = sum * 256 + isum8_lanes(lacc);
+      }
+      const float val = finish(o, facc, sum);
+      if (j != 0 || o >= nout) continue;
+      if (aout) aout[o] = val;
+      const unsigned long long kk = amax_key(val, o);
+      best = kk > best ? kk : best;
+    }
+    if (akeys) {  // one partial key per block, reduced by the consumer
+      for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long other = __shfl_xor(best, off);
+        best = other > best ? other : best;
+      }
+      unsigned long long* r64 = reinterpret_cast<unsigned long long*>(red);
+      if ((tid & 63) == 0) r64[tid >> 6] = best;
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long b = r64[0];
+        for (int w = 1; w < BS / 64; ++w) b = r64[w] > b ? r64[w] : b;
+        akeys[blockIdx.x] = b;
       }
     }
+    return;
+  } else {
+    // ---- one output group per block ----------------------------------------------------------
+    const int og = static_cast<int>(blockIdx.x);
+    float facc = 0.0f;
+    int32_t hacc = 0, lacc = 0;
+    if (KSPLIT) gemv(og, 0, part * Wc / KS, (part + 1) * Wc / KS, facc, hacc, lacc);
+    else if (part == 0) gemv(og, 0, 0, Wc, facc, hacc, lacc);
+    int32_t sum = 0;
+    if (MODE == kFloat) {
+      facc = hsum8_lanes(facc);
+    } else {
+      sum = isum8_lanes(hacc);
+      if (MODE == kFixed) sum = sum * 256 + isum8_lanes(lacc);
+      if (KSPLIT) {  // the parts' partial sums meet in LDS, added by part 0
+        int32_t* ps = reinterpret_cast<int32_t*>(vals);
+        if (j == 0) ps[(part * NM + mi) * 16 + ol] = sum;
+        __syncthreads();
+        if (part == 0) {
+          sum = ps[mi * 16 + ol];
+          for (int p = 1; p < KS; ++p) sum += ps[(p * NM + mi) * 16 + ol];
+        }
+        __syncthreads();  // vals is reused below
+      }
+    }
+    const int o = og * kGroup + ol;
+    const float val = (part == 0) ? finish(o, facc, sum) : 0.0f;
     float v1 = 0.0f, v2 = 0.0f;
     if (NM > 1) {  // gather the other matrices' results for the same outputs
-      if (j == 0) vals[mi * 16 + ol] = val;
+      if (part == 0 && j == 0) vals[mi * 16 + ol] = val;
       __syncthreads();
       v1 = vals[16 + ol];
       if (NM > 2) v2 = vals[32 + ol];
-      __syncthreads();
     }
-    if (mi != 0 || j != 0 || o >= nout) continue;
+    if (!epi) return;
 
     // ---- epilogues -------------------------------------------------------------------
-    const int p = (og == static_cast<int>(blockIdx.x))
-                      ? po
-                      : ((o < aoK8) ? (o & 7) * aoLc + (o >> 3) : 8 * aoLc + (o - aoK8));
+    const int p = po;
     if (KIND == kIFG) {
       const bool tl = o >= (aH & ~7);  // sigmoid / swiglu over T*H = H elements
       float f = sigmoid_of(v1, tl);
@@ -444,40 +495,43 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM) void k_decode(DecArg
       if (aout) aout[p] = src[0][p];  // layer 0: the embedding row becomes h
     } else if (KIND == kO || KIND == kDown) {
       aout[p] = e_hin + val;
-    } else if (KIND == kGate) {
+    } else {  // kGate
       aout[p] = swiglu_of(val, v1, o >= (nout & ~7));
-    } else {  // kLM
-      if (aout) aout[o] = val;
-      const unsigned long long kk = amax_key(val, o);
-      best = kk > best ? kk : best;
     }
   }
+}
 
-  MMF_MARK(KIND, 6);
-  if (KIND == kLM && akeys) {  // one partial key per block, reduced by the consumer
-    for (int off = 32; off > 0; off >>= 1) {
-      const unsigned long long other = __shfl_xor(best, off);
-      best = other > best ? other : best;
-    }
-    unsigned long long* r64 = reinterpret_cast<unsigned long long*>(red);
-    if ((tid & 63) == 0) r64[tid >> 6] = best;
-    __syncthreads();
-    if (tid == 0) akeys[blockIdx.x] = r64[0] > r64[1] ? r64[0] : r64[1];
-  }
-  MMF_MARK(KIND, 7);
-  MMF_SPAN(KIND, false);
+// Parts per block (see k_decode): integer modes split each chain's words over 2 (i/f/g,
+// gate/up) or 4 (o, down) parts; float keeps one part, except that the lm_head runs its groups
+// side by side in every mode.
+template <int MODE, int KIND>
+constexpr int kParts = (MODE == kFloat) ? 1 : ((KIND == kO || KIND == kDown) ? 4 : 2);
+
+template <int MODE, int KIND, int KS>
+hipError_t dec_ks(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
+  constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
+  const int W4 = (8 * a.p[0].g.Lc + 8) / 4;
+  if (W4 <= 2 * BS) k_decode<MODE, KIND, 2, KS><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 4 * BS) k_decode<MODE, KIND, 4, KS><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 8 * BS) k_decode<MODE, KIND, 8, KS><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 16 * BS) k_decode<MODE, KIND, 16, KS><<<grid, BS, lds, s>>>(a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 template <int MODE, int KIND>
 hipError_t dec_kind(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
-  constexpr int BS = kBlock * KindTraits<KIND>::NM;
-  const int W4 = (8 * a.p[0].g.Lc + 8) / 4;
-  if (W4 <= 2 * BS) k_decode<MODE, KIND, 2><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 4 * BS) k_decode<MODE, KIND, 4><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 8 * BS) k_decode<MODE, KIND, 8><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 16 * BS) k_decode<MODE, KIND, 16><<<grid, BS, lds, s>>>(a);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  if constexpr (KIND == kLM) {
+    switch (a.wgroups) {  // one part per group held in LDS, at most 4
+      case 0:
+      case 1: return dec_ks<MODE, KIND, 1>(a, lds, grid, s);
+      case 2: return dec_ks<MODE, KIND, 2>(a, lds, grid, s);
+      case 3: return dec_ks<MODE, KIND, 3>(a, lds, grid, s);
+      default: return dec_ks<MODE, KIND, 4>(a, lds, grid, s);
+    }
+  } else {
+    return dec_ks<MODE, KIND, kParts<MODE, KIND>>(a, lds, grid, s);
+  }
 }
 
 template <int MODE>
@@ -486,8 +540,9 @@ hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
   const int Lc = g.Lc;
   const int na = kind == kIFG ? 3 : 1;
   const size_t WL = 8 * static_cast<size_t>((Lc + 31) / 32 * 32 + 4) + 8, LQ = Lc + 16;
-  size_t lds = (2 * WL + 16 + 48) * sizeof(float);
-  lds += (MODE == kFloat) ? na * WL * sizeof(float) : na * (16 * LQ + 8 * sizeof(int32_t) + sizeof(float));
+  // X, S, red[32], vals[4 parts x 48]: sized for the most parts any kind takes
+  size_t lds = (2 * WL + 32 + 4 * 48) * sizeof(float);
+  lds += (MODE == kFloat) ? na * WL * sizeof(float) : na * (16 * LQ + 8 * sizeof(int32_t)) + 4 * sizeof(float);
   const int nout = (kind == kGate) ? g.N / 2 : g.N;
   int grid = (nout + kGroup - 1) / kGroup;
   if (kind == kLM) grid = lm_blocks(grid, g.K);
@@ -544,9 +599,3 @@ hipError_t launch_to_chain(const float* x, float* out, int rows, int K, int Lc, 
 }
 
 }  // namespace mmf
-
-#ifdef MMF_PHASE_TRACE
-extern "C" int mmf_debug_phase_trace(unsigned long long* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(mmf_phase_trace), sizeof(unsigned long long) * 50) == hipSuccess ? 0 : 2;
-}
-#endif
