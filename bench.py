@@ -13,7 +13,12 @@ launch duration, measured with an event pair around each launch; peak = 8 TB/s H
 
 cpu_baseline: the reference engine compiled from its own sources (oracle/_ref/mmfree-cli,
 built by oracle/Makefile) timed on this host's cores with its own --bench harness on the
-same blob and prompt; its greedy id stream is also compared with the GPU's.
+same blob and prompt, on one socket's physical cores (OMP_PROC_BIND=close, one place per
+core; `all_cpus`: every cpu this process may use); its greedy id stream is also compared
+with the GPU's. `cpu_baselines` holds the same reference beside the other workloads, on
+bounded samples that each entry names: the op sweep's integer matmul (CpuBackend), the
+1.3B prefill and decode (a 64-token prompt), and two lockstep serving steps per serving
+configuration.
 
 Beside the headline (all on seeded synthetic weights of the named shapes):
   op_sweep  BitLinear with int8-absmax activations: x ~N(0,1) [M, K], M in {1, 16, 256,
@@ -26,8 +31,11 @@ Beside the headline (all on seeded synthetic weights of the named shapes):
             norm, lm_head, argmax) per mode; per-GEMM microseconds and TOP/s (event pair
             around every launch); FixedQ510 runs two int8 passes (hi/lo code planes).
   serve     batched decode of independent streams (2.7B x 64 streams x 128-token prompts,
-            float and FixedQ510; 1.3B x 32 x 512, FixedQ510): prompts prefilled per stream,
-            then lockstep decode steps timed on the host around each step.
+            float and FixedQ510; 1.3B x 32 x 512, FixedQ510): prompts prefilled together,
+            then lockstep decode steps timed on the host around each step; weight bytes
+            per step against 8 TB/s.
+  decode_tok_s_fixed / kernels_fixed: the batch-1 decode in FixedQ510 (the reference CLI's
+            default mode) at the three shapes.
 """
 from __future__ import annotations
 
@@ -86,7 +94,8 @@ def measure(eng, preset, steps, warmup):
     for k in KINDS:
         us = kind_us[k]
         kernels[k] = {"us_per_launch": round(us, 3), "launches_per_token": nlaunch[k],
-                      "bytes_per_launch": int(nbytes[k]), "GBps": round(nbytes[k] / us / 1e3, 1)}
+                      "bytes_per_launch": int(nbytes[k]), "GBps": round(nbytes[k] / us / 1e3, 1),
+                      "frac": round(nbytes[k] / us / 1e3 / HBM_PEAK_GBS, 4)}
     tok_bytes = sum(nbytes[k] * nlaunch[k] for k in KINDS)
     return step_us, kernels, tok_bytes
 
@@ -214,31 +223,153 @@ def measure_serve(blob_dir, preset, B, T, mode_name, steps):
         cur = e.step(cur)
     dt = time.perf_counter() - t0
     e.close()
+    V, H, L, I = DIMS[preset]
+    wbytes = L * (4 * H * H + 3 * I * H) / 4 + V * H / 4  # packed ternary weights read per step
+    ops = 2.0 * B * (L * (4 * H * H + 3 * I * H) + V * H)
+    step_s = dt / steps
     r = {"streams": B, "prompt_tokens": T, "mode": mode_name, "steps_timed": steps,
-         "ms_per_step": round(dt / steps * 1e3, 3), "decode_tok_s": round(B * steps / dt, 1),
-         "prefill_s": round(t_pre, 3)}
+         "ms_per_step": round(step_s * 1e3, 3), "decode_tok_s": round(B * steps / dt, 1),
+         "prefill_s": round(t_pre, 3), "weight_GBps": round(wbytes / step_s / 1e9, 1),
+         "hbm_frac": round(wbytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+         "TOPS": round(ops / step_s / 1e12, 2)}
     log(f"[bench] serve {preset} B={B} T={T} {mode_name}: {r['ms_per_step']} ms/step, {r['decode_tok_s']} tok/s")
     return r
 
 
-def cpu_reference(blob, ids, gen, threads):
-    cli = os.path.join(ROOT, "oracle", "_ref", "mmfree-cli")
-    if not os.path.exists(cli):
-        return None, None
-    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="close", OMP_PLACES="cores")
-    idarg = ",".join(str(int(i)) for i in ids)
-    r = subprocess.run([cli, "--blob", blob, "--ids", idarg, "--gen", str(gen), "--mode", "float", "--print-ids"],
-                       capture_output=True, text=True, env=env, check=True)
-    ref_ids = np.array([int(t) for t in r.stdout.split()], np.int64)
+# ---- CPU baselines: the reference engine compiled from its own sources (oracle/_ref) -------
+
+REF_CLI = os.path.join(ROOT, "oracle", "_ref", "mmfree-cli")
+
+
+def cpu_sets():
+    """(cpus of one socket, one per physical core; every cpu this process may use): the
+    socket is the one holding most of the allowed cpus."""
+    cpus = sorted(os.sched_getaffinity(0))
+    sockets = {}
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            pkg = int(open(base + "physical_package_id").read())
+            core = int(open(base + "core_id").read())
+        except (OSError, ValueError):
+            pkg, core = 0, c
+        sockets.setdefault(pkg, {}).setdefault(core, c)
+    pkg = max(sockets, key=lambda p: len(sockets[p]))
+    return sorted(sockets[pkg].values()), cpus
+
+
+def omp_env(cpus):
+    """OpenMP settings for a CPU run on exactly `cpus`: one thread each, bound in order, threads
+    spinning between parallel regions (the reference's many short regions start faster)."""
+    places = ",".join("{%d}" % c for c in cpus)
+    return dict(os.environ, OMP_NUM_THREADS=str(len(cpus)), OMP_PROC_BIND="close", OMP_PLACES=places,
+                OMP_WAIT_POLICY="active")
+
+
+def ref_cli_bench(blob, ids, gen, mode, env, reps=3, warmup=1):
+    """The reference CLI's own --bench (bench.cpp:42-112): (avg prefill ms, avg decode tok/s, wall s)."""
     t = time.time()
-    r = subprocess.run([cli, "--blob", blob, "--ids", idarg, "--bench", "--gen", str(gen), "--warmup", "1",
-                        "--reps", "3", "--mode", "float"], capture_output=True, text=True, env=env, check=True)
+    r = subprocess.run([REF_CLI, "--blob", blob, "--ids", ",".join(str(int(i)) for i in ids), "--bench", "--gen",
+                        str(gen), "--warmup", str(warmup), "--reps", str(reps), "--mode", mode],
+                       capture_output=True, text=True, env=env, check=True, timeout=600)
     wall = time.time() - t
-    m = re.search(r"avg decode:\s+([0-9.]+) tok/s", r.stdout)
-    tps = float(m.group(1)) if m else None
-    return ref_ids, {"value": tps, "unit": "tok/s", "cores": threads, "kind": "reference",
-                     "sample": f"370M float, 16-token prompt, {gen} greedy tokens, reference --bench warmup 1 "
-                               f"reps 3 ({wall:.1f}s wall), OMP_NUM_THREADS={threads}"}
+    pre = re.search(r"avg prefill:\s+([0-9.]+) ms", r.stdout)
+    dec = re.search(r"avg decode:\s+([0-9.]+) tok/s", r.stdout)
+    return (float(pre.group(1)) if pre else None), (float(dec.group(1)) if dec else None), wall
+
+
+def cpu_leg(job):
+    """One CPU baseline job in this (child) process, whose OpenMP settings the parent set:
+    prints one JSON line. Jobs run the reference compiled from its sources."""
+    from oracle.oracle import FIXED, FLOAT, Ref
+    kind, arg = job.split(":", 1) if ":" in job else (job, "")
+    if kind == "op_sweep":  # CpuBackend::matmul_batch (ternary_backend.hpp:96-103) at every sweep shape
+        ref = Ref()
+        rng = np.random.default_rng(7)
+        out = []
+        for K, N in SWEEP_KN:
+            wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+            for M in SWEEP_M:
+                x = rng.integers(-128, 128, (M, K)).astype(np.int32)
+                ref.ternary_matmul(x[:1], wq)  # first touch of the weights
+                t = time.perf_counter()
+                ref.ternary_matmul(x, wq)
+                us = (time.perf_counter() - t) * 1e6
+                nbytes = N * K / 4 + 4 * M * K + 4 * M * N + 4 * K
+                out.append({"M": M, "K": K, "N": N, "us": round(us, 1), "GBps": round(nbytes / us / 1e3, 2),
+                            "TOPS": round(2.0 * M * N * K / us / 1e6, 3)})
+        print(json.dumps(out))
+    elif kind == "serve":  # Model::generate_serve (hgrn_model.cpp:349-454): time per lockstep step
+        blob, B, mode = arg.split(",")
+        B = int(B)
+        rm = Ref().model(blob, FIXED if mode == "fixed" else FLOAT)
+        prompts = [[3 + (7 * b) % 31000] for b in range(B)]  # one-token prompts: prefill = one row per stream
+        rm.generate_serve(prompts, 1)
+        t = time.perf_counter()
+        rm.generate_serve(prompts, 1)
+        t1 = time.perf_counter() - t
+        t = time.perf_counter()
+        rm.generate_serve(prompts, 3)
+        t3 = time.perf_counter() - t
+        rm.close()
+        step = max(t3 - t1, 1e-9) / 2
+        print(json.dumps({"ms_per_step": round(step * 1e3, 1), "tok_s": round(B / step, 1)}))
+    else:
+        raise SystemExit(f"unknown cpu job {job}")
+
+
+def run_cpu_leg(job, cpus, timeout=600):
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", job], capture_output=True, text=True,
+                       env=omp_env(cpus), check=True, timeout=timeout)
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def cpu_baselines(blob_dir, ids, gen):
+    """The reference engine on this host's cores beside every workload: one socket's
+    physical cores (OMP_PROC_BIND=close, one place per core), and for the headline also every
+    allowed cpu. Bounded samples; each dict says what was timed."""
+    if not os.path.exists(REF_CLI):
+        return None, None, {}
+    sock, allc = cpu_sets()
+    env_s, env_a = omp_env(sock), omp_env(allc)
+    res = {}
+    # config 0: the reference CLI's --bench on the 370M blob, float, as the GPU headline
+    blob0 = blob_path(blob_dir, "s0")
+    r = subprocess.run([REF_CLI, "--blob", blob0, "--ids", ",".join(str(int(i)) for i in ids), "--gen", str(gen),
+                        "--mode", "float", "--print-ids"], capture_output=True, text=True, env=env_s, check=True)
+    ref_ids = np.array([int(t) for t in r.stdout.split()], np.int64)
+    _, tps, wall = ref_cli_bench(blob0, ids, gen, "float", env_s)
+    _, tps_all, wall_all = ref_cli_bench(blob0, ids, gen, "float", env_a)
+    head = {"value": tps, "unit": "tok/s", "cores": len(sock), "kind": "reference",
+            "sample": f"370M float, 16-token prompt, {gen} greedy tokens: reference mmfree-cli --bench warmup 1 "
+                      f"reps 3 ({wall:.1f}s wall) on one socket's {len(sock)} physical cores, OMP_PROC_BIND=close, "
+                      "OMP_WAIT_POLICY=active",
+            "all_cpus": {"value": tps_all, "cores": len(allc), "wall_s": round(wall_all, 1)}}
+    log(f"[bench] cpu reference 370M float: {tps} tok/s on {len(sock)} cores, {tps_all} on {len(allc)} cpus")
+    # config 2: 1.3B prefill (64-token sample) + decode, float and fixed
+    blob2 = blob_path(blob_dir, "s2")
+    ids64 = np.random.default_rng(77).integers(3, 32000, 64)
+    c2 = {}
+    for mode in ("float", "fixed"):
+        pre_ms, dec, wall = ref_cli_bench(blob2, ids64, 16, mode, env_s, reps=1, warmup=0)
+        c2[mode] = {"prefill_tok_s": round(64 / pre_ms * 1e3, 2) if pre_ms else None, "decode_tok_s": dec,
+                    "wall_s": round(wall, 1)}
+    res["prefill_decode_1.3B"] = {"kind": "reference", "cores": len(sock), "modes": c2,
+                                  "sample": "1.3B, 64-token prompt (a sample of the 2048-token prefill), 16 "
+                                            "greedy tokens, reference mmfree-cli --bench warmup 0 reps 1"}
+    log(f"[bench] cpu reference 1.3B: {c2}")
+    # config 1: the op sweep's integer matmul through the reference's CpuBackend
+    res["op_sweep"] = {"kind": "reference", "cores": len(sock), "shapes": run_cpu_leg("op_sweep", sock),
+                       "sample": "CpuBackend::matmul_batch on int8-range codes at every (M, K, N), one call each"}
+    # configs 3 and 4: lockstep serving steps
+    for key, preset, B, mode in (("serve_2.7B_x64_float", "s3", 64, "float"), ("serve_2.7B_x64_fixed", "s3", 64, "fixed"),
+                                 ("serve_1.3B_x32_fixed", "s2", 32, "fixed")):
+        r = run_cpu_leg(f"serve:{blob_path(blob_dir, preset)},{B},{mode}", sock)
+        res[key] = dict(r, kind="reference", cores=len(sock),
+                        sample=f"Model::generate_serve, {B} one-token prompts, 2 lockstep steps timed (3 new tokens "
+                               "minus 1)")
+        log(f"[bench] cpu reference {key}: {r}")
+    return ref_ids, head, res
 
 
 def main():
@@ -253,7 +384,11 @@ def main():
                     help="comma list of decode,op_sweep,prefill,serve (decode is always run)")
     ap.add_argument("--vendor-int8", default=None, metavar="T,H,I",
                     help="only time the vendor int8 GEMM on one prefill layer's shapes (child process)")
+    ap.add_argument("--cpu-leg", default=None, help="run one CPU baseline job (child process)")
     args = ap.parse_args()
+    if args.cpu_leg:
+        cpu_leg(args.cpu_leg)
+        return
     if args.vendor_int8:
         T, H, I = (int(x) for x in args.vendor_int8.split(","))
         print(json.dumps(vendor_int8_gemm(T, H, I)))
@@ -263,7 +398,7 @@ def main():
               f"build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
     os.makedirs(args.blob_dir, exist_ok=True)
-    from matmulfreellmcpu_amd import FLOAT, Engine
+    from matmulfreellmcpu_amd import FIXED_Q510, FLOAT, Engine
 
     eng = Engine(0)
     devname, cus = eng.device_info()
@@ -276,26 +411,34 @@ def main():
     results = {}
     ids = np.random.default_rng(1234).integers(3, 32000, 16)
     gpu_ids = None
+    fixed = {}
     for name in shapes:
         preset = SHAPES[name]
         p = blob_path(args.blob_dir, preset)
-        t = time.time()
-        eng.close()
-        eng = Engine(0)
-        eng.load_blob(p, FLOAT)
-        log(f"[bench] {name}: loaded + repacked in {time.time() - t:.1f}s")
-        if name == "370M":
-            gpu_ids = eng.generate(ids, 128)
-            eng.generate(ids, 16)
-        steps = args.steps if name == "370M" else max(64, args.steps // 4)
-        eng.sync()
-        t0 = time.perf_counter()
-        step_us, kernels, tok_bytes = measure(eng, preset, steps, args.warmup)
-        eng.sync()
-        wall = time.perf_counter() - t0
-        results[name] = dict(step_us=step_us, kernels=kernels, tok_bytes=tok_bytes, steps=steps, wall=wall)
-        log(f"[bench] {name}: {1e6 / step_us:.1f} tok/s ({step_us:.1f} us/token), "
-            + ", ".join(f"{k} {v['us_per_launch']:.2f}us {v['GBps']:.0f}GB/s" for k, v in kernels.items()))
+        for mode in (FLOAT, FIXED_Q510):
+            t = time.time()
+            eng.close()
+            eng = Engine(0)
+            eng.load_blob(p, mode)
+            log(f"[bench] {name} mode {mode}: loaded + repacked in {time.time() - t:.1f}s")
+            if name == "370M" and mode == FLOAT:
+                gpu_ids = eng.generate(ids, 128)
+                eng.generate(ids, 16)
+            else:
+                eng.generate(ids, 8)
+            steps = args.steps if (name == "370M" and mode == FLOAT) else max(64, args.steps // 4)
+            eng.sync()
+            t0 = time.perf_counter()
+            step_us, kernels, tok_bytes = measure(eng, preset, steps, args.warmup)
+            eng.sync()
+            wall = time.perf_counter() - t0
+            r = dict(step_us=step_us, kernels=kernels, tok_bytes=tok_bytes, steps=steps, wall=wall)
+            if mode == FLOAT:
+                results[name] = r
+            else:
+                fixed[name] = r
+            log(f"[bench] {name} mode {mode}: {1e6 / step_us:.1f} tok/s ({step_us:.1f} us/token), "
+                + ", ".join(f"{k} {v['us_per_launch']:.2f}us {v['GBps']:.0f}GB/s" for k, v in kernels.items()))
     eng.close()
     sections = {x.strip() for x in args.sections.split(",")}
     extra = {}
@@ -328,9 +471,9 @@ def main():
 
     cpu = None
     parity = None
+    cpu_configs = {}
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-        ref_ids, cpu = cpu_reference(blob_path(args.blob_dir, "s0"), ids, 128, threads)
+        ref_ids, cpu, cpu_configs = cpu_baselines(args.blob_dir, ids, 128)
         if ref_ids is not None:
             parity = {"against": "reference mmfree-cli (oracle/_ref)", "tokens": 128,
                       "ids_identical": bool(np.array_equal(ref_ids, gpu_ids))}
@@ -355,6 +498,9 @@ def main():
         "decode_tok_s": {n: round(1e6 / r["step_us"], 1) for n, r in results.items()},
         "step_GBps": {n: round(r["tok_bytes"] / r["step_us"] / 1e3, 1) for n, r in results.items()},
         "kernels": {n: r["kernels"] for n, r in results.items()},
+        "decode_tok_s_fixed": {n: round(1e6 / r["step_us"], 1) for n, r in fixed.items()},
+        "kernels_fixed": {n: r["kernels"] for n, r in fixed.items()},
+        "cpu_baselines": cpu_configs,
         "parity": parity,
         "device": f"{devname}, {cus} CUs",
         "measured_ceilings": peaks,
