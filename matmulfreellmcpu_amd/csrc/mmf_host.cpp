@@ -212,9 +212,10 @@ int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float sc
   const size_t words = static_cast<size_t>(g.ngroups) * g.Wc * kGroup * 8;
   const size_t npad = static_cast<size_t>(g.ngroups) * kGroup;
   const size_t b_pk = words * 4, b_tail = npad * 8, b_rs = npad * 4, b_nw = normw_host ? K * 4 : 0;
+  const size_t b_nwT = normw_host ? (8 * static_cast<size_t>(g.Lc) + 8) * 4 : 0;  // chain-transposed copy
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t b_pkm = pkm_words(g) * 4;
-  MMF_HIP(hipMalloc(&P.mem, al(b_pk) + al(b_pkm) + al(b_tail) + al(b_rs) + al(b_nw) + 256));
+  MMF_HIP(hipMalloc(&P.mem, al(b_pk) + al(b_pkm) + al(b_tail) + al(b_rs) + al(b_nw) + al(b_nwT) + 256));
   char* base = static_cast<char*>(P.mem);
   P.d.pk = reinterpret_cast<uint32_t*>(base);
   P.d.pkm = reinterpret_cast<uint32_t*>(base + al(b_pk));
@@ -225,6 +226,9 @@ int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float sc
   if (normw_host) {
     MMF_HIP(hipMemcpy(nw, normw_host, b_nw, hipMemcpyHostToDevice));
     P.d.normw = nw;
+    float* nwT = reinterpret_cast<float*>(reinterpret_cast<char*>(nw) + al(b_nw));
+    MMF_HIP(launch_to_chain(nw, nwT, 1, static_cast<int>(K), g.Lc, c->stream));
+    P.d.normwT = nwT;
   } else {
     P.d.normw = normw_dev;
   }
@@ -407,7 +411,10 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.pre = kPreNorm;
     pa.pre_w = L.attn;
     pa.na = 3;
-    for (int k = 0; k < 3; ++k) pa.normw[k] = proj_of(c, L.proj[k]).d.normw;
+    for (int k = 0; k < 3; ++k) {
+      pa.normw[k] = proj_of(c, L.proj[k]).d.normw;
+      pa.normwT[k] = proj_of(c, L.proj[k]).d.normwT;
+    }
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
     tbeg(c, kRkPrologue);
@@ -454,6 +461,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.pre_w = L.gn;
     pa.na = 1;
     pa.normw[0] = proj_of(c, L.proj[3]).d.normw;
+    pa.normwT[0] = proj_of(c, L.proj[3]).d.normwT;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
     bool done = false;
@@ -497,6 +505,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.pre_w = L.mlp;
     pa.na = 1;
     pa.normw[0] = proj_of(c, L.proj[4]).d.normw;
+    pa.normwT[0] = proj_of(c, L.proj[4]).d.normwT;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
     tbeg(c, kRkPrologue);
@@ -519,6 +528,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.pre = kPreNone;
     pa.na = 1;
     pa.normw[0] = proj_of(c, L.proj[5]).d.normw;
+    pa.normwT[0] = proj_of(c, L.proj[5]).d.normwT;
     pa.eps = m.cfg.rms_norm_eps;
     pa.qs = m.qs;
     tbeg(c, kRkPrologue);
@@ -546,6 +556,7 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   pa.pre_w = m.norm_w;
   pa.na = 1;
   pa.normw[0] = proj_of(c, m.lm).d.normw;
+  pa.normwT[0] = proj_of(c, m.lm).d.normwT;
   pa.eps = m.cfg.rms_norm_eps;
   pa.qs = m.qs;
   tbeg(c, kRkLM);
@@ -1094,7 +1105,10 @@ static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac
   pa.x = x;
   pa.pre = kPreNone;
   pa.na = k;
-  for (int z = 0; z < k; ++z) pa.normw[z] = proj_of(c, ids[z]).d.normw;
+  for (int z = 0; z < k; ++z) {
+    pa.normw[z] = proj_of(c, ids[z]).d.normw;
+    pa.normwT[z] = proj_of(c, ids[z]).d.normwT;
+  }
   pa.eps = eps;
   pa.qs = static_cast<float>(1u << frac);
   tbeg(c, kRkPrologue);

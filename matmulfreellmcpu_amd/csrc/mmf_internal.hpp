@@ -153,6 +153,7 @@ struct PrologueArgs {
   const float* x2;     // kPreSwish: recurrence output rows [rows, K]; kPreMixSwish: i rows
   const float* pre_w;  // stage-1 norm weight
   const float* normw[3];
+  const float* normwT[3];  // the same, chain-transposed [8*Lc + 8] (null: the general kernel)
   int na;
   PreKind pre;
   float eps, qs;

@@ -5,6 +5,7 @@
 //
 // Numerics follow the reference engine exactly (see mmf_device.hpp): every fp32
 // reduction keeps the 8-lane order of the AVX2 code, every int32 sum is exact.
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 
@@ -228,212 +229,304 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
   }
 }
 
-// The same prologue for K % 4 == 0 with 16-byte aligned inputs: every global input of the
-// row (x, the gate input x2, the stage-1 weight, the NA BitLinear norm weights) is loaded
-// as float4 at entry -- one memory round trip -- and each thread then works on exactly the
-// elements it loaded. Arithmetic and order are those of k_prologue.
-// The 256-thread prologues of long row ranges fit 64 VGPRs (8 waves per SIMD: 8 rows resident
-// per CU, so 2048 rows run in one round) with 16-value chain batches; the recurrence and
-// the wide swish forms would spill there and keep the default.
-template <int PRE, int MAXV, int BT>
-constexpr bool prologue_eight_waves() {
-  return BT == 256 && PRE != kPreMixSwish && !(PRE == kPreSwish && MAXV > 3);
+// Byte packing of four codes (code 0 in byte 0) for the int8 planes: FixedQ510 hi = bits
+// 8..15 of each code, lo = bits 0..7 minus 128 (the top bit flipped); Int8 the low byte.
+// __builtin_amdgcn_perm(a, b, sel) is v_perm_b32: result byte i = byte sel[i] of the
+// eight bytes b[0..3], a[0..3] (selector 0x0c gives zero).
+__device__ __forceinline__ void pack_split4(const int32_t* c, uint32_t& hi, uint32_t& lo) {
+  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x04000501u);
+  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x04000501u);
+  hi = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+  lo = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+}
+__device__ __forceinline__ uint32_t pack_low4(const int32_t* c) {
+  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x0c0c0400u);
+  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x0c0c0400u);
+  return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
 }
 
-template <int MODE, int PRE, int NA, int MAXV, bool PW, int BT>
-__global__ __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(prologue_eight_waves<PRE, MAXV, BT>() ? 8 : 1)))
-void k_prologue4(PrologueArgs a, ActBuf act) {
+__device__ __forceinline__ float f4el(const float4& f, int c) {
+  return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w));
+}
+
+// Waves per SIMD of the row prologue: 8 (64 VGPRs; 8 rows resident per CU, so 2048 rows run
+// in one round; chains in batches of 16 values) where what a thread keeps -- the row inputs
+// and stage-1 weight through the first chain, two sets of norm weights (and the Int8
+// values, through the absmax) in the encoding -- fits without spilling, else the compiler's
+// choice.
+template <int MODE, int PRE, int NA, int MAXG, int BT>
+constexpr int rowpro_waves() {
+  constexpr int nx = PRE == kPreSwish ? 2 : (PRE == kPreMixSwish ? 5 : 1);
+  constexpr int entry = 8 * MAXG * (nx + (PRE != kPreNone ? 1 : 0));               // row inputs
+  constexpr int encode = 8 * MAXG * ((NA > 1 ? 2 : 1) + (MODE == kInt8 ? 1 : 0));  // weights, values
+  return (BT == 256 && entry <= 24 && encode <= 40) ? 8 : 1;
+}
+
+// The row prologue for K % 4 == 0 with 16-byte aligned inputs and the chain-transposed norm
+// weights normwT. One block per row; each thread owns
+//  - groups (the loads and the element-wise stage 1): group t < G = nb + (ntail > 0) is the
+//    eight elements 8t .. 8t+7, chain position t of every chain (two float4 loads), or for
+//    t = nb the ntail (= 4) tail elements. Its values go to the chain-transposed LDS row
+//    X[c * LS + t] (tail: X[8 * LS + c]) that the order-fixed norm chains read;
+//  - units (the BitLinear norm and the encoding): unit u < Lc is positions t0 .. t0+7 of
+//    chain j (u = j * Lc/8 + t0/8). Its eight normed values come from two LDS reads and two
+//    float4 reads of normwT and leave as one 8-byte store per int8 plane (positions
+//    t0 .. t0+7 are contiguous in the fragment layout) or as two float4 stores.
+// Every global input of a group, the stage-1 weight included, is loaded at entry (one
+// memory round trip); the BitLinear norm weights of the thread's units are loaded before the
+// second norm chain (projection 0) or while the previous projection is encoded, so their
+// latency hides behind work -- or, with PW (a few rows per launch: a launch is one row's
+// latency), at entry too. Arithmetic and order are those of k_prologue.
+template <int MODE, int PRE, int NA, int MAXG, bool PW, int BT>
+__global__ __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(rowpro_waves<MODE, PRE, NA, MAXG, BT>())))
+void k_rowpro(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
-  constexpr int CU = prologue_eight_waves<PRE, MAXV, BT>() ? 4 : 8;  // float4 per chain batch
+  constexpr int CU = rowpro_waves<MODE, PRE, NA, MAXG, BT>() == 8 ? 4 : 8;  // float4 per chain batch
   constexpr bool SW = PRE == kPreSwish || PRE == kPreMixSwish, MIX = PRE == kPreMixSwish;
-  constexpr int NV = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0) + NA;
-  constexpr int IX2 = 1, IPW = SW ? 2 : 1, INW = 1 + (SW ? 1 : 0) + (PRE != kPreNone ? 1 : 0);
+  constexpr int NX = SW ? 2 : 1;  // x, and x2 for the swish gate
+  constexpr bool PWG = PRE != kPreNone;  // the stage-1 weight is loaded at entry with the row
   const int row = xcd_row(blockIdx.x);
   if (row >= act.rows) return;
-  const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, K4 = K / 4;
+  const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, L8 = Lc / 8;
+  const int G = nb + (nt > 0 ? 1 : 0);
   const int LS = lds_stride(Lc);
+  const int tid = threadIdx.x;
   float* X = smem;
-  // second LDS row only for silu(x2) (g_norm); the normed values never go through LDS
-  float* S = SW ? X + 8 * LS + 8 : X;
+  float* S = SW ? X + 8 * LS + 8 : X;  // silu(x2), g_norm only
   float* red = S + 8 * LS + 8;
-  const float* src[NV];
-  src[0] = a.x + static_cast<size_t>(row) * K;
-  if (SW) src[IX2] = a.x2 + static_cast<size_t>(row) * K;
-  if (PRE != kPreNone) src[IPW] = a.pre_w;
-#pragma unroll
-  for (int i = 0; i < NA; ++i) src[INW + i] = a.normw[i];
-  // The row (and x2) in registers at entry. The norm weights, the same for every row and
-  // so L2-resident, are read in the pass that uses them (fewer registers per thread, more
-  // rows resident per CU) or, with PW (a few rows: the launch is one row's latency), loaded
-  // at entry with the row, so that no pass waits for a memory round trip of its own.
-  constexpr int NX = 1 + (SW ? 1 : 0);
-  constexpr int NWV = PW ? NV - NX : 1;
-  float4 v[NX][MAXV];
-  float4 wv[NWV][PW ? MAXV : 1];
-#pragma unroll
-  for (int j = 0; j < MAXV; ++j) {
-    const int k4 = threadIdx.x + j * blockDim.x;
-#pragma unroll
-    for (int vi = 0; vi < NX; ++vi)
-      v[vi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[vi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (PW) {
-#pragma unroll
-      for (int wi = 0; wi < NWV; ++wi)
-        wv[wi][j] = k4 < K4 ? reinterpret_cast<const float4*>(src[NX + wi])[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  // kPreMixSwish: the f projection and the state of the row, with the inputs
-  float4 fv[MIX ? MAXV : 1], sv[MIX ? MAXV : 1], lv[MIX ? MAXV : 1];
-  if constexpr (MIX) {
-    const float4* f4 = reinterpret_cast<const float4*>(a.mix_f + static_cast<size_t>(row) * K);
-    const float4* s4 = reinterpret_cast<const float4*>(a.mix_state + static_cast<size_t>(row) * K);
-    const float4* l4 = reinterpret_cast<const float4*>(a.mix_lb);
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const int k4 = threadIdx.x + j * blockDim.x;
-      fv[j] = k4 < K4 ? f4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      sv[j] = k4 < K4 ? s4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      lv[j] = (l4 && k4 < K4) ? l4[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  auto wt = [&](int vi, int k4, int j) {
-    if constexpr (PW) return wv[vi - NX][j];
-    else return reinterpret_cast<const float4*>(src[vi])[k4];
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // elements 8t .. 8t+7 of a K-long vector: two float4, or for the tail group one and zeros
+  // (the tail group's second load repeats its first, an address in bounds, and is replaced by
+  // zeros: a select of values, not of addresses)
+  auto ld8 = [&](const float* p, int t, float4* o) {
+    const float4* p4 = reinterpret_cast<const float4*>(p) + 2 * t;
+    const float4 h = p4[t < nb ? 1 : 0];
+    o[0] = p4[0];
+    o[1] = t < nb ? h : z4;
   };
-  auto el = [](const float4& f, int c) { return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w)); };
-  // x (and silu(x2)) into the padded chain-transposed LDS rows
+  const size_t rK = static_cast<size_t>(row) * K;
+
+  float4 v[NX][MAXG][2];
+  float4 pw[PWG ? MAXG : 1][2];
+  float4 fv[MIX ? MAXG : 1][2], sv[MIX ? MAXG : 1][2], lv[MIX ? MAXG : 1][2];
+  float4 nwv[PW ? NA : 1][PW ? MAXG : 1][2];
 #pragma unroll
-  for (int j = 0; j < MAXV; ++j) {
-    const int k4 = threadIdx.x + j * blockDim.x;
-    if (k4 >= K4) continue;
+  for (int g = 0; g < MAXG; ++g) {
+    const int t = tid + g * BT;
+    if (t < G) {
+#pragma unroll
+      for (int vi = 0; vi < NX; ++vi) ld8((vi ? a.x2 : a.x) + rK, t, v[vi][g]);
+      if constexpr (PWG) ld8(a.pre_w, t, pw[g]);
+      if constexpr (MIX) {
+        ld8(a.mix_f + rK, t, fv[g]);
+        ld8(a.mix_state + rK, t, sv[g]);
+        if (a.mix_lb) ld8(a.mix_lb, t, lv[g]);
+        else lv[g][0] = lv[g][1] = z4;
+      }
+    }
+    if constexpr (PW) {
+      const int u = tid + g * BT;
+      if (u < Lc) {
+        const int j = u / L8, t0 = 8 * (u - j * L8);
+#pragma unroll
+        for (int ai = 0; ai < NA; ++ai) {
+          const float4* wp = reinterpret_cast<const float4*>(a.normwT[ai] + j * Lc + t0);
+          nwv[ai][g][0] = wp[0];
+          nwv[ai][g][1] = wp[1];
+        }
+      }
+    }
+  }
+
+  // the groups into the chain-transposed LDS rows (and silu(x2) for the swish gate)
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g) {
+    const int t = tid + g * BT;
+    if (t >= G) continue;
+    float xs[8], x2s[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      xs[c] = f4el(v[0][g][c >> 2], c & 3);
+      x2s[c] = f4el(v[NX - 1][g][c >> 2], c & 3);
+    }
     if constexpr (MIX) {
       // the recurrence step of k_mixer (stream_state), element for element; the swiglu and
       // sigmoid tail rule counts over all rows x K elements
-      const size_t e0 = static_cast<size_t>(row) * K + 4 * k4;
+      const size_t e0 = rK + 8 * static_cast<size_t>(t);
       const size_t body = (static_cast<size_t>(act.rows) * K) & ~static_cast<size_t>(7);
-      const float4 lbv = lv[j];
-      float st[4];
+      float st[8];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < 8; ++c) {
         const bool tail = e0 + c >= body;
-        float f = sigmoid_of(el(fv[j], c), tail);
-        if (a.mix_lb) f = __builtin_fmaf(1.0f - el(lbv, c), f, el(lbv, c));
-        const float in = swiglu_of(el(v[IX2][j], c), 1.0f - f, tail);
-        st[c] = __builtin_fmaf(f, el(sv[j], c), in);
+        const float lb = f4el(lv[g][c >> 2], c & 3);
+        float f = sigmoid_of(f4el(fv[g][c >> 2], c & 3), tail);
+        if (a.mix_lb) f = __builtin_fmaf(1.0f - lb, f, lb);
+        const float in = swiglu_of(x2s[c], 1.0f - f, tail);
+        st[c] = __builtin_fmaf(f, f4el(sv[g][c >> 2], c & 3), in);
       }
-      reinterpret_cast<float4*>(a.mix_state + static_cast<size_t>(row) * K)[k4] = make_float4(st[0], st[1], st[2], st[3]);
+      float4* so = reinterpret_cast<float4*>(a.mix_state + rK) + 2 * t;
+      so[0] = make_float4(st[0], st[1], st[2], st[3]);
+      if (t < nb) so[1] = make_float4(st[4], st[5], st[6], st[7]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
-        X[p] = el(v[0][j], c);
-        S[p] = silu_of(st[c], k >= K8);
+      for (int c = 0; c < 8; ++c) x2s[c] = st[c];
+    }
+    if (t < nb) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        X[c * LS + t] = xs[c];
+        if (SW) S[c * LS + t] = silu_of(x2s[c], false);
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = 4 * k4 + c, p = act_pos(k, K8, LS);
-        X[p] = el(v[0][j], c);
-        if (SW) S[p] = silu_of(el(v[IX2][j], c), k >= K8);
+      for (int c = 0; c < 8; ++c) {
+        if (c < nt) {
+          X[8 * LS + c] = xs[c];
+          if (SW) S[8 * LS + c] = silu_of(x2s[c], true);
+        }
       }
     }
   }
   const int L32 = (Lc + 31) / 32 * 32;
   for (int jr = 0; jr < 8; ++jr)
-    for (int t = nb + threadIdx.x; t < L32; t += blockDim.x) X[jr * LS + t] = 0.0f;
-  for (int t = nt + threadIdx.x; t < 8; t += blockDim.x) X[8 * LS + t] = 0.0f;
+    for (int t = nb + tid; t < L32; t += BT) X[jr * LS + t] = 0.0f;
+  for (int t = nt + tid; t < 8; t += BT) X[8 * LS + t] = 0.0f;
   __syncthreads();
+
   if (PRE != kPreNone) {
     const float r1 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const int k4 = threadIdx.x + j * blockDim.x;
-      if (k4 >= K4) continue;
-      const float4 w = wt(IPW, k4, j);
+    for (int g = 0; g < MAXG; ++g) {
+      const int t = tid + g * BT;
+      if (t >= G) continue;
+      const float4* w = pw[g];
+      const int nc = t < nb ? 8 : nt;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int p = act_pos(4 * k4 + c, K8, LS);
-        float x = (X[p] * r1) * el(w, c);
-        if (SW) x = x * S[p];
-        X[p] = x;
+      for (int c = 0; c < 8; ++c) {
+        if (c < nc) {
+          const int p = t < nb ? c * LS + t : 8 * LS + c;
+          float x = (f4el(v[0][g][c >> 2], c & 3) * r1) * f4el(w[c >> 2], c & 3);
+          if (SW) x = x * S[p];
+          X[p] = x;
+        }
       }
     }
     __syncthreads();
   }
+  // the norm weights of the units: projection ai into set ai % 2 (not PW)
+  float4 wq[PW ? 1 : 2][PW ? 1 : MAXG][2];
+  auto load_w = [&](int ai, int set) {
+    if constexpr (!PW) {
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g) {
+        const int u = tid + g * BT;
+        if (u >= Lc) continue;
+        const int j = u / L8, t0 = 8 * (u - j * L8);
+        const float4* wp = reinterpret_cast<const float4*>(a.normwT[ai] + j * Lc + t0);
+        wq[set][g][0] = wp[0];
+        wq[set][g][1] = wp[1];
+      }
+    }
+  };
+  load_w(0, 0);
   const float r2 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
-  // Each thread keeps the BitLinear-normed values of its own elements in registers and
-  // writes them (or their codes) straight to their chain-transposed positions: no staging
-  // row, no extra pass.
+
+  // the BitLinear norm of unit g: y = (x * rstd) * normw (bitlinear.cpp:62-70)
+  auto unit_y = [&](int ai, int g, float* y) {
+    const int u = tid + g * BT;
+    const int j = u / L8, t0 = 8 * (u - j * L8);
+    const float4* xp = reinterpret_cast<const float4*>(X + j * LS + t0);
+    const float4 x0 = xp[0], x1 = xp[1];
+    float4 w0, w1;
+    if constexpr (PW) {
+      w0 = nwv[ai][g][0];
+      w1 = nwv[ai][g][1];
+    } else {
+      w0 = wq[ai & 1][g][0];
+      w1 = wq[ai & 1][g][1];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      y[c] = (f4el(x0, c) * r2) * f4el(w0, c);
+      y[4 + c] = (f4el(x1, c) * r2) * f4el(w1, c);
+    }
+  };
 #pragma unroll
   for (int ai = 0; ai < NA; ++ai) {
+    if (ai + 1 < NA) load_w(ai + 1, (ai + 1) & 1);
     const size_t ar = static_cast<size_t>(ai) * act.rows + row;
-    float4 yv[MAXV];
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const int k4 = threadIdx.x + j * blockDim.x;
-      if (k4 >= K4) continue;
-      const float4 w = wt(INW + ai, k4, j);
-      float y[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        y[c] = (X[act_pos(4 * k4 + c, K8, LS)] * r2) * el(w, c);
-        if (MODE == kInt8) m = fmaxf(m, fabsf(y[c]));
-      }
-      yv[j] = make_float4(y[0], y[1], y[2], y[3]);
-    }
-    float sa = 0.0f;
-    if (MODE == kInt8) {
-      m = block_max(m, red);
-      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
-      if (threadIdx.x == 0) act.sa[ar] = sa;
-    }
     float* yo = act.y + ar * act.ystride();
     int8_t* q = act.q + act.qoff(ai, 0, row, 0);  // plane 0 of this row; plane 1 at + qplane
     const size_t lop = act.qplane();
-    int32_t* ct = act.ct + ar * 8;
+    // unit g's eight values out: padding positions (t >= nb) as zeros in every plane
+    auto unit_out = [&](int g, const float* y, float sa) {
+      const int u = tid + g * BT;
+      const int j = u / L8, t0 = 8 * (u - j * L8);
+      const int nv = nb - t0;
+      if (MODE == kFloat) {
+        float o[8];
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const int k4 = threadIdx.x + j * blockDim.x;
-      if (k4 >= K4) continue;
+        for (int c = 0; c < 8; ++c) o[c] = c < nv ? y[c] : 0.0f;
+        float4* yp = reinterpret_cast<float4*>(yo + j * Lc + t0);
+        yp[0] = make_float4(o[0], o[1], o[2], o[3]);
+        yp[1] = make_float4(o[4], o[5], o[6], o[7]);
+      } else {
+        int32_t cd[8];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = 4 * k4 + c;
-        const float y = el(yv[j], c);
-        if (k < K8) {  // chain k % 8, position k / 8
-          const int pos = (k & 7) * Lc + (k >> 3);
-          if (MODE == kFloat) {
-            yo[pos] = y;
-          } else if (MODE == kFixed) {
-            const int32_t code = q510_body(y, a.qs);
-            const size_t o = ActBuf::qpos(pos);
-            q[o] = static_cast<int8_t>((code >> 8) & 0xFF);
-            q[lop + o] = static_cast<int8_t>(((code & 0xFF) - 128) & 0xFF);
-          } else {
-            q[ActBuf::qpos(pos)] = static_cast<int8_t>(q8_of(y, sa));
-          }
-        } else if (MODE == kFloat) {
-          yo[8 * Lc + (k - K8)] = y;
+        for (int c = 0; c < 8; ++c) cd[c] = (MODE == kFixed) ? q510_body(y[c], a.qs) : q8_of(y[c], sa);
+        uint32_t h0, h1, l0 = 0, l1 = 0;
+        if (MODE == kFixed) {
+          pack_split4(cd, h0, l0);
+          pack_split4(cd + 4, h1, l1);
         } else {
-          ct[k - K8] = (MODE == kFixed) ? q510_tail(y, a.qs) : q8_of(y, sa);
+          h0 = pack_low4(cd);
+          h1 = pack_low4(cd + 4);
         }
+        if (nv < 8) {
+          const uint32_t m0 = nv >= 4 ? ~0u : (nv <= 0 ? 0u : (1u << (8 * nv)) - 1u);
+          const uint32_t m1 = nv <= 4 ? 0u : (1u << (8 * (nv - 4))) - 1u;
+          h0 &= m0;
+          h1 &= m1;
+          l0 &= m0;
+          l1 &= m1;
+        }
+        const size_t o = ActBuf::qpos(j * Lc + t0);
+        *reinterpret_cast<uint2*>(q + o) = make_uint2(h0, h1);
+        if (MODE == kFixed) *reinterpret_cast<uint2*>(q + lop + o) = make_uint2(l0, l1);
+      }
+    };
+    // the tail elements, one per lane c < ntail
+    float yt = 0.0f;
+    if (tid < nt) yt = (X[8 * LS + tid] * r2) * a.normw[ai][K8 + tid];
+    float sa = 0.0f;
+    if constexpr (MODE == kInt8) {
+      // absmax over the row first (the padding contributes zeros)
+      float y[MAXG][8];
+      float m = tid < nt ? fabsf(yt) : 0.0f;
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g) {
+        if (tid + g * BT >= Lc) continue;
+        unit_y(ai, g, y[g]);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(y[g][c]));
+      }
+      m = block_max(m, red);
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+      if (tid == 0) act.sa[ar] = sa;
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g)
+        if (tid + g * BT < Lc) unit_out(g, y[g], sa);
+    } else {
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g) {
+        if (tid + g * BT >= Lc) continue;
+        float y[8];
+        unit_y(ai, g, y);
+        unit_out(g, y, 0.0f);
       }
     }
-    // zeros past each chain's last element and past the tail (padding the GEMMs read)
-    const int padw = Lc - nb;
-    for (int e = threadIdx.x; e < 8 * padw + (8 - nt); e += blockDim.x) {
-      if (e < 8 * padw) {
-        const int pos = (e / padw) * Lc + nb + e % padw;
-        if (MODE == kFloat) {
-          yo[pos] = 0.0f;
-        } else {
-          q[ActBuf::qpos(pos)] = 0;
-          if (MODE == kFixed) q[lop + ActBuf::qpos(pos)] = 0;
-        }
-      } else {
-        const int t = nt + (e - 8 * padw);
-        if (MODE == kFloat) yo[8 * Lc + t] = 0.0f;
-        else ct[t] = 0;
-      }
+    if (tid < 8) {
+      if (MODE == kFloat) yo[8 * Lc + tid] = tid < nt ? yt : 0.0f;
+      else act.ct[ar * 8 + tid] = tid < nt ? ((MODE == kFixed) ? q510_tail(yt, a.qs) : q8_of(yt, sa)) : 0;
     }
   }
 }
@@ -1237,34 +1330,45 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
 static int host_lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
 
 // Up to kPrologueFewRows rows (two per CU, the CUs otherwise idle) a row gets a 1024-thread
-// block with every input, the norm weights included, loaded at entry: each thread then
-// encodes 4-8 elements instead of 12-28, with four waves per SIMD to hide each other's
-// latency. Above it, 256-thread blocks that read the weights in the pass that uses them
-// keep more rows resident per CU.
+// block (k_rowpro) with every input, the norm weights included, loaded at entry: each thread
+// then works on one group and one unit, with four waves per SIMD to hide each other's
+// latency. Above it, 256-thread blocks keep more rows resident per CU. (One wave per row with
+// one chain wave for 8 rows measured slower: every row of a block then waits for the
+// slowest row's loads, and a single wave per row serialises the encoding.)
 constexpr int kPrologueFewRows = 512;
 
+// groups or units per row, whichever is more (k_rowpro)
+static int rowpro_need(const ActBuf& act) { return std::max(act.Lc, act.nb + (act.ntail > 0 ? 1 : 0)); }
+static bool rowpro_fits(const ActBuf& act) {
+  return rowpro_need(act) <= (act.rows <= kPrologueFewRows ? 2048 : 1024);
+}
+
 template <int MODE, int PRE, int NA>
-static hipError_t prologue4_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
-  const int K4 = act.K / 4;
+static hipError_t rowpro_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
+  const int need = rowpro_need(act), grid = row_grid(act.rows);
   if (act.rows <= kPrologueFewRows) {
-    if (K4 <= 1024) k_prologue4<MODE, PRE, NA, 1, true, 1024><<<row_grid(act.rows), 1024, lds, s>>>(a, act);
-    else k_prologue4<MODE, PRE, NA, 2, true, 1024><<<row_grid(act.rows), 1024, lds, s>>>(a, act);
-  } else if (K4 <= 3 * 256) {
-    k_prologue4<MODE, PRE, NA, 3, false, 256><<<row_grid(act.rows), 256, lds, s>>>(a, act);
+    if (need <= 1024) k_rowpro<MODE, PRE, NA, 1, true, 1024><<<grid, 1024, lds, s>>>(a, act);
+    else k_rowpro<MODE, PRE, NA, 2, true, 1024><<<grid, 1024, lds, s>>>(a, act);
+  } else if (need <= 256) {
+    k_rowpro<MODE, PRE, NA, 1, false, 256><<<grid, 256, lds, s>>>(a, act);
+  } else if (need <= 512) {
+    k_rowpro<MODE, PRE, NA, 2, false, 256><<<grid, 256, lds, s>>>(a, act);
+  } else if (need <= 768) {
+    k_rowpro<MODE, PRE, NA, 3, false, 256><<<grid, 256, lds, s>>>(a, act);
   } else {
-    k_prologue4<MODE, PRE, NA, 7, false, 256><<<row_grid(act.rows), 256, lds, s>>>(a, act);
+    k_rowpro<MODE, PRE, NA, 4, false, 256><<<grid, 256, lds, s>>>(a, act);
   }
   return hipGetLastError();
 }
 
 template <int MODE>
-static hipError_t prologue4_mode(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
-  if (a.pre == kPreNorm && a.na == 3) return prologue4_inst<MODE, kPreNorm, 3>(a, act, lds, s);
-  if (a.pre == kPreNorm && a.na == 1) return prologue4_inst<MODE, kPreNorm, 1>(a, act, lds, s);
-  if (a.pre == kPreSwish && a.na == 1) return prologue4_inst<MODE, kPreSwish, 1>(a, act, lds, s);
-  if (a.pre == kPreMixSwish && a.na == 1) return prologue4_inst<MODE, kPreMixSwish, 1>(a, act, lds, s);
-  if (a.pre == kPreNone && a.na == 1) return prologue4_inst<MODE, kPreNone, 1>(a, act, lds, s);
-  if (a.pre == kPreNone && a.na == 3) return prologue4_inst<MODE, kPreNone, 3>(a, act, lds, s);
+static hipError_t rowpro_mode(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
+  if (a.pre == kPreNorm && a.na == 3) return rowpro_inst<MODE, kPreNorm, 3>(a, act, lds, s);
+  if (a.pre == kPreNorm && a.na == 1) return rowpro_inst<MODE, kPreNorm, 1>(a, act, lds, s);
+  if (a.pre == kPreSwish && a.na == 1) return rowpro_inst<MODE, kPreSwish, 1>(a, act, lds, s);
+  if (a.pre == kPreMixSwish && a.na == 1) return rowpro_inst<MODE, kPreMixSwish, 1>(a, act, lds, s);
+  if (a.pre == kPreNone && a.na == 1) return rowpro_inst<MODE, kPreNone, 1>(a, act, lds, s);
+  if (a.pre == kPreNone && a.na == 3) return rowpro_inst<MODE, kPreNone, 3>(a, act, lds, s);
   return hipErrorNotSupported;
 }
 
@@ -1274,21 +1378,21 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
   const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);
   const size_t lds = (2 * rowf + 16) * sizeof(float);
   const bool sw = a.pre == kPreSwish || a.pre == kPreMixSwish;
-  const size_t lds4 = ((sw ? 2 : 1) * rowf + 16) * sizeof(float);  // k_prologue4
-  bool fast = act.K % 4 == 0 && act.K / 4 <= 7 * 256 && aligned16(a.x) && (a.na == 1 || a.na == 3);
+  const size_t lds4 = ((sw ? 2 : 1) * rowf + 16) * sizeof(float);  // k_rowpro
+  bool fast = act.K % 4 == 0 && rowpro_fits(act) && aligned16(a.x) && (a.na == 1 || a.na == 3);
   if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
   if (sw) fast = fast && aligned16(a.x2);
+  for (int i = 0; i < a.na; ++i) fast = fast && a.normwT[i] && aligned16(a.normwT[i]);
   if (a.pre == kPreMixSwish) {
     fast = fast && a.na == 1 && aligned16(a.mix_f) && aligned16(a.mix_state) && (!a.mix_lb || aligned16(a.mix_lb));
     if (!fast) return hipErrorNotSupported;
   }
-  for (int i = 0; i < a.na; ++i) fast = fast && aligned16(a.normw[i]);
   if (fast) {
     hipError_t e = hipErrorNotSupported;
     switch (mode) {
-      case kFloat: e = prologue4_mode<kFloat>(a, act, lds4, s); break;
-      case kFixed: e = prologue4_mode<kFixed>(a, act, lds4, s); break;
-      default: e = prologue4_mode<kInt8>(a, act, lds4, s); break;
+      case kFloat: e = rowpro_mode<kFloat>(a, act, lds4, s); break;
+      case kFixed: e = rowpro_mode<kFixed>(a, act, lds4, s); break;
+      default: e = rowpro_mode<kInt8>(a, act, lds4, s); break;
     }
     if (e != hipErrorNotSupported) return e;
   }
