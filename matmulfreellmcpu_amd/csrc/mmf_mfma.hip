@@ -28,14 +28,14 @@
 // Block: WM x WN waves (2 x 4 for long row ranges and wide matrices: 128 x 256 tiles, so
 // the activations are re-read once per 256 columns), each wave a 64 x 64 tile (2 x 2
 // fragments).
-// The operands of each 64-position stage are staged through registers: every wave loads its
-// share of the stage (16 bytes or one word per lane, in the matrix cores' lane order) two
-// stages ahead into one of two register sets, writes it to one of two LDS slots a stage
-// ahead, and one barrier per stage publishes the slot to the block. Every fragment read is
-// one linear 1 KB (A) or 256 B (B) LDS access. Direct global-to-LDS DMA into a 4-slot ring
-// measured 5-9% slower: the compiler cannot count LDS reads against an outstanding LDS DMA,
-// so each stage's first product waited for all of that stage's LDS reads.
-//
+// The operands of each 64-position stage move from global memory straight into a ring of
+// LDS slots (buffer loads into LDS, up to 6 slots, 5 stages ahead), each wave moving its
+// share of every stage (16 bytes or one word per lane, in the matrix cores' lane order);
+// one barrier per stage publishes a slot to the block. Every fragment read is one linear
+// 1 KB (A) or 256 B (B) LDS access. (Against staging the same loads through registers two
+// stages ahead, this measured 10% faster on the long-prefill shapes; most of the remaining
+// gap to the matrix-core peak is the stage barriers' LDS-read bubble, the output stores
+// after the loop, and whole-chip rounds of tiles.)
 // Split-K: when a GEMM has too few tiles to occupy the chip (a few dozen rows, or narrow
 // matrices), blockIdx.y selects a contiguous range of stages; each block stores its exact
 // int32 partial tile, and k_splitk_epi adds the partials in split order and applies the
@@ -96,30 +96,66 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-// LDS bytes before the int8 row scales: KW groups of two stage slots, or the K-group
-// reduction buffer (one int32 tile per wave of a group) when that is larger.
-template <int MODE, int WM, int WN, int KQ, int KW>
-__host__ __device__ constexpr int lds_main() {
-  const int slots = KW * 2 * (((MODE == kFixed) ? 2 : 1) * 2 * WM * KQ * 1024 + 2 * WN * KQ * 256);
-  const int red = (KW > 1) ? WM * WN * 64 * 64 * 4 : 0;
-  return slots > red ? slots : red;
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Buffer loads straight into LDS (buffer_load ... lds) of 16 (or 4) bytes per lane from
+// byte offset voff (per lane) + soff (uniform) of a raw buffer (base, num_records bytes;
+// offsets past it read zeros): lane l's bytes land at LDS address m0 + 16 l (4 l).
+// Written as inline assembly so that the compiler, which cannot tell which LDS bytes such a
+// transfer writes, adds no waits of its own: it made every LDS read after a transfer wait
+// for all transfers in flight (or, for global_load_lds, for all earlier LDS reads), which
+// undid the ring. The kernel orders the transfers itself: it waits for a stage's transfers
+// (vmcnt) and passes a barrier before any wave reads that stage's slot, and a slot is
+// refilled only after every wave has passed the barrier that follows its last reads. M0 is
+// set by each of these statements (one wait state before the load reads it) and used by
+// nothing else in the kernel.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return u32x4{static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+// the 32-bit LDS address of a pointer into a __shared__ array
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)p));
+}
+__device__ __forceinline__ void lds_dma16(u32x4 r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "s"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(u32x4 r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "s"(lds)
+               : "memory");
 }
 
-template <int MODE, int EPI, int WM, int WN, int KQ, int KW>
+// Bytes of one stage of one K-group: the activation fragments [plane][frag][k-chunk] of
+// 1 KB, then the weight fragments [group][k-chunk] of 256 B.
+template <int MODE, int WM, int WN, int FM, int FN, int KQ>
+__host__ __device__ constexpr int stage_bytes() {
+  return ((MODE == kFixed) ? 2 : 1) * FM * WM * KQ * 1024 + FN * WN * KQ * 256;
+}
+// Depth of the stage ring: as many slots (at most 6) as fit the LDS of the blocks a CU
+// holds (two for blocks of at most four waves, else one), with the int8 row scales.
+template <int MODE, int WM, int WN, int FM, int FN, int KQ, int KW>
+__host__ __device__ constexpr int ring_depth() {
+  constexpr int per_cu = 160 * 1024, blocks = (WM * WN * KW > 4) ? 1 : 2;
+  constexpr int d = (per_cu / blocks - 32 * FM * WM * 4 - 256) / (KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>());
+  return d > 6 ? 6 : d;
+}
+
+template <int MODE, int EPI, int WM, int WN, int FM, int FN, int KQ, int KW>
 __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
   constexpr int NW = WM * WN;                   // waves per K-group (one tile)
-  constexpr int BM = 64 * WM;                   // rows per block
-  constexpr int BG = 2 * WN;                    // physical 32-column groups per block
-  constexpr int FR = BM / 32;                   // 32-row fragments
+  constexpr int BM = 32 * FM * WM;              // rows per block
+  constexpr int BG = FN * WN;                   // physical 32-column groups per block
+  constexpr int FR = FM * WM;                   // 32-row fragments per block
   constexpr int SA = P * FR * KQ * 1024;        // A bytes per stage: [plane][frag][k-chunk]
   constexpr int SS = SA + BG * KQ * 256;        // stage bytes (A, then B: [group][k-chunk])
   constexpr int DA = P * FR * KQ / NW;          // A transfers per wave per stage
   constexpr int DB = BG * KQ / NW;              // B transfers per wave per stage
   static_assert(DA * NW == P * FR * KQ && DB * NW == BG * KQ, "transfers must split evenly over the waves");
-  constexpr int LB = lds_main<MODE, WM, WN, KQ, KW>();  // stage slots, reused by the K-group reduction
-  extern __shared__ __align__(16) unsigned char lds[];   // [KW][2][SS] slots, then srow[BM]
-  float* srow = reinterpret_cast<float*>(lds + LB);      // Int8: the block's activation scales
+  static_assert(EPI != kEpiSwigluPair || FN % 2 == 0, "a swiglu pair needs both its column groups in one wave");
+  static_assert(SS == stage_bytes<MODE, WM, WN, FM, FN, KQ>(), "stage layout");
 
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
@@ -137,8 +173,9 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   // K-groups: with KW > 1 the block's waves form KW groups of NW waves; group kg multiplies
   // the kg-th of KW equal runs of the block's stages through its own LDS slots, and the
   // groups' partial tiles are added in LDS before the epilogue (exact int32 sums)
-  const int kg = (KW > 1) ? (tid >> 6) / NW : 0, wave = (KW > 1) ? (tid >> 6) % NW : (tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar stage offsets
+  const int kg = (KW > 1) ? wid / NW : 0, wave = (KW > 1) ? wid % NW : wid;
+  const int wm = wave / WN, wn = wave % WN;  // this wave: row fragments wm*FM.., groups wn*FN..
   const int row0 = (tile / nct) * BM;
   const int cgb = (tile % nct) * BG;
   const int am = (act.na > 1) ? z : 0;
@@ -151,11 +188,14 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   const int ng = max(0, min(cnt, nst - gb));     // stages the group multiplies
   const int8_t* qbase = act.q + 2 * static_cast<size_t>(am) * act.qplane();
 
-  // per-lane sources of this wave's loads (advanced by KQ fragments = KQ KB of the
-  // fragment-tiled activations / 128 words per stage). Row groups past the last 32-row
-  // group of the activations (a row tile that overhangs it) read that last group again;
-  // their products are never stored.
-  const int8_t* asrc[DA];
+  // per-lane sources of this wave's transfers (advanced by KQ fragments = KQ KB of the
+  // fragment-tiled activations / KQ x 256 B of weights per stage). Row groups past the last
+  // 32-row group of the activations (a row tile that overhangs it) read that last group
+  // again; their products are never stored. (Byte offsets from the matrix's planes and
+  // from its weights: both below 2^31, which launch_gemm checks.)
+  const u32x4 arsrc = raw_rsrc(qbase, static_cast<uint32_t>(P * act.qplane()));
+  const u32x4 brsrc = raw_rsrc(W.pkm, static_cast<uint32_t>(ng32 * (Lc / 4) * 256));
+  uint32_t aoff[DA];
   const int lastg = act.rows32() / 32 - 1;
 #pragma unroll
   for (int i = 0; i < DA; ++i) {
@@ -163,15 +203,15 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
     const int kh = f % KQ, pl = (f / KQ) / FR, rf = (f / KQ) % FR;
     int g = (row0 >> 5) + rf;
     g = g < lastg ? g : lastg;
-    asrc[i] = qbase + pl * act.qplane() + (static_cast<size_t>(g) * (Lc / 4) + kh) * 1024 + lane * 16;
+    aoff[i] = static_cast<uint32_t>(pl * act.qplane() + (static_cast<size_t>(g) * (Lc / 4) + kh) * 1024 + lane * 16);
   }
-  const uint32_t* bsrc[DB];
+  uint32_t boff[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i) {
     const int f = wave * DB + i;  // = group * KQ + k-chunk
     int cg = cgb + f / KQ;
     cg = cg < ng32 ? cg : ng32 - 1;
-    bsrc[i] = W.pkm + (static_cast<size_t>(cg) * (Lc / 4) + f % KQ) * 64 + lane;
+    boff[i] = static_cast<uint32_t>(((static_cast<size_t>(cg) * (Lc / 4) + f % KQ) * 64 + lane) * 4);
   }
 
   // epilogue operands that do not depend on the accumulators, fetched before the main loop
@@ -185,13 +225,15 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   }
   const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
   const int ol = lane & 31;
-  int col[2];
-  int32_t csum[2];
+  // column (in N) of each of the wave's groups; a swiglu pair's gate group is even and its
+  // up partner follows it: gate column (cg/2)*32 + ol, up column Nout + the same
+  int col[FN];
+  int32_t csum[FN];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int cg = cgb + wn * 2 + (EPI == kEpiSwigluPair ? 0 : b);
-    col[b] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + (b ? Nout : 0) : cg * 32 + ol;
-    csum[b] = (MODE == kFixed && ksp == 1 && col[b] < N) ? 128 * W.rowsum[col[b]] : 0;
+  for (int bj = 0; bj < FN; ++bj) {
+    const int cg = cgb + wn * FN + bj;
+    col[bj] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + ((bj & 1) ? Nout : 0) : cg * 32 + ol;
+    csum[bj] = (MODE == kFixed && ksp == 1 && col[bj] < N) ? 128 * W.rowsum[col[bj]] : 0;
   }
   float* const outz = a.out[EPI == kEpiSwigluPair ? 0 : z];
   int32_t* const accz = a.acc[z];
@@ -203,135 +245,151 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rawacc), "s"(swn), "s"(ntail), "s"(invf),
           "s"(scw));
 
-  v16i acc[P][2][2];
+  v16i acc[P][FM][FN];
 #pragma unroll
   for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-    for (int ai = 0; ai < 2; ++ai)
+    for (int ai = 0; ai < FM; ++ai)
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj) acc[pl][ai][bj] = v16i{};
+      for (int bj = 0; bj < FN; ++bj) acc[pl][ai][bj] = v16i{};
 
-  // Register sets: stage s lives in set s % 2 from its load (two stages ahead) to its LDS
-  // write (one stage ahead); LDS slot s % 2 holds it while it is multiplied. Loads past the
-  // block's last stage repeat that stage (never written to a slot that is read), so every
-  // path through the loop has the same loads in flight and the compiler's vmcnt waits
-  // for a register set let the other set's loads stay outstanding.
-  v4i ra[2][DA];
-  uint32_t rb[2][DB];
-  unsigned char* const gslots = lds + kg * 2 * SS;
-  auto gload = [&](auto setc, int s2) {
-    constexpr int SET = decltype(setc)::value;
+  // The stage ring: D slots, each its own LDS array (so that the compiler tells the slot
+  // being filled from the slot being read and waits for nothing it need not), each holding
+  // one stage of every K-group ([KW][SS] bytes). Every wave moves its share of a stage (DA
+  // activation transfers of 1 KB, DB weight transfers of 256 B) from global memory straight
+  // into a slot with buffer loads into LDS (lds_dma16/4: lane l's bytes land at the
+  // transfer's base + l * size), D - 1 stages ahead: no registers and no LDS stores on the way. Before stage st a
+  // wave waits until only the later stages' transfers are outstanding, and one barrier per
+  // stage publishes slot st % D to the block and frees the slot of stage st - 1 for stage
+  // st + D - 1. Loads past the block's last stage repeat that stage (never read), so every
+  // stage issues the same transfers and the wait count is a constant.
+  constexpr int D = ring_depth<MODE, WM, WN, FM, FN, KQ, KW>();
+  constexpr int NT = DA + DB;  // transfers per wave per stage
+  static_assert(D >= 3 && D <= 6 && (D - 2) * NT < 64, "ring depth");
+  constexpr int QB = KW * SS;
+  __shared__ __align__(16) unsigned char q0[QB], q1[QB], q2[QB], q3[D > 3 ? QB : 16], q4[D > 4 ? QB : 16],
+      q5[D > 5 ? QB : 16];
+  __shared__ float srow[BM];  // Int8: the block's activation scales
+  auto slot = [&](auto sc) -> unsigned char* {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return q0;
+    else if constexpr (S == 1) return q1;
+    else if constexpr (S == 2) return q2;
+    else if constexpr (S == 3) return q3;
+    else if constexpr (S == 4) return q4;
+    else return q5;
+  };
+  auto issue = [&](auto sc, int s2) {
+    unsigned char* sb = slot(sc) + kg * SS;
     const int sg = st0 + min(gb + s2, nst - 1);
 #pragma unroll
-    for (int i = 0; i < DA; ++i) ra[SET][i] = *reinterpret_cast<const v4i*>(asrc[i] + sg * 1024 * KQ);
+    for (int i = 0; i < DA; ++i) lds_dma16(arsrc, aoff[i], sg * 1024 * KQ, lds_addr(sb + (wave * DA + i) * 1024));
 #pragma unroll
-    for (int i = 0; i < DB; ++i) rb[SET][i] = bsrc[i][sg * 64 * KQ];
+    for (int i = 0; i < DB; ++i) lds_dma4(brsrc, boff[i], sg * 256 * KQ, lds_addr(sb + SA + (wave * DB + i) * 256));
   };
-  auto lwrite = [&](auto setc) {
-    constexpr int SET = decltype(setc)::value;
-    unsigned char* sb = gslots + SET * SS;
-#pragma unroll
-    for (int i = 0; i < DA; ++i) *reinterpret_cast<v4i*>(sb + (wave * DA + i) * 1024 + lane * 16) = ra[SET][i];
-#pragma unroll
-    for (int i = 0; i < DB; ++i) *reinterpret_cast<uint32_t*>(sb + SA + (wave * DB + i) * 256 + lane * 4) = rb[SET][i];
-  };
-  // one stage: slot SET is complete once every wave's LDS writes have returned and all
-  // have passed the barrier, which also means every wave has finished reading slot SET ^ 1
-  // (the previous stage), so the next stage goes there
-  auto stage = [&](auto setc, int st) {
-    constexpr int SET = decltype(setc)::value;
+  auto stage = [&](auto sc, int st) {
+    constexpr int S = decltype(sc)::value;
+    // this wave's reads of the previous stage have returned (a group past its run issues
+    // reads it never waits for) and its transfers of stage st have landed
     wait_lds();
+    wait_vm<(D - 2) * NT>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    const unsigned char* sb = gslots + SET * SS;
-    uint32_t bw[KQ][2];
-    v4i av[KQ][P][2];
+    issue(ic<(S + D - 1) % D>{}, st + D - 1);
+    const unsigned char* sb = slot(sc) + kg * SS;
+    uint32_t bw[KQ][FN];
+    v4i av[KQ][P][FM];
 #pragma unroll
     for (int kh = 0; kh < KQ; ++kh)
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj)
-        bw[kh][bj] = *reinterpret_cast<const uint32_t*>(sb + SA + ((wn * 2 + bj) * KQ + kh) * 256 + lane * 4);
+      for (int bj = 0; bj < FN; ++bj)
+        bw[kh][bj] = *reinterpret_cast<const uint32_t*>(sb + SA + ((wn * FN + bj) * KQ + kh) * 256 + lane * 4);
 #pragma unroll
     for (int kh = 0; kh < KQ; ++kh)
 #pragma unroll
       for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-        for (int ai = 0; ai < 2; ++ai)
-          av[kh][pl][ai] = *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * 2 + ai) * KQ + kh) * 1024 + lane * 16);
-    lwrite(ic<SET ^ 1>{});
-    gload(ic<SET ^ 1>{}, st + 3);
+        for (int ai = 0; ai < FM; ++ai)
+          av[kh][pl][ai] = *reinterpret_cast<const v4i*>(sb + ((pl * FR + wm * FM + ai) * KQ + kh) * 1024 + lane * 16);
     // all LDS reads of the stage first, then the matrix-core work: each product waits only
-    // for its own operands while the later reads are in flight
+    // for its own operands while the later reads are in flight. A group past its run (an
+    // uneven split) multiplies zero weights instead of branching around the products: a
+    // branch would make the first product wait for every read of the stage.
     __builtin_amdgcn_sched_barrier(0);
-    if (KW > 1 && st >= ng) return;  // a group past its run (uneven split): loads only
+    const bool run = !(KW > 1 && st >= ng);
 #pragma unroll
     for (int kh = 0; kh < KQ; ++kh) {
-      v4i bop[2];
+      v4i bop[FN];
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj) bop[bj] = expand_w(bw[kh][bj]);
+      for (int bj = 0; bj < FN; ++bj) bop[bj] = expand_w(run ? bw[kh][bj] : 0u);
 #pragma unroll
       for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-        for (int ai = 0; ai < 2; ++ai)
+        for (int ai = 0; ai < FM; ++ai)
 #pragma unroll
-          for (int bj = 0; bj < 2; ++bj)
+          for (int bj = 0; bj < FN; ++bj)
             acc[pl][ai][bj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[kh][pl][ai], bop[bj], acc[pl][ai][bj], 0, 0, 0);
     }
   };
   if (cnt > 0) {
-    gload(ic<0>{}, 0);
-    gload(ic<1>{}, 1);
-    lwrite(ic<0>{});
-    gload(ic<0>{}, 2);
+    issue(ic<0>{}, 0);
+    issue(ic<1>{}, 1);
+    if constexpr (D > 3) issue(ic<2>{}, 2);
+    if constexpr (D > 4) issue(ic<3>{}, 3);
+    if constexpr (D > 5) issue(ic<4>{}, 4);
     int st = 0;
-    for (; st + 1 < cnt; st += 2) {  // straight-line pairs: the same loads in flight on every path
+    for (; st + D <= cnt; st += D) {  // straight-line runs of D stages: compile-time slots
       stage(ic<0>{}, st);
       stage(ic<1>{}, st + 1);
+      stage(ic<2>{}, st + 2);
+      if constexpr (D > 3) stage(ic<3>{}, st + 3);
+      if constexpr (D > 4) stage(ic<4>{}, st + 4);
+      if constexpr (D > 5) stage(ic<5>{}, st + 5);
     }
     if (st < cnt) stage(ic<0>{}, st);
+    if (st + 1 < cnt) stage(ic<1>{}, st + 1);
+    if constexpr (D > 3) if (st + 2 < cnt) stage(ic<2>{}, st + 2);
+    if constexpr (D > 4) if (st + 3 < cnt) stage(ic<3>{}, st + 3);
+    if constexpr (D > 5) if (st + 4 < cnt) stage(ic<4>{}, st + 4);
   }
+  // every transfer (the repeats past the last stage included) has landed before the LDS is
+  // reused or the block ends
   wait_lds();
   wait_vm<0>();
   if (MODE == kInt8) {
-    // the scales to LDS for the epilogue (every wave has finished its last stage's reads)
-    __builtin_amdgcn_s_barrier();
     if (kg == 0 && wave * 64 < BM) srow[wave * 64 + lane] = sv;
     __syncthreads();
   }
   if constexpr (KW > 1) {
     // K-group reduction: FixedQ510 folds its planes first (hi * 256 + lo into plane 1, as
-    // the split-K partials do), then groups 1..KW-1 in turn hand their tiles to group 0
-    // through the stage slots, free once every wave has passed the barrier
+    // the split-K partials do), then groups 1..KW-1 in turn hand their tiles to group 0,
+    // one fragment at a time, through slot 0 (free once every wave has passed a barrier)
     if constexpr (MODE == kFixed) {
 #pragma unroll
-      for (int ai = 0; ai < 2; ++ai)
+      for (int ai = 0; ai < FM; ++ai)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
+        for (int bj = 0; bj < FN; ++bj)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             acc[1][ai][bj][i] = acc[0][ai][bj][i] * 256 + acc[1][ai][bj][i];
             acc[0][ai][bj][i] = 0;
           }
     }
-    int32_t* red = reinterpret_cast<int32_t*>(lds);  // [NW][64 values][64 lanes]
-    for (int r = 1; r < KW; ++r) {
-      __syncthreads();
-      if (kg == r) {
+    static_assert(NW * 16 * 64 * 4 <= QB, "a fragment of every wave fits one slot");
+    int32_t* red = reinterpret_cast<int32_t*>(q0);  // [NW][16 values][64 lanes]
 #pragma unroll
-        for (int ai = 0; ai < 2; ++ai)
+    for (int f = 0; f < FM * FN; ++f) {
+      for (int r = 1; r < KW; ++r) {
+        __syncthreads();
+        if (kg == r) {
 #pragma unroll
-          for (int bj = 0; bj < 2; ++bj)
+          for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * 64 + lane] = acc[P - 1][f / FN][f % FN][i];
+        }
+        __syncthreads();
+        if (kg == 0) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) red[(wave * 64 + (ai * 2 + bj) * 16 + i) * 64 + lane] = acc[P - 1][ai][bj][i];
-      }
-      __syncthreads();
-      if (kg == 0) {
-#pragma unroll
-        for (int ai = 0; ai < 2; ++ai)
-#pragma unroll
-          for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[P - 1][ai][bj][i] += red[(wave * 64 + (ai * 2 + bj) * 16 + i) * 64 + lane];
+          for (int i = 0; i < 16; ++i) acc[P - 1][f / FN][f % FN][i] += red[(wave * 16 + i) * 64 + lane];
+        }
       }
     }
     if (kg != 0) return;
@@ -342,15 +400,15 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
     int32_t* wp = wsp + (static_cast<size_t>(ks) * a.nmat + z) * act.rows * static_cast<size_t>(N);
     const int Nh = N / 2;
 #pragma unroll
-    for (int bj = 0; bj < 2; ++bj) {
-      const int cg = cgb + wn * 2 + bj;
-      const int o = (EPI == kEpiSwigluPair) ? ((cg & 1) ? Nh : 0) + (cg >> 1) * 32 + (lane & 31) : cg * 32 + (lane & 31);
+    for (int bj = 0; bj < FN; ++bj) {
+      const int cg = cgb + wn * FN + bj;
+      const int o = (EPI == kEpiSwigluPair) ? ((cg & 1) ? Nh : 0) + (cg >> 1) * 32 + ol : cg * 32 + ol;
       if (cg >= ng32 || o >= N) continue;
 #pragma unroll
-      for (int ai = 0; ai < 2; ++ai)
+      for (int ai = 0; ai < FM; ++ai)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int row = row0 + wm * 64 + ai * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+          const int row = row0 + (wm * FM + ai) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
           if (row >= act.rows) continue;
           wp[static_cast<size_t>(row) * N + o] =
               (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] : acc[0][ai][bj][i];
@@ -360,19 +418,20 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   }
 
   // epilogue: exact integer totals, dequantisation, output stage. The residual rows of
-  // both fragments are loaded in one batch before any store.
-  // stored columns of this lane: fragment b (non-pair) or the pair's gate column
-  constexpr int NB = (EPI == kEpiSwigluPair) ? 1 : 2;
+  // all fragments are loaded in one batch before any store. Stored columns of this lane:
+  // one per group (NB = FN), or one per swiglu pair (its gate column; NB = FN / 2).
+  constexpr int NB = (EPI == kEpiSwigluPair) ? FN / 2 : FN;
+  constexpr int GS = (EPI == kEpiSwigluPair) ? 2 : 1;  // groups per stored column
   bool cok[NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) cok[b] = col[b] < Nout;
-  float addv[2][16][NB];
+  for (int b = 0; b < NB; ++b) cok[b] = col[GS * b] < Nout;
+  float addv[FM][16][NB];
   if (EPI == kEpiAdd) {
 #pragma unroll
-    for (int ai = 0; ai < 2; ++ai)
+    for (int ai = 0; ai < FM; ++ai)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        int row = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5) + 8 * (i >> 2) + (i & 3);
+        int row = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5) + 8 * (i >> 2) + (i & 3);
         row = row < act.rows ? row : act.rows - 1;
 #pragma unroll
         for (int b = 0; b < NB; ++b) addv[ai][i][b] = cok[b] ? addp[static_cast<size_t>(row) * N + col[b]] : 0.0f;
@@ -385,24 +444,24 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
                     (EPI != kEpiSwigluPair || static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
   if (fast) {
 #pragma unroll
-    for (int ai = 0; ai < 2; ++ai) {
-      const int rbase = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5);
+    for (int ai = 0; ai < FM; ++ai) {
+      const int rbase = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = rbase + 8 * (i >> 2) + (i & 3);
         const size_t grow = static_cast<size_t>(r);
         const float den = (MODE == kInt8) ? scw * srow[r - row0] : 1.0f;
-        float val[2];
+        float val[FN];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int32_t s = (MODE == kFixed) ? acc[0][ai][b][i] * 256 + acc[P - 1][ai][b][i] + csum[b] : acc[0][ai][b][i];
-          val[b] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den;
+        for (int bj = 0; bj < FN; ++bj) {
+          const int32_t s = (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] + csum[bj] : acc[0][ai][bj][i];
+          val[bj] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den;
         }
-        if (EPI == kEpiSwigluPair) {
-          outz[grow * Nout + col[0]] = swiglu_of(val[0], val[1], false);
-        } else {
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
+        for (int b = 0; b < NB; ++b) {
+          if (EPI == kEpiSwigluPair)
+            outz[grow * Nout + col[2 * b]] = swiglu_of(val[2 * b], val[2 * b + 1], false);
+          else
             outz[grow * N + col[b]] = (EPI == kEpiAdd) ? addv[ai][i][b] + val[b] : val[b];
         }
       }
@@ -410,8 +469,8 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
     return;
   }
 #pragma unroll
-  for (int ai = 0; ai < 2; ++ai) {
-    const int rbase = row0 + wm * 64 + ai * 32 + 4 * (lane >> 5);
+  for (int ai = 0; ai < FM; ++ai) {
+    const int rbase = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5);
     float den[16];
     if (MODE == kInt8) {
 #pragma unroll
@@ -423,29 +482,28 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
       if (row >= act.rows) continue;
       const size_t grow = static_cast<size_t>(row);
       const int32_t* ct = act.ct + (static_cast<size_t>(am) * act.rows + row) * 8;
-      int32_t tot[2];
-      float val[2];
+      int32_t tot[FN];
+      float val[FN];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        int32_t s = (MODE == kFixed) ? acc[0][ai][b][i] * 256 + acc[P - 1][ai][b][i] + csum[b] : acc[0][ai][b][i];
-        if (ntail && col[b] < N)
-          for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(tailp[col[b] * 8 + t]) * ct[t];
-        tot[b] = s;
-        val[b] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den[i];
+      for (int bj = 0; bj < FN; ++bj) {
+        int32_t s = (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] + csum[bj] : acc[0][ai][bj][i];
+        if (ntail && col[bj] < N)
+          for (int t = 0; t < ntail; ++t) s += static_cast<int32_t>(tailp[col[bj] * 8 + t]) * ct[t];
+        tot[bj] = s;
+        val[bj] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den[i];
       }
-      if (EPI == kEpiSwigluPair) {
-        if (!cok[0]) continue;
-        if (accz) {
-          accz[grow * N + col[0]] = tot[0];
-          accz[grow * N + col[1]] = tot[1];
-        }
-        if (rawacc) continue;
-        const size_t e = grow * Nout + col[0];
-        outz[e] = swiglu_of(val[0], val[1], static_cast<int64_t>(e) >= (swn & ~7));
-      } else {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          if (!cok[b]) continue;
+      for (int b = 0; b < NB; ++b) {
+        if (!cok[b]) continue;
+        if (EPI == kEpiSwigluPair) {
+          if (accz) {
+            accz[grow * N + col[2 * b]] = tot[2 * b];
+            accz[grow * N + col[2 * b + 1]] = tot[2 * b + 1];
+          }
+          if (rawacc) continue;
+          const size_t e = grow * Nout + col[2 * b];
+          outz[e] = swiglu_of(val[2 * b], val[2 * b + 1], static_cast<int64_t>(e) >= (swn & ~7));
+        } else {
           const size_t e = grow * N + col[b];
           if (accz) accz[e] = tot[b];
           if (rawacc) continue;
@@ -533,12 +591,6 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   }
 }
 
-// LDS bytes: the stage slots (or the K-group reduction buffer), then the int8 row scales
-template <int MODE, int WM, int WN, int KQ, int KW>
-constexpr int ring_bytes() {
-  return lds_main<MODE, WM, WN, KQ, KW>() + 64 * WM * 4;
-}
-
 template <int WM, int WN>
 int tiles_of(const GemmArgs& a) {
   const int ng32 = (a.p[0].g.N + 31) / 32;
@@ -549,11 +601,17 @@ int tiles_of(const GemmArgs& a) {
 // slower for Int8Absmax (one block per CU instead of two).
 constexpr int kStageKQ = 2;
 
-template <int MODE, int EPI, int WM, int WN, int KQ, int KW>
+// A tile of 64 TM rows and 64 TN columns: TM x TN waves of 64 x 64 (2 x 2 fragments) per
+// K-group. (Waves of 32 x 128, one row fragment by four column groups, read 40% fewer
+// operand bytes from LDS per product but measured 10-20% slower on every long-prefill
+// shape: twice the weight expansion per product, for no fewer stalls.)
+template <int MODE, int EPI, int TM, int TN, int KQ, int KW>
 bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
-  constexpr int bytes = ring_bytes<MODE, WM, WN, KQ, KW>();  // at most 97 KB
+  constexpr int WM = TM, WN = TN, FM = 2, FN = 2;
+  constexpr int bytes =
+      ring_depth<MODE, WM, WN, FM, FN, KQ, KW>() * KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>() + 32 * FM * WM * 4;
   if (bytes > lds_limit()) return false;
-  k_mfma<MODE, EPI, WM, WN, KQ, KW><<<grid, dim3(64 * WM * WN * KW), bytes, s>>>(a, act);
+  k_mfma<MODE, EPI, WM, WN, FM, FN, KQ, KW><<<grid, dim3(64 * WM * WN * KW), 0, s>>>(a, act);
   return true;
 }
 

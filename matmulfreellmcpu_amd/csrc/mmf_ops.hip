@@ -1494,9 +1494,11 @@ int mfma_min_rows() {
 
 hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   if (a.mode != kFloat && mfma_min_rows() > 0 && a.rows >= mfma_min_rows()) {
-    bool ok = true;
+    // (the matrix-core kernel addresses a matrix's planes and weights with 31-bit offsets)
+    bool ok = 2 * act.qplane() <= 0x7FFFFFFFu;
     for (int z = 0; z < (a.epi == kEpiSwigluPair ? 1 : a.nmat); ++z)
-      ok = ok && a.p[z].pkm && (a.p[z].pair != 0) == (a.epi == kEpiSwigluPair);
+      ok = ok && a.p[z].pkm && (a.p[z].pair != 0) == (a.epi == kEpiSwigluPair) &&
+           pkm_words(a.p[z].g) * 4 <= 0x7FFFFFFFu;
     if (ok) return launch_gemm_mfma(a, act, s);
   }
   switch (a.mode) {
