@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
@@ -1058,140 +1059,176 @@ __global__ void k_gather_rows(const float* __restrict__ x, const int* __restrict
   for (int k = threadIdx.x; k < K; k += blockDim.x) dst[k] = src[k];
 }
 
-// The recurrence for H % 16 == 0, staged through LDS so that enough bytes are in flight:
-// a block owns 16 columns (H/16 blocks spread over the CUs) and walks time in tiles of
-// kScTT steps. Waves by role: wave 0 runs the 16 column chains (state = fma(g, state, in),
-// in time order) from LDS; waves 1-4 fill a ring of kScNR tiles of g and in by direct
-// global-to-LDS DMA (lane l's 16 bytes land at LDS base + 16l: 16 steps x 16 columns per
-// transfer); waves 5-6 store the previous tile's results. One barrier per tile.
-constexpr int kScCols = 16, kScTT = 128, kScNR = 4;
-constexpr int kScWaves = 7;
+// The recurrence for H % C == 0 (C = 4, 8 or 16 columns per block), staged through LDS so
+// that enough bytes are in flight: a block owns C columns and walks time in tiles of kScTT
+// steps. Waves by role: wave 0 runs the C column chains (state = fma(g, state, in), in
+// time order) at raised issue priority; waves 1-4 fill a ring of kScNR tiles of g and in by
+// direct global-to-LDS DMA (lane l's 16 bytes land at LDS base + 16 l: 256 / C steps x C
+// columns per transfer); all fifteen other waves convert each tile into column-major rows
+// for the chain, and the last four store the previous tile's results. One barrier per
+// tile. (Launches use C = 16, one 64-byte line per step row: narrower blocks shared lines
+// between blocks and measured twice as slow at 2048 x 2048.) The column groups of one
+// line go to blocks of the same XCD (blocks are dealt to the 8 XCDs round-robin).
+constexpr int kScTT = 128;
+constexpr int kScWaves = 16, kScStoreWaves = 4;  // the last kScStoreWaves waves store
+// Ring depth (tiles): the loads of a tile are in flight for NR - 2 tiles of chain work
+// (about 1.5 us each at C = 16).
+template <int C>
+constexpr int scan_ring_depth() {
+  return C == 4 ? 16 : (C == 8 ? 8 : 4);
+}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+template <int C>
 __device__ __forceinline__ void scan_issue(const float* g, const float* in, float* ring, int tile, int slot,
                                            int T, int H, int c0, int lw, int lane) {
-  // loader wave lw (0..3) issues chunks lw*4 .. lw*4+3 of this tile (8 per array)
+  constexpr int TA = kScTT * C / 256;  // transfers per array per tile
+  constexpr int LPW = 2 * TA / 4;      // transfers per loader wave per tile
+  constexpr int SPT = 256 / C;         // steps per transfer
+  constexpr int LPR = C / 4;           // lanes per step row
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = lw * 4 + i, arr = idx >> 3, q = idx & 7;
-    int t = tile * kScTT + 16 * q + (lane >> 2);
+  for (int i = 0; i < LPW; ++i) {
+    const int idx = lw * LPW + i, arr = idx / TA, q = idx % TA;
+    int t = tile * kScTT + SPT * q + lane / LPR;
     t = t < T ? t : T - 1;
-    const float* src = (arr ? in : g) + static_cast<size_t>(t) * H + c0 + 4 * (lane & 3);
-    float* dst = ring + ((slot * 2 + arr) * kScTT + 16 * q) * kScCols;
+    const float* src = (arr ? in : g) + static_cast<size_t>(t) * H + c0 + 4 * (lane % LPR);
+    float* dst = ring + ((slot * 2 + arr) * kScTT + SPT * q) * C;
     __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
   }
 }
 
-// GATE: g and in are the raw f and i projections. The six non-chain waves apply the gate
-// math (sigmoid, lower bound, swiglu; hgrn_model.cpp:113-124, the same functions as k_gate)
-// to each tile in LDS one iteration before the chain wave reads it, so the gated values
-// never go through memory. Tile k + 1 must then be complete at the barrier of iteration k
-// (one tile less in flight), and an extra first iteration converts tile 0. Element tail
-// rules do not arise: this kernel requires H % 16 == 0.
-template <bool GATE>
+// GATE: g and in are the raw f and i projections, and the conversion applies the gate math
+// (sigmoid, lower bound, swiglu; hgrn_model.cpp:113-124, the same functions as k_gate), so
+// the gated values never go through memory. Element tail rules do not arise: this kernel
+// requires H % 16 == 0.
+//
+// Each iteration k: the loaders issue the transfers of tile k + kScNR - 1; the fifteen
+// non-chain waves convert tile k + 1 from the ring (step-major, as loaded) into
+// column-major rows GT / IT (one per column, kScTT + 36 floats apart); wave 0 chains tile k
+// from its column's rows, four steps per LDS read, into column-major results RT; the store
+// waves write tile k - 1's results back step-major, a float4 (4 columns of one step) per
+// thread. Tile k + 1 must then be in LDS at the barrier of iteration k, and an extra first
+// iteration converts tile 0.
+template <bool GATE, int C, int kScNR = scan_ring_depth<C>()>
 __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __restrict__ g, const float* __restrict__ in,
                                                              const float* __restrict__ lb, float* __restrict__ recur,
                                                              float* __restrict__ state, int T, int H) {
+  static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 columns per block");
+  static_assert((64 * (kScWaves - 1)) % C == 0, "a converting lane keeps its column");
+  static_assert((kScNR - 2) * kScTT * C / 512 < 64, "outstanding transfers per loader wave");
+  constexpr int LPW = kScTT * C / 512;  // transfers per loader wave per tile
+  constexpr int LPR = C / 4;            // float4 per step row
+  constexpr int LT = kScTT + 36;  // column row: the tile, the chain's reads ahead, no bank conflicts
   extern __shared__ __align__(16) float sm[];
-  float* ring = sm;                                      // [kScNR][2][kScTT][16]
-  float* R = sm + kScNR * 2 * kScTT * kScCols;           // [2][kScTT][16]
+  float* ring = sm;                        // [kScNR][2][kScTT][C], as loaded
+  float* GT = ring + kScNR * 2 * kScTT * C;  // [2][C][LT] converted g (tile parity)
+  float* IT = GT + 2 * C * LT;             // [2][C][LT] converted in
+  float* RT = IT + 2 * C * LT;             // [2][C][LT] results
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c0 = blockIdx.x * kScCols;
+  // column group: XCD-contiguous when the groups split evenly over the 8 XCDs
+  const int ngrp = H / C, b = blockIdx.x;
+  const int grp = (ngrp % 8 == 0) ? (b & 7) * (ngrp / 8) + (b >> 3) : b;
+  const int c0 = grp * C;
   const int ntiles = (T + kScTT - 1) / kScTT;
   const bool loader = wave >= 1 && wave <= 4;
-  float s = (wave == 0 && lane < kScCols) ? state[c0 + lane] : 0.0f;
-  // GATE: the column a gate lane converts is fixed (384 lanes, 16 columns per tile row)
-  const float lbc = (GATE && wave >= 1 && lb) ? lb[c0 + (threadIdx.x - 64) % kScCols] : 0.0f;
+  const bool storer = wave >= kScWaves - kScStoreWaves;
+  float s = (wave == 0 && lane < C) ? state[c0 + lane] : 0.0f;
+  // the chain is the block's critical path: its instructions issue ahead of the conversion
+  // sharing its SIMD
+  if (wave == 0) __builtin_amdgcn_s_setprio(3);
+  // the column a converting lane handles is fixed (64 x 15 lanes, C columns per step row)
+  const int ccol = (threadIdx.x - 64) % C;
+  const float lbc = (GATE && wave >= 1 && lb) ? lb[c0 + ccol] : 0.0f;
   if (loader)
-    for (int t = 0; t < kScNR - 1 && t < ntiles; ++t) scan_issue(g, in, ring, t, t, T, H, c0, wave - 1, lane);
-  for (int k = GATE ? -1 : 0; k <= ntiles; ++k) {
-    // this wave's LDS writes (wave 0's results, converted gates) have landed before the
-    // barrier publishes them
+    for (int t = 0; t < kScNR - 1 && t < ntiles; ++t) scan_issue<C>(g, in, ring, t, t, T, H, c0, wave - 1, lane);
+  for (int k = -1; k <= ntiles; ++k) {
+    // this wave's LDS writes (results, converted tiles) have landed before the barrier
+    // publishes them
     __builtin_amdgcn_s_waitcnt(0xC07F);
     if (loader) {
-      // this wave's transfers of tile k (GATE: k + 1) are done once only later tiles' are
-      // outstanding
-      if (GATE) {
-        if (k >= 0 && k + kScNR - 2 < ntiles)
-          __builtin_amdgcn_s_waitcnt(((kScNR - 3) * 4 & 0xF) | (((kScNR - 3) * 4 >> 4) << 14) | 0x0F70);
-        else
-          __builtin_amdgcn_s_waitcnt(0x0F70);
-      } else {
-        if (k + kScNR - 2 < ntiles)
-          __builtin_amdgcn_s_waitcnt(((kScNR - 2) * 4 & 0xF) | (((kScNR - 2) * 4 >> 4) << 14) | 0x0F70);
-        else
-          __builtin_amdgcn_s_waitcnt(0x0F70);
-      }
+      // this wave's transfers of tile k + 1 are done once only later tiles' are outstanding
+      if (k >= 0 && k + kScNR - 2 < ntiles)
+        __builtin_amdgcn_s_waitcnt(((kScNR - 3) * LPW & 0xF) | (((kScNR - 3) * LPW >> 4) << 14) | 0x0F70);
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
     }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (loader && k >= 0 && k + kScNR - 1 < ntiles)
-      scan_issue(g, in, ring, k + kScNR - 1, (k + kScNR - 1) % kScNR, T, H, c0, wave - 1, lane);
-    if (GATE && wave >= 1 && k + 1 < ntiles) {
-      // gate math on tile k + 1, in place: g' = sigmoid(f) (then the lower bound), in =
-      // swiglu(i, 1 - g')
-      float* Gt = ring + (((k + 1) % kScNR) * 2 + 0) * kScTT * kScCols;
-      float* It = ring + (((k + 1) % kScNR) * 2 + 1) * kScTT * kScCols;
-      for (int e = threadIdx.x - 64; e < kScTT * kScCols; e += 64 * (kScWaves - 1)) {
-        float gg = sigmoid_of(Gt[e], false);
-        if (lb) gg = __builtin_fmaf(1.0f - lbc, gg, lbc);
-        It[e] = swiglu_of(It[e], 1.0f - gg, false);
-        Gt[e] = gg;
+      scan_issue<C>(g, in, ring, k + kScNR - 1, (k + kScNR - 1) % kScNR, T, H, c0, wave - 1, lane);
+    if (wave >= 1 && k + 1 < ntiles) {
+      // tile k + 1 into column-major rows (GATE: g' = sigmoid(f), then the lower bound;
+      // in' = swiglu(i, 1 - g'))
+      const float* Gr = ring + (((k + 1) % kScNR) * 2 + 0) * kScTT * C;
+      const float* Ir = ring + (((k + 1) % kScNR) * 2 + 1) * kScTT * C;
+      float* Gc = GT + ((k + 1) & 1) * C * LT + ccol * LT;
+      float* Ic = IT + ((k + 1) & 1) * C * LT + ccol * LT;
+      const int n = min(kScTT, T - (k + 1) * kScTT);
+      for (int e = threadIdx.x - 64; e < n * C; e += 64 * (kScWaves - 1)) {
+        float gg = Gr[e], ii = Ir[e];
+        if (GATE) {
+          gg = sigmoid_of(gg, false);
+          if (lb) gg = __builtin_fmaf(1.0f - lbc, gg, lbc);
+          ii = swiglu_of(ii, 1.0f - gg, false);
+        }
+        const int st = e / C;
+        Gc[st] = gg;
+        Ic[st] = ii;
       }
     }
-    if (wave == 0 && k >= 0 && k < ntiles && lane < kScCols) {
-      const float* G = ring + ((k % kScNR) * 2 + 0) * kScTT * kScCols;
-      const float* I = ring + ((k % kScNR) * 2 + 1) * kScTT * kScCols;
-      float* Rt = R + (k & 1) * kScTT * kScCols;
+    if (wave == 0 && k >= 0 && k < ntiles && lane < C) {
+      const float* Gc = GT + (k & 1) * C * LT + lane * LT;
+      const float* Ic = IT + (k & 1) * C * LT + lane * LT;
+      float* Rc = RT + (k & 1) * C * LT + lane * LT;
       const int n = min(kScTT, T - k * kScTT);
-      if (n == kScTT) {
-        // whole tile: the operands of the next 8 steps are read while the current 8 are
-        // chained (reads past the tile's end stay inside the ring and are not used)
-        float gv[8], iv[8], gn[8], in8[8];
+      // four steps per read, eight reads ahead (32 steps, longer than an LDS round trip):
+      // group u of a round of 32 steps is read in the round before. The rows are padded so
+      // that the reads ahead of the last round stay inside them (and are not used); the
+      // steps past the last whole round go one at a time.
+      const int nr = n & ~31;
+      float4 gq[8], iq[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        gq[u] = *reinterpret_cast<const float4*>(Gc + 4 * u);
+        iq[u] = *reinterpret_cast<const float4*>(Ic + 4 * u);
+      }
+      for (int t = 0; t < nr; t += 32) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          gv[u] = G[u * kScCols + lane];
-          iv[u] = I[u * kScCols + lane];
-        }
-        for (int t = 0; t < kScTT; t += 8) {
-          const int tn = t + 8 < kScTT ? t + 8 : t;
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            gn[u] = G[(tn + u) * kScCols + lane];
-            in8[u] = I[(tn + u) * kScCols + lane];
-          }
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            s = __builtin_fmaf(gv[u], s, iv[u]);
-            Rt[(t + u) * kScCols + lane] = s;
-          }
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            gv[u] = gn[u];
-            iv[u] = in8[u];
-          }
-        }
-      } else {
-        for (int t = 0; t < n; ++t) {
-          s = __builtin_fmaf(G[t * kScCols + lane], s, I[t * kScCols + lane]);
-          Rt[t * kScCols + lane] = s;
+          const float4 gv = gq[u], iv = iq[u];
+          gq[u] = *reinterpret_cast<const float4*>(Gc + t + 32 + 4 * u);
+          iq[u] = *reinterpret_cast<const float4*>(Ic + t + 32 + 4 * u);
+          float4 r;
+          s = __builtin_fmaf(gv.x, s, iv.x);
+          r.x = s;
+          s = __builtin_fmaf(gv.y, s, iv.y);
+          r.y = s;
+          s = __builtin_fmaf(gv.z, s, iv.z);
+          r.z = s;
+          s = __builtin_fmaf(gv.w, s, iv.w);
+          r.w = s;
+          *reinterpret_cast<float4*>(Rc + t + 4 * u) = r;
         }
       }
+      for (int t = nr; t < n; ++t) {
+        s = __builtin_fmaf(Gc[t], s, Ic[t]);
+        Rc[t] = s;
+      }
     }
-    if (wave >= 5 && k >= 1) {
-      // results of tile k - 1 to global memory, a float4 (4 columns of one step) per thread
-      const float* Rp = R + ((k - 1) & 1) * kScTT * kScCols;
+    if (storer && k >= 1) {
+      // results of tile k - 1 to global memory, step-major, a float4 per thread
+      const float* Rp = RT + ((k - 1) & 1) * C * LT;
       const int n = min(kScTT, T - (k - 1) * kScTT);
-      for (int f = threadIdx.x - 320; f < kScTT * kScCols / 4; f += 128) {
-        const int row = f >> 2, c4 = f & 3;
-        if (row < n)
-          *reinterpret_cast<float4*>(recur + static_cast<size_t>((k - 1) * kScTT + row) * H + c0 + 4 * c4) =
-              *reinterpret_cast<const float4*>(Rp + row * kScCols + 4 * c4);
+      for (int f = threadIdx.x - 64 * (kScWaves - kScStoreWaves); f < n * LPR; f += 64 * kScStoreWaves) {
+        const int row = f / LPR, c4 = f % LPR;
+        const float4 v = make_float4(Rp[(4 * c4) * LT + row], Rp[(4 * c4 + 1) * LT + row], Rp[(4 * c4 + 2) * LT + row],
+                                     Rp[(4 * c4 + 3) * LT + row]);
+        *reinterpret_cast<float4*>(recur + static_cast<size_t>((k - 1) * kScTT + row) * H + c0 + 4 * c4) = v;
       }
     }
   }
-  if (wave == 0 && lane < kScCols) state[c0 + lane] = s;
+  if (wave == 0 && lane < C) state[c0 + lane] = s;
 }
 
 __global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict__ ids,
@@ -1508,14 +1545,27 @@ hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   }
 }
 
+// Columns per k_scan_ring block: 16 (a 64-byte line per step row per block).
+template <bool GATE>
+static hipError_t scan_ring_launch(const float* g, const float* in, const float* lb, float* recur, float* state,
+                                   int rows, int H, hipStream_t s) {
+  auto go = [&](auto cc) {
+    constexpr int C = decltype(cc)::value;
+    const size_t lds =
+        (static_cast<size_t>(scan_ring_depth<C>()) * 2 * kScTT * C + 6 * static_cast<size_t>(C) * (kScTT + 36)) *
+        sizeof(float);
+    k_scan_ring<GATE, C><<<H / C, 64 * kScWaves, lds, s>>>(g, in, lb, recur, state, rows, H);
+    return hipGetLastError();
+  };
+  return go(std::integral_constant<int, 16>{});
+}
+
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
                         const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s) {
-  if (!stream_state && !keep_gates && rows > 1 && H % kScCols == 0 &&
+  if (!stream_state && !keep_gates && rows > 1 && H % 16 == 0 &&
       ((reinterpret_cast<uintptr_t>(i) | reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(recur)) & 15) == 0) {
-    // one kernel: the gate math runs inside the scan on each tile (k_scan_ring<true>)
-    const size_t lds = (static_cast<size_t>(kScNR) * 2 + 2) * kScTT * kScCols * sizeof(float);
-    k_scan_ring<true><<<H / kScCols, 64 * kScWaves, lds, s>>>(f, i, lb, recur, state, rows, H);
-    return hipGetLastError();
+    // one kernel: the gate math runs inside the scan on each tile (k_scan_ring<true, C>)
+    return scan_ring_launch<true>(f, i, lb, recur, state, rows, H, s);
   }
   if (!stream_state && scan_out && rows > 1) {
     const size_t n = static_cast<size_t>(rows) * H;
@@ -1525,9 +1575,8 @@ hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur,
     if (e != hipSuccess) return e;
     const bool aligned = ((reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(scan_out) |
                            reinterpret_cast<uintptr_t>(recur)) & 15) == 0;
-    if (H % kScCols == 0 && aligned) {
-      const size_t lds = (static_cast<size_t>(kScNR) * 2 + 2) * kScTT * kScCols * sizeof(float);
-      k_scan_ring<false><<<H / kScCols, 64 * kScWaves, lds, s>>>(f, scan_out, nullptr, recur, state, rows, H);
+    if (H % 16 == 0 && aligned) {
+      return scan_ring_launch<false>(f, scan_out, nullptr, recur, state, rows, H, s);
     } else {
       k_scan_seq<<<(H + 63) / 64, 64, 0, s>>>(f, scan_out, recur, state, rows, H);
     }
