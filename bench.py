@@ -385,6 +385,8 @@ def main():
     ap.add_argument("--vendor-int8", default=None, metavar="T,H,I",
                     help="only time the vendor int8 GEMM on one prefill layer's shapes (child process)")
     ap.add_argument("--cpu-leg", default=None, help="run one CPU baseline job (child process)")
+    ap.add_argument("--decode-modes", default="float,fixed",
+                    help="comma list of float,fixed: the batch-1 decode modes timed (float always runs: it carries the headline)")
     args = ap.parse_args()
     if args.cpu_leg:
         cpu_leg(args.cpu_leg)
@@ -406,6 +408,8 @@ def main():
     peaks = eng.measure_peaks()
     log(f"[bench] measured ceilings: {peaks}")
     shapes = [s.strip() for s in args.shapes.split(",") if s.strip()]
+    dm = {x.strip() for x in args.decode_modes.split(",")}
+    decode_modes = {FLOAT: True, FIXED_Q510: "fixed" in dm}
     if "370M" not in shapes:
         shapes.insert(0, "370M")
     results = {}
@@ -415,7 +419,7 @@ def main():
     for name in shapes:
         preset = SHAPES[name]
         p = blob_path(args.blob_dir, preset)
-        for mode in (FLOAT, FIXED_Q510):
+        for mode in [m for m in (FLOAT, FIXED_Q510) if decode_modes[m]]:
             t = time.time()
             eng.close()
             eng = Engine(0)
