@@ -36,6 +36,19 @@ template <> struct KindTraits<kLM> { static constexpr int NM = 1, NA = 1, NP = 3
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// Lane l's segment of a chain-transposed vector of chain length 32 RC: floats
+// [4 RC l, 4 RC (l + 1)), i.e. segment l % 8 of chain l / 8, plus the 8 tail floats after
+// the 8 rows (the same for every lane).
+template <int RC>
+__device__ __forceinline__ void load_seg(const float* p, int l, float4 (&d)[RC], float (&t)[8]) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int c = 0; c < RC; ++c) d[c] = q[l * RC + c];
+  const float4 t0 = q[64 * RC], t1 = q[64 * RC + 1];
+  t[0] = t0.x; t[1] = t0.y; t[2] = t0.z; t[3] = t0.w;
+  t[4] = t1.x; t[5] = t1.y; t[6] = t1.z; t[7] = t1.w;
+}
+
 // A block is KS parts of NM * 128 threads. In every part, thread (mi, ol, j) sums chain j of
 // output ol of the block's group for matrix mi. What the parts do:
 //   kLM             part p takes the block's p-th output group (the groups a block strides
@@ -44,7 +57,15 @@ typedef __attribute__((address_space(3))) void lds_void;
 //                   partials meet in LDS (integer sums do not depend on their order);
 //   float           only part 0 runs the GEMV (a chain is one reference lane, in order); the
 //                   other parts share the loads, the normalisation and the encoding.
-template <int MODE, int KIND, int NV, int KS>
+//
+// RC > 0 (the chain length Lc is 32 RC, no row padding): wave 0 runs both norm chains from
+// registers. Lane 8j + s holds segment s (4 RC consecutive steps) of chain j of the input
+// row and of the stage-1 weights; each chain runs segment by segment, every lane summing its
+// own segment and a DPP row shift handing the running sum to the next segment's lane, so a
+// step costs one dependent FMA (about 6.4 cycles) instead of an LDS round trip. Wave 0 then
+// writes the stage-1 output to LDS for the encoding pass; the row norm needs no barrier of
+// its own. RC == 0 runs the same chains over LDS rows (any Lc).
+template <int MODE, int KIND, int NV, int KS, int RC>
 __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(DecArgs a) {
   constexpr int NM = KindTraits<KIND>::NM, NA = KindTraits<KIND>::NA, NP = KindTraits<KIND>::NP;
   constexpr int BM = kBlock * NM;  // threads of one part
@@ -177,9 +198,24 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   if (KIND == kO) { src[1] = ax2; src[2] = apre; src[3] = nw0; }
   if (KIND == kGate || KIND == kLM) { src[1] = apre; src[2] = nw0; }
   if (KIND == kDown) { src[1] = nw0; }
+  constexpr int NW0 = NP - NA;              // first BitLinear norm-weight source
+  constexpr int PW = (KIND == kO) ? 2 : 1;  // which source holds the stage-1 weight
+  // RC > 0: wave 0 loads its segments of the input row, the stage-1 weight and kO's gate first
+  constexpr int RX = RC > 0 ? RC : 1;
+  float4 xs[RX], ws[RX], gs[RX];
+  float xt[8], wt[8], gt[8];
+  if constexpr (RC > 0) {
+    if (tid < 64) {
+      load_seg<RC>(src[0], tid, xs, xt);
+      if constexpr (KIND != kDown) load_seg<RC>(src[PW], tid, ws, wt);
+      if constexpr (KIND == kO) load_seg<RC>(src[1], tid, gs, gt);
+    }
+  }
+  // the rest in the block layout (RC > 0: only the BitLinear norm weights)
+  constexpr int S0 = RC > 0 ? NW0 : 0;
   float4 v[NP][NV];
 #pragma unroll
-  for (int s = 0; s < NP; ++s)
+  for (int s = S0; s < NP; ++s)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = tid + i * BS;
@@ -208,47 +244,83 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
     const int jj = p / Lc;
     li[i] = (p < 8 * Lc) ? (jj * LS + (p - jj * Lc)) / 4 : (8 * LS + (p - 8 * Lc)) / 4;
   }
+  float r2;
+  if constexpr (RC > 0) {
+    // ---- both norm chains on wave 0, from registers (no barrier until the row is in LDS) ----
+    if (tid < 64) {
+      if constexpr (KIND != kDown) {
+        const float r1 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int e = tid + i * BS;
-    if (e < W4) {
-      reinterpret_cast<float4*>(X)[li[i]] = v[0][i];
-      if (KIND == kO) reinterpret_cast<float4*>(S)[li[i]] = v[1][i];
+        for (int c = 0; c < RC; ++c) {
+          float4 x = xs[c];
+          const float4 w = ws[c];
+          x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
+          if (KIND == kO) {
+            const float4 sg = gs[c];
+            x.x = x.x * sg.x; x.y = x.y * sg.y; x.z = x.z * sg.z; x.w = x.w * sg.w;
+          }
+          xs[c] = x;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          xt[t] = (xt[t] * r1) * wt[t];
+          if (KIND == kO) xt[t] = xt[t] * gt[t];
+        }
+      }
+      const float ss2 = seg_sumsq<RC>(xs, xt, nt);
+      // the stage-1 output into the LDS rows: lane 8j + s -> row j, floats [4 RC s, 4 RC (s + 1))
+      float4* xr = reinterpret_cast<float4*>(X + (tid >> 3) * LS + 4 * RC * (tid & 7));
+#pragma unroll
+      for (int c = 0; c < RC; ++c) xr[c] = xs[c];
+      if (tid == 0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) X[8 * LS + t] = xt[t];
+        red[0] = rstd_of(ss2, gK, aeps);
+      }
     }
-  }
-  for (int z = tid; z < 8 * (L32 - Lc); z += BS) {  // zeros past Lc in each row
-    const int jj = z / (L32 - Lc);
-    X[jj * LS + Lc + (z - jj * (L32 - Lc))] = 0.0f;
-  }
-  __syncthreads();
-
-  // ---- stage 1: the kernel's own pre-norm -------------------------------------------------
-  if (KIND != kDown) {
-    chain_begin(X, Lc, LS, red);
     __syncthreads();
-    const float r1 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
-    constexpr int PW = (KIND == kO) ? 2 : 1;  // which source holds the stage-1 weight
+    r2 = red[0];
+  } else {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = tid + i * BS;
       if (e < W4) {
-        float4 x = reinterpret_cast<float4*>(X)[li[i]];
-        const float4 w = v[PW][i];
-        x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
-        if (KIND == kO) {
-          const float4 sg = reinterpret_cast<float4*>(S)[li[i]];
-          x.x = x.x * sg.x; x.y = x.y * sg.y; x.z = x.z * sg.z; x.w = x.w * sg.w;
-        }
-        reinterpret_cast<float4*>(X)[li[i]] = x;
+        reinterpret_cast<float4*>(X)[li[i]] = v[0][i];
+        if (KIND == kO) reinterpret_cast<float4*>(S)[li[i]] = v[1][i];
       }
     }
+    for (int z = tid; z < 8 * (L32 - Lc); z += BS) {  // zeros past Lc in each row
+      const int jj = z / (L32 - Lc);
+      X[jj * LS + Lc + (z - jj * (L32 - Lc))] = 0.0f;
+    }
     __syncthreads();
+    // ---- stage 1: the kernel's own pre-norm -----------------------------------------------
+    if (KIND != kDown) {
+      chain_begin(X, Lc, LS, red);
+      __syncthreads();
+      const float r1 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = tid + i * BS;
+        if (e < W4) {
+          float4 x = reinterpret_cast<float4*>(X)[li[i]];
+          const float4 w = v[PW][i];
+          x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
+          if (KIND == kO) {
+            const float4 sg = reinterpret_cast<float4*>(S)[li[i]];
+            x.x = x.x * sg.x; x.y = x.y * sg.y; x.z = x.z * sg.z; x.w = x.w * sg.w;
+          }
+          reinterpret_cast<float4*>(X)[li[i]] = x;
+        }
+      }
+      __syncthreads();
+    }
+    // ---- stage 2: BitLinear RMSNorm -------------------------------------------------------
+    chain_begin(X, Lc, LS, red);
+    __syncthreads();
+    r2 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
   }
-  // ---- stage 2: BitLinear RMSNorm, activation encoding ------------------------------------
-  chain_begin(X, Lc, LS, red);
-  __syncthreads();
-  const float r2 = rstd_of(chain_end(X, LS, nt, red), gK, aeps);
-  constexpr int NW0 = NP - NA;  // first norm-weight source
+  // ---- activation encoding -------------------------------------------------------------------
 #pragma unroll
   for (int aa = 0; aa < NA; ++aa) {
     if (MODE == kFloat) {
@@ -507,14 +579,43 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 template <int MODE, int KIND>
 constexpr int kParts = (MODE == kFloat) ? 1 : ((KIND == kO || KIND == kDown) ? 4 : 2);
 
+constexpr int nv_for(int W4, int BS) { return W4 <= 2 * BS ? 2 : (W4 <= 4 * BS ? 4 : (W4 <= 8 * BS ? 8 : 16)); }
+
+template <int MODE, int KIND, int KS, int RC>
+hipError_t dec_rc(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
+  constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
+  constexpr int W4 = (8 * 32 * RC + 8) / 4;
+  static_assert(W4 <= 16 * BS, "row too long for the block layout");
+  k_decode<MODE, KIND, nv_for(W4, BS), KS, RC><<<grid, BS, lds, s>>>(a);
+  return hipGetLastError();
+}
+
 template <int MODE, int KIND, int KS>
 hipError_t dec_ks(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
   constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
-  const int W4 = (8 * a.p[0].g.Lc + 8) / 4;
-  if (W4 <= 2 * BS) k_decode<MODE, KIND, 2, KS><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 4 * BS) k_decode<MODE, KIND, 4, KS><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 8 * BS) k_decode<MODE, KIND, 8, KS><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 16 * BS) k_decode<MODE, KIND, 16, KS><<<grid, BS, lds, s>>>(a);
+  const int Lc = a.p[0].g.Lc;
+  if (Lc % 32 == 0) {  // register chains at the model widths: H 1024/2048/2560, I 2816/5632/6912
+    if constexpr (KIND == kDown) {
+      switch (Lc / 32) {
+        case 11: return dec_rc<MODE, KIND, KS, 11>(a, lds, grid, s);
+        case 22: return dec_rc<MODE, KIND, KS, 22>(a, lds, grid, s);
+        case 27: return dec_rc<MODE, KIND, KS, 27>(a, lds, grid, s);
+        default: break;
+      }
+    } else {
+      switch (Lc / 32) {
+        case 4: return dec_rc<MODE, KIND, KS, 4>(a, lds, grid, s);
+        case 8: return dec_rc<MODE, KIND, KS, 8>(a, lds, grid, s);
+        case 10: return dec_rc<MODE, KIND, KS, 10>(a, lds, grid, s);
+        default: break;
+      }
+    }
+  }
+  const int W4 = (8 * Lc + 8) / 4;
+  if (W4 <= 2 * BS) k_decode<MODE, KIND, 2, KS, 0><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 4 * BS) k_decode<MODE, KIND, 4, KS, 0><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 8 * BS) k_decode<MODE, KIND, 8, KS, 0><<<grid, BS, lds, s>>>(a);
+  else if (W4 <= 16 * BS) k_decode<MODE, KIND, 16, KS, 0><<<grid, BS, lds, s>>>(a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

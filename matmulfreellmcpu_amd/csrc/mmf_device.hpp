@@ -120,6 +120,38 @@ __device__ inline float chain_end(const float* X, int LS, int nt, const float* r
   return s;
 }
 
+// The same sums from registers across one wave: lane 8j + s holds steps [4 RC s, 4 RC (s+1))
+// of chain j in v. Segment s of every chain is summed in round s, and a DPP row shift by
+// one lane (within rows of 16 lanes, so never across chains j) hands each running sum to
+// the lane of the next segment; after round 7 lane 8j + 7 holds chain j. Lanes outside
+// their round sum data that the next shift overwrites. Returns hsum_ps of the 8 chains plus
+// the tail tv[0..nt) (uniform over the wave). Call from all 64 lanes of one wave.
+template <int RC>
+__device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&tv)[8], int nt) {
+  float a = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      a = __builtin_fmaf(v[c].x, v[c].x, a);
+      a = __builtin_fmaf(v[c].y, v[c].y, a);
+      a = __builtin_fmaf(v[c].z, v[c].z, a);
+      a = __builtin_fmaf(v[c].w, v[c].w, a);
+    }
+    if (s < 7)
+      a = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x111 /* row_shr:1 */,
+                                                                  0xf, 0xf, false));
+  }
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) p[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 8 * j + 7));
+  float s = hsum8(p);
+#pragma unroll
+  for (int t = 0; t < 7; ++t)
+    if (t < nt) s = __builtin_fmaf(tv[t], tv[t], s);
+  return s;
+}
+
 // ---- Cephes exp (simd.hpp:212-249) ----------------------------------------------------
 constexpr float kExpHi = 88.3762626647949f;
 constexpr float kExpLo = -88.3762626647949f;
