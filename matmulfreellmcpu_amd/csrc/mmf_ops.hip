@@ -393,6 +393,9 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   for (int t = nt + tid; t < 8; t += BT) X[8 * LS + t] = 0.0f;
   __syncthreads();
 
+  // the chain wave (wave 0) issues ahead of the other rows' waves on its SIMD until both
+  // norms are known
+  if (tid < 64) __builtin_amdgcn_s_setprio(3);
   if (PRE != kPreNone) {
     const float r1 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
 #pragma unroll
@@ -430,6 +433,7 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   };
   load_w(0, 0);
   const float r2 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
+  if (tid < 64) __builtin_amdgcn_s_setprio(0);
 
   // the BitLinear norm of unit g: y = (x * rstd) * normw (bitlinear.cpp:62-70)
   auto unit_y = [&](int ai, int g, float* y) {

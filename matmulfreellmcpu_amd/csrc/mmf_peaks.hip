@@ -1,6 +1,7 @@
 // mmf_peaks.hip -- device calibration for the rooflines. Each kernel does one kind of work
 // and nothing else, so its rate is the sustained ceiling of that resource on this device:
-//   - HBM read: a 2 GiB buffer (far beyond the 256 MB Infinity Cache) read once per pass;
+//   - HBM read: a 2 GiB buffer (far beyond the 256 MB Infinity Cache) read once per pass,
+//     nontemporal, in contiguous per-block chunks;
 //   - Infinity Cache (MALL) read: a 128 MiB buffer (beyond the 8 x 4 MB of L2, within the
 //     MALL) read repeatedly;
 //   - int8 matrix cores: independent v_mfma_i32_32x32x32_i8 on register operands;
@@ -18,17 +19,29 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Grid-stride float4 reads of n4 elements, `passes` times; each thread's sum is stored so
-// the loads cannot be dropped.
+// Reads of n4 float4 elements, `passes` times: each pass a block reads one contiguous chunk
+// (n4 / gridDim.x elements, a multiple of 2048), eight 16-byte loads in flight per thread;
+// NT marks them nontemporal (streamed past the caches: the HBM pass). Each thread's sum is
+// stored so the loads cannot be dropped.
+template <bool NT>
 __global__ __launch_bounds__(256) void k_peak_read(const float4* __restrict__ p, size_t n4, int passes,
                                                    float* __restrict__ sink) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  constexpr int U = 8;
   float acc = 0.0f;
-  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  const size_t per = n4 / gridDim.x;
   for (int r = 0; r < passes; ++r) {
-#pragma unroll 8
-    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n4; i += stride) {
-      const float4 v = p[i];
-      acc += (v.x + v.y) + (v.z + v.w);
+    // pass r reads the chunk gridDim.x / 8 blocks further on (the same XCD under round-robin
+    // dispatch, so a chunk is re-read only after the XCD's L2 has seen the whole buffer's
+    // eighth)
+    const size_t c = (blockIdx.x + static_cast<size_t>(r) * (gridDim.x / 8)) % gridDim.x;
+    const f4v* q = reinterpret_cast<const f4v*>(p) + c * per;
+    for (size_t i = threadIdx.x; i < per; i += 256 * U) {
+      f4v v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = NT ? __builtin_nontemporal_load(q + i + u * 256) : q[i + u * 256];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
     }
   }
   sink[blockIdx.x * blockDim.x + threadIdx.x] = acc;
@@ -66,7 +79,7 @@ __global__ __launch_bounds__(256) void k_peak_fma(int iters, float x, float* __r
   sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Milliseconds of the fastest of `reps` timed runs of f (after one untimed run).
+// Milliseconds of the fastest of `reps` timed runs of f (after two untimed runs).
 template <class F>
 float best_ms(hipStream_t s, int reps, F f) {
   hipEvent_t e0, e1;
@@ -76,6 +89,7 @@ float best_ms(hipStream_t s, int reps, F f) {
     return -1.0f;
   }
   float best = -1.0f;
+  f();
   f();
   for (int r = 0; r < reps; ++r) {
     if (hipEventRecord(e0, s) != hipSuccess) break;
@@ -95,7 +109,10 @@ float best_ms(hipStream_t s, int reps, F f) {
 hipError_t measure_peaks(int cus, hipStream_t s, double out[4]) {
   constexpr size_t kHbm = size_t(2) << 30, kMall = size_t(128) << 20;
   constexpr int kMallPasses = 8;
-  const int blocks = 8 * (cus > 0 ? cus : 256);
+  // 4096 blocks: chunks of 32768 (HBM) and 2048 (MALL) float4, whole multiples of a block's
+  // 2048-element step
+  constexpr int blocks = 4096;
+  static_assert((kHbm / 16) % (blocks * 2048) == 0 && (kMall / 16) % (blocks * 2048) == 0, "whole steps");
   void* buf = nullptr;
   float* sink = nullptr;
   hipError_t e = hipMalloc(&buf, kHbm);
@@ -108,9 +125,9 @@ hipError_t measure_peaks(int cus, hipStream_t s, double out[4]) {
   e = hipMemsetAsync(buf, 0, kHbm, s);
   const float4* p = static_cast<const float4*>(buf);
   if (e == hipSuccess) {
-    const float ms = best_ms(s, 5, [&] { k_peak_read<<<blocks, 256, 0, s>>>(p, kHbm / 16, 1, sink); });
+    const float ms = best_ms(s, 10, [&] { k_peak_read<true><<<blocks, 256, 0, s>>>(p, kHbm / 16, 1, sink); });
     out[0] = ms > 0.0f ? kHbm / (ms * 1e-3) / 1e9 : 0.0;
-    const float mm = best_ms(s, 5, [&] { k_peak_read<<<blocks, 256, 0, s>>>(p, kMall / 16, kMallPasses, sink); });
+    const float mm = best_ms(s, 5, [&] { k_peak_read<false><<<blocks, 256, 0, s>>>(p, kMall / 16, kMallPasses, sink); });
     out[1] = mm > 0.0f ? static_cast<double>(kMall) * kMallPasses / (mm * 1e-3) / 1e9 : 0.0;
     constexpr int kIters = 4096;
     const int mb = 2 * (cus > 0 ? cus : 256);  // two 4-wave blocks per CU: two waves per SIMD
