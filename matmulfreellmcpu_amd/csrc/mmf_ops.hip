@@ -1070,13 +1070,15 @@ __global__ void k_gather_rows(const float* __restrict__ x, const int* __restrict
 // direct global-to-LDS DMA (lane l's 16 bytes land at LDS base + 16 l: 256 / C steps x C
 // columns per transfer); all fifteen other waves convert each tile into column-major rows
 // for the chain, and the last four store the previous tile's results. One barrier per
-// tile. (Launches use C = 16, one 64-byte line per step row: narrower blocks shared lines
-// between blocks and measured twice as slow at 2048 x 2048.) The column groups of one
-// line go to blocks of the same XCD (blocks are dealt to the 8 XCDs round-robin).
+// tile. (Launches use C = 8: at 2048 x 2048 a tile iteration takes about 1.2 us, set by the
+// chain wave; 16 columns per block, half the blocks, measured 5% slower and 4 columns per
+// block 40% slower.) The column groups of one line go to blocks of the same XCD (blocks
+// are dealt to the 8 XCDs round-robin).
 constexpr int kScTT = 128;
 constexpr int kScWaves = 16, kScStoreWaves = 4;  // the last kScStoreWaves waves store
+constexpr int kScSets = 3;  // register sets of the chain's 8-step groups
 // Ring depth (tiles): the loads of a tile are in flight for NR - 2 tiles of chain work
-// (about 1.5 us each at C = 16).
+// (about 1.2 us each).
 template <int C>
 constexpr int scan_ring_depth() {
   return C == 4 ? 16 : (C == 8 ? 8 : 4);
@@ -1123,7 +1125,7 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
   static_assert((kScNR - 2) * kScTT * C / 512 < 64, "outstanding transfers per loader wave");
   constexpr int LPW = kScTT * C / 512;  // transfers per loader wave per tile
   constexpr int LPR = C / 4;            // float4 per step row
-  constexpr int LT = kScTT + 36;  // column row: the tile, the chain's reads ahead, no bank conflicts
+  constexpr int LT = kScTT + 36;  // column row: the tile and a pad against bank conflicts
   extern __shared__ __align__(16) float sm[];
   float* ring = sm;                        // [kScNR][2][kScTT][C], as loaded
   float* GT = ring + kScNR * 2 * kScTT * C;  // [2][C][LT] converted g (tile parity)
@@ -1186,38 +1188,60 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
       const float* Ic = IT + (k & 1) * C * LT + lane * LT;
       float* Rc = RT + (k & 1) * C * LT + lane * LT;
       const int n = min(kScTT, T - k * kScTT);
-      // four steps per read, eight reads ahead (32 steps, longer than an LDS round trip):
-      // group u of a round of 32 steps is read in the round before. The rows are padded so
-      // that the reads ahead of the last round stay inside them (and are not used); the
-      // steps past the last whole round go one at a time.
-      const int nr = n & ~31;
-      float4 gq[8], iq[8];
+      if (n == kScTT) {
+        // A whole tile, fully unrolled in groups of 8 steps held in kScSets rotating register
+        // sets: group m's operands are read right after group m - kScSets is chained (into
+        // the registers it freed), so each read is issued kScSets - 1 groups ahead of its
+        // use and no values move between registers (a rolled loop with rotating arrays
+        // compiled to a register copy per value and waited for every read at the end of
+        // each round). Each group issues six LDS operations (four reads, two result writes),
+        // so 6 (kScSets - 1) = 12 are younger than the reads a group waits for: within the
+        // wait counter's range.
+        constexpr int NG = kScTT / 8;
+        const float4* G4 = reinterpret_cast<const float4*>(Gc);
+        const float4* I4 = reinterpret_cast<const float4*>(Ic);
+        float4* R4 = reinterpret_cast<float4*>(Rc);
+        float4 gs[kScSets][2], is[kScSets][2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        gq[u] = *reinterpret_cast<const float4*>(Gc + 4 * u);
-        iq[u] = *reinterpret_cast<const float4*>(Ic + 4 * u);
-      }
-      for (int t = 0; t < nr; t += 32) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const float4 gv = gq[u], iv = iq[u];
-          gq[u] = *reinterpret_cast<const float4*>(Gc + t + 32 + 4 * u);
-          iq[u] = *reinterpret_cast<const float4*>(Ic + t + 32 + 4 * u);
-          float4 r;
-          s = __builtin_fmaf(gv.x, s, iv.x);
-          r.x = s;
-          s = __builtin_fmaf(gv.y, s, iv.y);
-          r.y = s;
-          s = __builtin_fmaf(gv.z, s, iv.z);
-          r.z = s;
-          s = __builtin_fmaf(gv.w, s, iv.w);
-          r.w = s;
-          *reinterpret_cast<float4*>(Rc + t + 4 * u) = r;
+        for (int m = 0; m < kScSets; ++m) {
+          gs[m][0] = G4[2 * m];
+          gs[m][1] = G4[2 * m + 1];
+          is[m][0] = I4[2 * m];
+          is[m][1] = I4[2 * m + 1];
         }
-      }
-      for (int t = nr; t < n; ++t) {
-        s = __builtin_fmaf(Gc[t], s, Ic[t]);
-        Rc[t] = s;
+#pragma unroll
+        for (int m = 0; m < NG; ++m) {
+          const int q = m % kScSets;
+          float4 r[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            s = __builtin_fmaf(gs[q][h].x, s, is[q][h].x);
+            r[h].x = s;
+            s = __builtin_fmaf(gs[q][h].y, s, is[q][h].y);
+            r[h].y = s;
+            s = __builtin_fmaf(gs[q][h].z, s, is[q][h].z);
+            r[h].z = s;
+            s = __builtin_fmaf(gs[q][h].w, s, is[q][h].w);
+            r[h].w = s;
+          }
+          R4[2 * m] = r[0];
+          R4[2 * m + 1] = r[1];
+          if (m + kScSets < NG) {
+            gs[q][0] = G4[2 * (m + kScSets)];
+            gs[q][1] = G4[2 * (m + kScSets) + 1];
+            is[q][0] = I4[2 * (m + kScSets)];
+            is[q][1] = I4[2 * (m + kScSets) + 1];
+          }
+          // keeps the reads where they are issued (the scheduler would otherwise sink them
+          // next to their use and wait a full LDS round trip per group)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        // the last, partial tile: one step at a time
+        for (int t = 0; t < n; ++t) {
+          s = __builtin_fmaf(Gc[t], s, Ic[t]);
+          Rc[t] = s;
+        }
       }
     }
     if (storer && k >= 1) {
@@ -1549,7 +1573,8 @@ hipError_t launch_gemm(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   }
 }
 
-// Columns per k_scan_ring block: 16 (a 64-byte line per step row per block).
+// Columns per k_scan_ring block: 8, so that H / 8 blocks (256 at H = 2048) cover the CUs;
+// the two blocks of a 64-byte line sit on one XCD and share its L2.
 template <bool GATE>
 static hipError_t scan_ring_launch(const float* g, const float* in, const float* lb, float* recur, float* state,
                                    int rows, int H, hipStream_t s) {
@@ -1561,7 +1586,7 @@ static hipError_t scan_ring_launch(const float* g, const float* in, const float*
     k_scan_ring<GATE, C><<<H / C, 64 * kScWaves, lds, s>>>(g, in, lb, recur, state, rows, H);
     return hipGetLastError();
   };
-  return go(std::integral_constant<int, 16>{});
+  return go(std::integral_constant<int, 8>{});
 }
 
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
