@@ -1068,17 +1068,15 @@ __global__ void k_gather_rows(const float* __restrict__ x, const int* __restrict
 // steps. Waves by role: wave 0 runs the C column chains (state = fma(g, state, in), in
 // time order) at raised issue priority; waves 1-4 fill a ring of kScNR tiles of g and in by
 // direct global-to-LDS DMA (lane l's 16 bytes land at LDS base + 16 l: 256 / C steps x C
-// columns per transfer); all fifteen other waves convert each tile into column-major rows
-// for the chain, and the last four store the previous tile's results. One barrier per
-// tile. (Launches use C = 8: at 2048 x 2048 a tile iteration takes about 1.2 us, set by the
-// chain wave; 16 columns per block, half the blocks, measured 5% slower and 4 columns per
-// block 40% slower.) The column groups of one line go to blocks of the same XCD (blocks
-// are dealt to the 8 XCDs round-robin).
+// columns per transfer); waves 1-14 convert each tile into column-major rows for the chain,
+// and the last wave stores the previous tile. One barrier per tile. (Launches use C = 8: at
+// 2048 x 2048 16 columns per block, half the blocks, measured 15% slower and 4 columns per
+// block 60% slower.) The column groups of one line go to blocks of the same XCD (blocks are
+// dealt to the 8 XCDs round-robin).
 constexpr int kScTT = 128;
-constexpr int kScWaves = 16, kScStoreWaves = 4;  // the last kScStoreWaves waves store
-constexpr int kScSets = 3;  // register sets of the chain's 8-step groups
-// Ring depth (tiles): the loads of a tile are in flight for NR - 2 tiles of chain work
-// (about 1.2 us each).
+constexpr int kScWaves = 16, kScStoreWaves = 1;  // the last kScStoreWaves waves store
+// Ring depth (tiles): the loads of a tile are in flight for NR - 2 tile iterations (about
+// 1 us each).
 template <int C>
 constexpr int scan_ring_depth() {
   return C == 4 ? 16 : (C == 8 ? 8 : 4);
@@ -1109,28 +1107,40 @@ __device__ __forceinline__ void scan_issue(const float* g, const float* in, floa
 // the gated values never go through memory. Element tail rules do not arise: this kernel
 // requires H % 16 == 0.
 //
-// Each iteration k: the loaders issue the transfers of tile k + kScNR - 1; the fifteen
-// non-chain waves convert tile k + 1 from the ring (step-major, as loaded) into
-// column-major rows GT / IT (one per column, kScTT + 36 floats apart); wave 0 chains tile k
-// from its column's rows, four steps per LDS read, into column-major results RT; the store
-// waves write tile k - 1's results back step-major, a float4 (4 columns of one step) per
-// thread. Tile k + 1 must then be in LDS at the barrier of iteration k, and an extra first
-// iteration converts tile 0.
+// Each iteration k: the loaders issue the transfers of tile k + kScNR - 1; waves 1 .. 14
+// convert tile k + 1 from the ring (step-major, as loaded) into column-major rows GT / IT
+// (three tile buffers, one row per column); wave 0 chains tile k; wave 15 stores tile k - 1.
+// Cycles per tile at 2048 x 2048 (timing copy, medians): chain 1370, gate math 990, store
+// wave 1850 with its stores drained, iteration 2350 (the chain alone took 2300 when it
+// wrote its results).
+//  * The chain: lane (cl, sg) = NSEG cl + sg holds segment sg (SL = kScTT / NSEG steps) of
+//    column cl, read once per tile. Round r runs segment r's steps in every lane (only the
+//    lanes of segment r hold the running state; the others compute values nobody uses), and
+//    a DPP row shift hands each running state to the next segment's lane (after the last
+//    round, back to segment 0). The lanes of segment r keep the state they start it from,
+//    and these starting states are the chain's only LDS write (a result write costs the
+//    issuing wave some 25-30 cycles; one per 4 steps doubled the chain's time).
+//  * The store wave recomputes each segment of tile k - 1 from its starting state, with the
+//    same FMAs in the same order (so the same values), and stores the states step by step.
+// Tile k + 1 must then be in LDS at the barrier of iteration k, and an extra first iteration
+// converts tile 0. A partial last tile is chained one step at a time by the segment-0 lanes,
+// which store it themselves.
 template <bool GATE, int C, int kScNR = scan_ring_depth<C>()>
 __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __restrict__ g, const float* __restrict__ in,
                                                              const float* __restrict__ lb, float* __restrict__ recur,
                                                              float* __restrict__ state, int T, int H) {
   static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 columns per block");
-  static_assert((64 * (kScWaves - 1)) % C == 0, "a converting lane keeps its column");
+  constexpr int NCONV = kScWaves - 1 - kScStoreWaves;  // converting waves 1 .. NCONV
+  static_assert((64 * NCONV) % C == 0, "a converting lane keeps its column");
   static_assert((kScNR - 2) * kScTT * C / 512 < 64, "outstanding transfers per loader wave");
   constexpr int LPW = kScTT * C / 512;  // transfers per loader wave per tile
-  constexpr int LPR = C / 4;            // float4 per step row
+  constexpr int NSEG = 64 / C, SL = kScTT / NSEG;
   constexpr int LT = kScTT + 36;  // column row: the tile and a pad against bank conflicts
   extern __shared__ __align__(16) float sm[];
-  float* ring = sm;                        // [kScNR][2][kScTT][C], as loaded
-  float* GT = ring + kScNR * 2 * kScTT * C;  // [2][C][LT] converted g (tile parity)
-  float* IT = GT + 2 * C * LT;             // [2][C][LT] converted in
-  float* RT = IT + 2 * C * LT;             // [2][C][LT] results
+  float* ring = sm;                          // [kScNR][2][kScTT][C], as loaded
+  float* GT = ring + kScNR * 2 * kScTT * C;  // [3][C][LT] converted g (tile % 3)
+  float* IT = GT + 3 * C * LT;               // [3][C][LT] converted in
+  float* ST = IT + 3 * C * LT;               // [2][64] starting states of the segments (tile & 1)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // column group: XCD-contiguous when the groups split evenly over the 8 XCDs
   const int ngrp = H / C, b = blockIdx.x;
@@ -1138,19 +1148,24 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
   const int c0 = grp * C;
   const int ntiles = (T + kScTT - 1) / kScTT;
   const bool loader = wave >= 1 && wave <= 4;
+  const bool conv = wave >= 1 && wave <= NCONV;
   const bool storer = wave >= kScWaves - kScStoreWaves;
-  float s = (wave == 0 && lane < C) ? state[c0 + lane] : 0.0f;
+  constexpr int SQ = SL / kScStoreWaves;  // steps of a segment each store wave stores
+  const int sq0 = (wave - (kScWaves - kScStoreWaves)) * SQ;
+  // chain and store waves: lane (cl, sg)
+  const int cl = lane / NSEG, sg = lane % NSEG;
+  float s = (wave == 0 && sg == 0) ? state[c0 + cl] : 0.0f;
   // the chain is the block's critical path: its instructions issue ahead of the conversion
   // sharing its SIMD
   if (wave == 0) __builtin_amdgcn_s_setprio(3);
-  // the column a converting lane handles is fixed (64 x 15 lanes, C columns per step row)
+  // the column a converting lane handles is fixed (64 x NCONV lanes, C columns per step row)
   const int ccol = (threadIdx.x - 64) % C;
-  const float lbc = (GATE && wave >= 1 && lb) ? lb[c0 + ccol] : 0.0f;
+  const float lbc = (GATE && conv && lb) ? lb[c0 + ccol] : 0.0f;
   if (loader)
     for (int t = 0; t < kScNR - 1 && t < ntiles; ++t) scan_issue<C>(g, in, ring, t, t, T, H, c0, wave - 1, lane);
   for (int k = -1; k <= ntiles; ++k) {
-    // this wave's LDS writes (results, converted tiles) have landed before the barrier
-    // publishes them
+    // this wave's LDS writes (converted tiles, starting states) have landed before the
+    // barrier publishes them
     __builtin_amdgcn_s_waitcnt(0xC07F);
     if (loader) {
       // this wave's transfers of tile k + 1 are done once only later tiles' are outstanding
@@ -1163,15 +1178,15 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (loader && k >= 0 && k + kScNR - 1 < ntiles)
       scan_issue<C>(g, in, ring, k + kScNR - 1, (k + kScNR - 1) % kScNR, T, H, c0, wave - 1, lane);
-    if (wave >= 1 && k + 1 < ntiles) {
+    if (conv && k + 1 < ntiles) {
       // tile k + 1 into column-major rows (GATE: g' = sigmoid(f), then the lower bound;
       // in' = swiglu(i, 1 - g'))
       const float* Gr = ring + (((k + 1) % kScNR) * 2 + 0) * kScTT * C;
       const float* Ir = ring + (((k + 1) % kScNR) * 2 + 1) * kScTT * C;
-      float* Gc = GT + ((k + 1) & 1) * C * LT + ccol * LT;
-      float* Ic = IT + ((k + 1) & 1) * C * LT + ccol * LT;
+      float* Gc = GT + ((k + 1) % 3) * C * LT + ccol * LT;
+      float* Ic = IT + ((k + 1) % 3) * C * LT + ccol * LT;
       const int n = min(kScTT, T - (k + 1) * kScTT);
-      for (int e = threadIdx.x - 64; e < n * C; e += 64 * (kScWaves - 1)) {
+      for (int e = threadIdx.x - 64; e < n * C; e += 64 * NCONV) {
         float gg = Gr[e], ii = Ir[e];
         if (GATE) {
           gg = sigmoid_of(gg, false);
@@ -1183,80 +1198,79 @@ __global__ __launch_bounds__(64 * kScWaves) void k_scan_ring(const float* __rest
         Ic[st] = ii;
       }
     }
-    if (wave == 0 && k >= 0 && k < ntiles && lane < C) {
-      const float* Gc = GT + (k & 1) * C * LT + lane * LT;
-      const float* Ic = IT + (k & 1) * C * LT + lane * LT;
-      float* Rc = RT + (k & 1) * C * LT + lane * LT;
+    if (wave == 0 && k >= 0 && k < ntiles) {
+      const float* Gc = GT + (k % 3) * C * LT + cl * LT;
+      const float* Ic = IT + (k % 3) * C * LT + cl * LT;
       const int n = min(kScTT, T - k * kScTT);
       if (n == kScTT) {
-        // A whole tile, fully unrolled in groups of 8 steps held in kScSets rotating register
-        // sets: group m's operands are read right after group m - kScSets is chained (into
-        // the registers it freed), so each read is issued kScSets - 1 groups ahead of its
-        // use and no values move between registers (a rolled loop with rotating arrays
-        // compiled to a register copy per value and waited for every read at the end of
-        // each round). Each group issues six LDS operations (four reads, two result writes),
-        // so 6 (kScSets - 1) = 12 are younger than the reads a group waits for: within the
-        // wait counter's range.
-        constexpr int NG = kScTT / 8;
-        const float4* G4 = reinterpret_cast<const float4*>(Gc);
-        const float4* I4 = reinterpret_cast<const float4*>(Ic);
-        float4* R4 = reinterpret_cast<float4*>(Rc);
-        float4 gs[kScSets][2], is[kScSets][2];
+        const float4* G4 = reinterpret_cast<const float4*>(Gc + sg * SL);
+        const float4* I4 = reinterpret_cast<const float4*>(Ic + sg * SL);
+        float4 gv[SL / 4], iv[SL / 4];
 #pragma unroll
-        for (int m = 0; m < kScSets; ++m) {
-          gs[m][0] = G4[2 * m];
-          gs[m][1] = G4[2 * m + 1];
-          is[m][0] = I4[2 * m];
-          is[m][1] = I4[2 * m + 1];
+        for (int u = 0; u < SL / 4; ++u) {
+          gv[u] = G4[u];
+          iv[u] = I4[u];
         }
+        float s0 = s;  // the state this lane's segment starts from (segment 0: the tile's)
 #pragma unroll
-        for (int m = 0; m < NG; ++m) {
-          const int q = m % kScSets;
-          float4 r[2];
+        for (int r = 0; r < NSEG; ++r) {
+          if (r > 0) s0 = (sg == r) ? s : s0;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            s = __builtin_fmaf(gs[q][h].x, s, is[q][h].x);
-            r[h].x = s;
-            s = __builtin_fmaf(gs[q][h].y, s, is[q][h].y);
-            r[h].y = s;
-            s = __builtin_fmaf(gs[q][h].z, s, is[q][h].z);
-            r[h].z = s;
-            s = __builtin_fmaf(gs[q][h].w, s, is[q][h].w);
-            r[h].w = s;
+          for (int u = 0; u < SL / 4; ++u) {
+            s = __builtin_fmaf(gv[u].x, s, iv[u].x);
+            s = __builtin_fmaf(gv[u].y, s, iv[u].y);
+            s = __builtin_fmaf(gv[u].z, s, iv[u].z);
+            s = __builtin_fmaf(gv[u].w, s, iv[u].w);
           }
-          R4[2 * m] = r[0];
-          R4[2 * m + 1] = r[1];
-          if (m + kScSets < NG) {
-            gs[q][0] = G4[2 * (m + kScSets)];
-            gs[q][1] = G4[2 * (m + kScSets) + 1];
-            is[q][0] = I4[2 * (m + kScSets)];
-            is[q][1] = I4[2 * (m + kScSets) + 1];
-          }
-          // keeps the reads where they are issued (the scheduler would otherwise sink them
-          // next to their use and wait a full LDS round trip per group)
-          __builtin_amdgcn_sched_barrier(0);
+          // row_shr:1, after the last round row_shl:NSEG-1 (within rows of 16 lanes; a
+          // column's NSEG lanes never straddle a row)
+          const int si = __builtin_bit_cast(int, s);
+          s = __builtin_bit_cast(float, r + 1 < NSEG ? __builtin_amdgcn_update_dpp(0, si, 0x111, 0xf, 0xf, false)
+                                                     : __builtin_amdgcn_update_dpp(0, si, 0x100 + NSEG - 1, 0xf, 0xf, false));
         }
-      } else {
-        // the last, partial tile: one step at a time
+        ST[(k & 1) * 64 + lane] = s0;
+      } else if (sg == 0) {
+        // the last, partial tile: one step at a time, stored here
+        float* out = recur + static_cast<size_t>(k) * kScTT * H + c0 + cl;
         for (int t = 0; t < n; ++t) {
           s = __builtin_fmaf(Gc[t], s, Ic[t]);
-          Rc[t] = s;
+          out[static_cast<size_t>(t) * H] = s;
         }
       }
     }
-    if (storer && k >= 1) {
-      // results of tile k - 1 to global memory, step-major, a float4 per thread
-      const float* Rp = RT + ((k - 1) & 1) * C * LT;
-      const int n = min(kScTT, T - (k - 1) * kScTT);
-      for (int f = threadIdx.x - 64 * (kScWaves - kScStoreWaves); f < n * LPR; f += 64 * kScStoreWaves) {
-        const int row = f / LPR, c4 = f % LPR;
-        const float4 v = make_float4(Rp[(4 * c4) * LT + row], Rp[(4 * c4 + 1) * LT + row], Rp[(4 * c4 + 2) * LT + row],
-                                     Rp[(4 * c4 + 3) * LT + row]);
-        *reinterpret_cast<float4*>(recur + static_cast<size_t>((k - 1) * kScTT + row) * H + c0 + 4 * c4) = v;
+    if (storer && k >= 1 && k * kScTT <= T) {
+      // tile k - 1 (whole): segment sg of column cl again from its starting state
+      const int kk = k - 1;
+      const float4* G4 = reinterpret_cast<const float4*>(GT + (kk % 3) * C * LT + cl * LT + sg * SL);
+      const float4* I4 = reinterpret_cast<const float4*>(IT + (kk % 3) * C * LT + cl * LT + sg * SL);
+      float r = ST[(kk & 1) * 64 + lane];
+      float4 gv[SL / 4], iv[SL / 4];
+#pragma unroll
+      for (int u = 0; u < SL / 4; ++u) {
+        gv[u] = G4[u];
+        iv[u] = I4[u];
+      }
+      float* out = recur + static_cast<size_t>(kk * kScTT + sg * SL) * H + c0 + cl;
+      // every store wave recomputes the segment from its start and stores steps
+      // [sq0, sq0 + SQ) (two store waves measured no faster than one)
+#pragma unroll
+      for (int u = 0; u < SL / 4; ++u) {
+        float v[4];
+        r = __builtin_fmaf(gv[u].x, r, iv[u].x);
+        v[0] = r;
+        r = __builtin_fmaf(gv[u].y, r, iv[u].y);
+        v[1] = r;
+        r = __builtin_fmaf(gv[u].z, r, iv[u].z);
+        v[2] = r;
+        r = __builtin_fmaf(gv[u].w, r, iv[u].w);
+        v[3] = r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (4 * u + c >= sq0 && 4 * u + c < sq0 + SQ) out[static_cast<size_t>(4 * u + c) * H] = v[c];
       }
     }
   }
-  if (wave == 0 && lane < C) state[c0 + lane] = s;
+  if (wave == 0 && sg == 0) state[c0 + cl] = s;
 }
 
 __global__ void k_embed(const float* __restrict__ emb, const int64_t* __restrict__ ids,
@@ -1581,7 +1595,8 @@ static hipError_t scan_ring_launch(const float* g, const float* in, const float*
   auto go = [&](auto cc) {
     constexpr int C = decltype(cc)::value;
     const size_t lds =
-        (static_cast<size_t>(scan_ring_depth<C>()) * 2 * kScTT * C + 6 * static_cast<size_t>(C) * (kScTT + 36)) *
+        (static_cast<size_t>(scan_ring_depth<C>()) * 2 * kScTT * C + 6 * static_cast<size_t>(C) * (kScTT + 36) +
+         128) *
         sizeof(float);
     k_scan_ring<GATE, C><<<H / C, 64 * kScWaves, lds, s>>>(g, in, lb, recur, state, rows, H);
     return hipGetLastError();
