@@ -421,8 +421,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
       if (MODE == kFloat) {
         const float y[16] = {x.f[0].x, x.f[0].y, x.f[0].z, x.f[0].w, x.f[1].x, x.f[1].y, x.f[1].z, x.f[1].w,
                              x.f[2].x, x.f[2].y, x.f[2].z, x.f[2].w, x.f[3].x, x.f[3].y, x.f[3].z, x.f[3].w};
-#pragma unroll
-        for (int t = 0; t < 16; ++t) facc = __builtin_fmaf(y[t], code_f(w, t), facc);
+        facc = word_dot_f(w, y, facc);
       } else {
         const uint32_t w0 = w4_i8(w, 0), w1 = w4_i8(w, 1), w2 = w4_i8(w, 2), w3 = w4_i8(w, 3);
         hacc = dot4(w3, x.h.w, dot4(w2, x.h.z, dot4(w1, x.h.y, dot4(w0, x.h.x, hacc))));
