@@ -29,7 +29,8 @@ Beside the headline (all on seeded synthetic weights of the named shapes):
             8 TB/s, ops 2MNK against the 5.0 POP/s int8 peak.
   prefill   1.3B shape, 2048-token prompt, time to the first token (all layers + final
             norm, lm_head, argmax) per mode; per-GEMM microseconds and TOP/s (event pair
-            around every launch); FixedQ510 runs two int8 passes (hi/lo code planes).
+            around every launch); FixedQ510 runs two int8 passes (hi/lo code planes);
+            float also with the opt-in chunked parallel scan (`chunked_scan`).
   serve     batched decode of independent streams (2.7B x 64 streams x 128-token prompts,
             float and FixedQ510; 1.3B x 32 x 512, FixedQ510): prompts prefilled together,
             then lockstep decode steps timed on the host around each step; weight bytes
@@ -179,9 +180,18 @@ def measure_prefill(blob_dir, T=2048, modes=("fixed", "int8", "float")):
         e = Engine(0)
         e.load_blob(p, mode)
         total, kinds = e.time_prefill(ids, warmup=1, reps=3)
+        chunked = None
+        if name == "float":
+            # the opt-in chunked parallel scan (within fp32 rounding of the reference, not equal)
+            e.set_scan(True)
+            ctotal, ckinds = e.time_prefill(ids, warmup=1, reps=3)
+            e.set_scan(False)
+            chunked = {"ms": round(ctotal / 1e3, 3), "mixer_ms": round(ckinds["mixer"] / 1e3, 3)}
         e.close()
         r = {"ms": round(total / 1e3, 3), "tok_s": round(T / total * 1e6, 1),
              "kinds_ms": {k: round(v / 1e3, 3) for k, v in kinds.items()}}
+        if chunked:
+            r["chunked_scan"] = chunked
         if name != "float":
             planes = 2 if name == "fixed" else 1
             ops = {"gemm_ifg": 2.0 * T * 3 * H * H * L, "gemm_o": 2.0 * T * H * H * L,

@@ -159,6 +159,16 @@ typedef int (*mmf_matmul_fn)(void* user, int layer, int proj, int k, const int32
                              size_t K, size_t N, size_t rows);
 int mmf_model_set_matmul(mmf_ctx* ctx, mmf_matmul_fn fn, void* user);
 
+/* The prefill recurrence of float mode. chunked = 0 (the default): the time-ordered scan,
+ * state = fma(f, state, in) step by step as the reference runs it (hgrn_scan.cpp:11-19,
+ * simd.hpp:335-357), bit-exact. chunked = 1: a chunked parallel scan (chunks of 16 steps
+ * scanned from zero with the product of their gates, the chunks' starting states combined
+ * in time order, then each chunk re-run from its starting state), which rounds differently:
+ * logits agree within fp32 rounding, not bit for bit. It has no counterpart in the reference;
+ * it applies to float-mode prefills of one sequence with hidden % 64 == 0 (everything else
+ * keeps the time-ordered scan). */
+int mmf_model_set_scan(mmf_ctx* ctx, int chunked);
+
 /* Device-time op profile of the model's kernels, for the Profiler / --profile breakdown
  * (the reference times each op on the host: hgrn_model.cpp:88-189, bench.cpp:16-40).
  * While on, every model launch is bracketed by events on the context's stream, the decode

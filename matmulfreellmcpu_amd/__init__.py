@@ -79,6 +79,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_model_prefill_streams": (i, [_vp, _sz, _i64p, C.POINTER(C.c_size_t), _fp, _i64p]),
         "mmf_model_step": (i, [_vp, _i64p, _fp, _i64p]),
         "mmf_model_state": (i, [_vp, _fp]),
+        "mmf_model_set_scan": (i, [_vp, i]),
         "mmf_model_forward": (i, [_vp, _i64p, _sz, _fp]),
         "mmf_model_trace": (i, [_vp, _i64p, _sz, _fp, _fp, _fp]),
         "mmf_model_time_decode": (i, [_vp, i, i, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -265,6 +266,10 @@ class Engine:
                                           lg.ctypes.data_as(_fp) if lg is not None else None,
                                           am.ctypes.data_as(_i64p)))
         return (am, lg) if want_logits else am
+
+    def set_scan(self, chunked: bool):
+        """Float-mode prefill recurrence: time-ordered (default, bit-exact) or chunked parallel."""
+        self._chk(self.lib.mmf_model_set_scan(self.h, 1 if chunked else 0))
 
     def state(self):
         c = self.cfg

@@ -95,6 +95,7 @@ struct RowScratch {
   DBuf ids, h, resid, i, f, g, recur, scan, z, logits, state0, am;
   DBuf acty, actq, actct, actsa;
   DBuf segs;  // stacked prompts: nseg + 1 row offsets, then the nseg last-row indices
+  DBuf chunk;  // chunk summaries and starting states of the chunked scan
 };
 
 struct Model {
@@ -102,6 +103,7 @@ struct Model {
   bool begun = false, finalized = false;
   int mode = kFloat, frac = 10;
   float qs = 1024.0f;
+  bool chunked_scan = false;  // float prefill: chunked parallel scan (mmf_model_set_scan)
   std::unordered_map<std::string, DevTensor> tensors;
   const float* emb = nullptr;
   const float* norm_w = nullptr;
@@ -441,7 +443,18 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     tend(c);
     return e;
   };
-  if (!mix_in_prologue) MMF_HIP(run_mixer());
+  // float mode, opt-in: the chunked parallel scan instead of the time-ordered one (a prefill
+  // of one sequence without a trace; H % 64 == 0)
+  const bool chunked = mode == kFloat && m.chunked_scan && !stream_state && !segs && !trace_dev && rows > 1 &&
+                       H % 64 == 0;
+  if (chunked) {
+    tbeg(c, kRkMixer);
+    float* ws = s.chunk.as<float>(scan_chunked_ws_floats(rows, H));
+    MMF_HIP(launch_scan_chunked(ib, fb, L.lb, rb, state, ws, rows, H, st));
+    tend(c);
+  } else if (!mix_in_prologue) {
+    MMF_HIP(run_mixer());
+  }
   if (trace_dev) {
     const size_t n = static_cast<size_t>(rows) * H * sizeof(float);
     MMF_HIP(hipMemcpyAsync(trace_dev + 0 * rows * H, ib, n, hipMemcpyDeviceToDevice, st));
@@ -1631,6 +1644,14 @@ int mmf_model_set_matmul(mmf_ctx* c, mmf_matmul_fn fn, void* user) {
     Model& m = model_of(c);
     m.ext_fn = fn;
     m.ext_user = fn ? user : nullptr;
+  });
+}
+
+int mmf_model_set_scan(mmf_ctx* c, int chunked) {
+  return guard(c, [&] {
+    if (chunked != 0 && chunked != 1) fail(MMF_ERR_ARG, "mmf_model_set_scan: chunked must be 0 or 1");
+    Model& m = model_of(c);
+    m.chunked_scan = chunked != 0;
   });
 }
 

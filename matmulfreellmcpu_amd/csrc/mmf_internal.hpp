@@ -228,6 +228,13 @@ int float_mfma_min_rows();
 // scan_out untouched.
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
                         const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s);
+// The chunked parallel scan of a prefill (float mode, opt-in): the gate math of the raw i
+// and f rows [rows, H] and the recurrence from state [H] (updated), with chunk summaries in
+// ws (scan_chunked_ws_floats floats). Results are within fp32 rounding of the time-ordered
+// scan, not equal to it. Needs H % 64 == 0.
+size_t scan_chunked_ws_floats(int rows, int H);
+hipError_t launch_scan_chunked(const float* i, const float* f, const float* lb, float* recur, float* state,
+                               float* ws, int rows, int H, hipStream_t s);
 // The same over nseg sequences stacked as row segments [off[b], off[b + 1]) (device array of
 // nseg + 1 offsets), segment b scanning from and into state + b * H. Needs H % 8 == 0, so
 // that no element of any segment is a SIMD tail element of the gate math. keep_gates as

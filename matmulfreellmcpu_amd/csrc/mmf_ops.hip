@@ -1604,6 +1604,126 @@ static hipError_t scan_ring_launch(const float* g, const float* in, const float*
   return go(std::integral_constant<int, 8>{});
 }
 
+// Chunked parallel scan of the prefill recurrence (float mode, opt-in; not the reference's
+// rounding). Time is cut into chunks of kChunkT steps (16: at T = 2048, H = 2048 that is 4096
+// waves, four per SIMD, to hide the loads), and three launches run:
+//   1. k_chunk_sum, per (chunk, column): the gate math of k_gate and the chunk's scan from a
+//      zero state, l = fma(g, l, in), with the product of its gates, p = g * p;
+//   2. k_chunk_carry, per column: the chunks' starting states in time order,
+//      S_c = fma(p_{c-1}, S_{c-1}, l_{c-1}), S_0 = the layer's state;
+//   3. k_chunk_apply, per (chunk, column): the chunk again from its starting state with the
+//      reference's own steps, state = fma(g, state, in); the last chunk stores the state.
+// In real arithmetic S_c is the state the time-ordered scan reaches; in fp32 it differs by
+// the rounding of the products and of the combination, so the result is within tolerance of
+// the reference rather than equal to it. The chunks and columns run in parallel (one wave
+// per 64 columns of a chunk); the gate math runs twice, in launches 1 and 3.
+constexpr int kChunkT = 16;
+
+__device__ __forceinline__ void gate_pair(float f, float i, float lbv, bool has_lb, float& g, float& in) {
+  g = sigmoid_of(f, false);
+  if (has_lb) g = __builtin_fmaf(1.0f - lbv, g, lbv);
+  in = swiglu_of(i, 1.0f - g, false);
+}
+
+__global__ __launch_bounds__(64) void k_chunk_sum(const float* __restrict__ fr, const float* __restrict__ ir,
+                                                  const float* __restrict__ lb, float* __restrict__ lsum,
+                                                  float* __restrict__ prod, int T, int H) {
+  const int h = blockIdx.x * 64 + threadIdx.x, c = blockIdx.y;
+  const int t0 = c * kChunkT, n = min(kChunkT, T - t0);
+  float fv[kChunkT], iv[kChunkT];
+#pragma unroll
+  for (int u = 0; u < kChunkT; ++u) {
+    const size_t e = static_cast<size_t>(t0 + (u < n ? u : 0)) * H + h;
+    fv[u] = fr[e];
+    iv[u] = ir[e];
+  }
+  const float lbv = lb ? lb[h] : 0.0f;
+  float l = 0.0f, p = 1.0f;
+#pragma unroll
+  for (int u = 0; u < kChunkT; ++u) {
+    if (u < n) {
+      float g, in;
+      gate_pair(fv[u], iv[u], lbv, lb != nullptr, g, in);
+      l = __builtin_fmaf(g, l, in);
+      p = p * g;
+    }
+  }
+  lsum[static_cast<size_t>(c) * H + h] = l;
+  prod[static_cast<size_t>(c) * H + h] = p;
+}
+
+__global__ __launch_bounds__(64) void k_chunk_carry(const float* __restrict__ lsum, const float* __restrict__ prod,
+                                                    const float* __restrict__ state, float* __restrict__ start,
+                                                    int nchunks, int H) {
+  const int h = blockIdx.x * 64 + threadIdx.x;
+  float S = state[h];
+  constexpr int B = 64;  // chunks' summaries in flight at once (one memory round trip per 64 chunks)
+  for (int c0 = 0; c0 < nchunks; c0 += B) {
+    float lv[B], pv[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int c = c0 + u < nchunks ? c0 + u : nchunks - 1;
+      lv[u] = lsum[static_cast<size_t>(c) * H + h];
+      pv[u] = prod[static_cast<size_t>(c) * H + h];
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (c0 + u < nchunks) {
+        start[static_cast<size_t>(c0 + u) * H + h] = S;
+        S = __builtin_fmaf(pv[u], S, lv[u]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void k_chunk_apply(const float* __restrict__ fr, const float* __restrict__ ir,
+                                                    const float* __restrict__ lb, const float* __restrict__ start,
+                                                    float* __restrict__ recur, float* __restrict__ state, int T,
+                                                    int H) {
+  const int h = blockIdx.x * 64 + threadIdx.x, c = blockIdx.y;
+  const int t0 = c * kChunkT, n = min(kChunkT, T - t0);
+  float fv[kChunkT], iv[kChunkT];
+#pragma unroll
+  for (int u = 0; u < kChunkT; ++u) {
+    const size_t e = static_cast<size_t>(t0 + (u < n ? u : 0)) * H + h;
+    fv[u] = fr[e];
+    iv[u] = ir[e];
+  }
+  const float lbv = lb ? lb[h] : 0.0f;
+  float s = start[static_cast<size_t>(c) * H + h];
+#pragma unroll
+  for (int u = 0; u < kChunkT; ++u) {
+    if (u < n) {
+      float g, in;
+      gate_pair(fv[u], iv[u], lbv, lb != nullptr, g, in);
+      s = __builtin_fmaf(g, s, in);
+      recur[static_cast<size_t>(t0 + u) * H + h] = s;
+    }
+  }
+  if (c == static_cast<int>(gridDim.y) - 1) state[h] = s;
+}
+
+size_t scan_chunked_ws_floats(int rows, int H) {
+  return 3 * static_cast<size_t>((rows + kChunkT - 1) / kChunkT) * H;
+}
+
+hipError_t launch_scan_chunked(const float* i, const float* f, const float* lb, float* recur, float* state,
+                               float* ws, int rows, int H, hipStream_t s) {
+  if (rows < 1 || H % 64 != 0) return hipErrorInvalidValue;
+  const int nch = (rows + kChunkT - 1) / kChunkT;
+  float* lsum = ws;
+  float* prod = lsum + static_cast<size_t>(nch) * H;
+  float* start = prod + static_cast<size_t>(nch) * H;
+  k_chunk_sum<<<dim3(H / 64, nch), 64, 0, s>>>(f, i, lb, lsum, prod, rows, H);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_chunk_carry<<<H / 64, 64, 0, s>>>(lsum, prod, state, start, nch, H);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_chunk_apply<<<dim3(H / 64, nch), 64, 0, s>>>(f, i, lb, start, recur, state, rows, H);
+  return hipGetLastError();
+}
+
 hipError_t launch_mixer(const float* i, float* f, float* scan_out, float* recur, float* state,
                         const float* lb, int rows, int H, bool stream_state, bool keep_gates, hipStream_t s) {
   if (!stream_state && !keep_gates && rows > 1 && H % 16 == 0 &&
