@@ -633,6 +633,11 @@ Plan plan_of(const GemmArgs& a) {
   const int nz = (a.epi == kEpiSwigluPair) ? 1 : a.nmat;
   Plan p{a.rows <= 64 ? 1 : 2, 4, 1, 1};
   if (p.wm == 1 ? tiles_of<1, 4>(a) * nz < 256 : tiles_of<2, 4>(a) * nz < 256) p.wn = 2;
+  // FixedQ510 (two int8 passes per tile) over 128-row tiles: 128 x 128 tiles throughout.
+  // Finer tiles balance the CUs (the 1.3B i/f/g GEMM: 768 tiles, three per CU, instead of
+  // 384, one or two per CU): i/f/g 1.57 -> 1.30 ms and gate/up 2.43 -> 2.31 ms per 2048-token
+  // prefill. Int8Absmax gained nothing on i/f/g and lost 5% on gate/up.
+  if (a.mode == kFixed && p.wm == 2) p.wn = 2;
   const int tiles = (p.wm == 1 ? (p.wn == 4 ? tiles_of<1, 4>(a) : tiles_of<1, 2>(a))
                                : (p.wn == 4 ? tiles_of<2, 4>(a) : tiles_of<2, 2>(a))) * nz;
   // split K until there are 128 blocks (one per two CUs; more splits measured slower, the
