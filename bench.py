@@ -34,7 +34,9 @@ Beside the headline (all on seeded synthetic weights of the named shapes):
   serve     batched decode of independent streams (2.7B x 64 streams x 128-token prompts,
             float and FixedQ510; 1.3B x 32 x 512, FixedQ510): prompts prefilled together,
             then lockstep decode steps timed on the host around each step; weight bytes
-            per step against 8 TB/s.
+            per step against 8 TB/s; `kinds_per_step`: microseconds per step in each
+            launch kind and its weight GB/s (the step launched kernel by kernel with an
+            event pair around every launch).
   decode_tok_s_fixed / kernels_fixed: the batch-1 decode in FixedQ510 (the reference CLI's
             default mode) at the three shapes.
 """
@@ -232,8 +234,17 @@ def measure_serve(blob_dir, preset, B, T, mode_name, steps):
     for _ in range(steps):
         cur = e.step(cur)
     dt = time.perf_counter() - t0
+    # per launch kind: the same step launched kernel by kernel, an event pair around each
+    kinds = e.time_step_kinds(cur, warmup=1, reps=4)
     e.close()
     V, H, L, I = DIMS[preset]
+    kbytes = {"gemm_ifg": L * 3 * H * H / 4, "gemm_o": L * H * H / 4, "gemm_gate": L * 2 * I * H / 4,
+              "gemm_down": L * H * I / 4, "lm": V * H / 4}  # packed ternary weights per kind and step
+    kind_r = {k: {"us": round(v, 1)} for k, v in kinds.items() if v > 0}
+    for k, b in kbytes.items():
+        if kinds.get(k, 0) > 0:
+            kind_r[k]["weight_GBps"] = round(b / kinds[k] / 1e3, 1)
+            kind_r[k]["hbm_frac"] = round(b / kinds[k] / 1e3 / HBM_PEAK_GBS, 4)
     wbytes = L * (4 * H * H + 3 * I * H) / 4 + V * H / 4  # packed ternary weights read per step
     ops = 2.0 * B * (L * (4 * H * H + 3 * I * H) + V * H)
     step_s = dt / steps
@@ -241,7 +252,7 @@ def measure_serve(blob_dir, preset, B, T, mode_name, steps):
          "ms_per_step": round(step_s * 1e3, 3), "decode_tok_s": round(B * steps / dt, 1),
          "prefill_s": round(t_pre, 3), "weight_GBps": round(wbytes / step_s / 1e9, 1),
          "hbm_frac": round(wbytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
-         "TOPS": round(ops / step_s / 1e12, 2)}
+         "TOPS": round(ops / step_s / 1e12, 2), "kinds_per_step": kind_r}
     log(f"[bench] serve {preset} B={B} T={T} {mode_name}: {r['ms_per_step']} ms/step, {r['decode_tok_s']} tok/s")
     return r
 

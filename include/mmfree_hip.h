@@ -242,6 +242,14 @@ int mmf_model_time_decode(mmf_ctx* ctx, int warmup, int reps, double* step_us, d
 int mmf_model_time_prefill(mmf_ctx* ctx, const int64_t* ids, size_t T, int warmup, int reps,
                            double* total_us, double* kind_us);
 
+/* Timing of one lockstep serving step of the context's streams (mmf_model_reset(ctx, B)),
+ * launched kernel by kernel with an HIP event pair around every launch: after `warmup`
+ * steps, kind_us (8 doubles, the kinds of mmf_model_time_prefill; the embedding is counted
+ * under "embedding", the argmax with the lm_head) receives the microseconds per step spent
+ * in each kind over `reps` steps. The steps advance the streams' states like mmf_model_step.
+ * No counterpart in the reference engine: measurement only. */
+int mmf_model_time_step(mmf_ctx* ctx, const int64_t* tokens, int warmup, int reps, double* kind_us);
+
 /* Timing of mmf_bitlinear on device buffers (same arguments): average microseconds per call
  * with `reps` calls back to back in one HIP graph (device time; launched one by one when
  * MMF_GRAPH=0), and of its two launches (prologue: RMSNorm + activation codes; GEMM) from an

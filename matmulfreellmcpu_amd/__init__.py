@@ -80,6 +80,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_model_step": (i, [_vp, _i64p, _fp, _i64p]),
         "mmf_model_state": (i, [_vp, _fp]),
         "mmf_model_set_scan": (i, [_vp, i]),
+        "mmf_model_time_step": (i, [_vp, _i64p, i, i, C.POINTER(C.c_double)]),
         "mmf_model_forward": (i, [_vp, _i64p, _sz, _fp]),
         "mmf_model_trace": (i, [_vp, _i64p, _sz, _fp, _fp, _fp]),
         "mmf_model_time_decode": (i, [_vp, i, i, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -312,6 +313,13 @@ class Engine:
         self._chk(self.lib.mmf_model_time_prefill(self.h, ids.ctypes.data_as(_i64p), ids.size, warmup, reps,
                                                   C.byref(total), k if kinds else None))
         return total.value, (dict(zip(self.PREFILL_KINDS, list(k))) if kinds else None)
+
+    def time_step_kinds(self, tokens, warmup=1, reps=4):
+        """Microseconds per serving step in each launch kind (launches timed one by one)."""
+        tokens, _ = _np(tokens, np.int64)
+        k = (C.c_double * 8)()
+        self._chk(self.lib.mmf_model_time_step(self.h, tokens.ctypes.data_as(_i64p), warmup, reps, k))
+        return dict(zip(self.PREFILL_KINDS, list(k)))
 
     def measure_peaks(self):
         """Measured device ceilings: HBM and Infinity Cache read GB/s, int8 MFMA TOP/s, fp32

@@ -1549,6 +1549,30 @@ int mmf_model_prefill_streams(mmf_ctx* c, size_t n, const int64_t* ids, const si
   });
 }
 
+}  // extern "C"
+
+namespace {
+
+// The launches of one lockstep serving step of the m.streams streams: embedding of the
+// device tokens d, every layer over the B rows, final norm + lm_head into lg, argmax into am.
+void step_kernels(mmf_ctx* c, Model& m, const int64_t* d, float* h, float* lg, int64_t* am) {
+  const size_t B = m.streams, H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+  tbeg(c, kRkOther);
+  MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
+  tend(c);
+  for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
+    layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H, true,
+               nullptr);
+  lm_rows(c, m, static_cast<int>(B), h, lg);
+  tbeg(c, kRkLM);
+  MMF_HIP(launch_argmax_rows(lg, static_cast<int>(B), static_cast<int>(V), am, c->stream));
+  tend(c);
+}
+
+}  // namespace
+
+extern "C" {
+
 int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* argmax) {
   return guard(c, [&] {
     Model& m = model_of(c);
@@ -1563,16 +1587,7 @@ int mmf_model_step(mmf_ctx* c, const int64_t* tokens, float* logits, int64_t* ar
     int64_t* am = s.am.as<int64_t>(B);
     // embedding, all layers, final norm + lm_head, argmax: captured once per stream count
     // and replayed while no scratch buffer has moved (the first step runs them directly)
-    auto work = [&] {
-      tbeg(c, kRkOther);
-      MMF_HIP(launch_embed(m.emb, d, h, static_cast<int>(B), static_cast<int>(H), c->stream));
-      tend(c);
-      for (size_t l = 0; l < m.cfg.num_hidden_layers; ++l)
-        layer_rows(c, m, static_cast<int>(l), static_cast<int>(B), h, static_cast<float*>(m.state.p) + l * B * H,
-                   true, nullptr);
-      lm_rows(c, m, static_cast<int>(B), h, lg);
-      MMF_HIP(launch_argmax_rows(lg, static_cast<int>(B), static_cast<int>(V), am, c->stream));
-    };
+    auto work = [&] { step_kernels(c, m, d, h, lg, am); };
     if (m.ext_on() || c->timer.on) {  // host matmul or per-launch profiling: no graph
       work();
     } else if (m.step_graph && m.step_B == B && m.step_epoch == dbuf_epoch.load()) {
@@ -1797,6 +1812,26 @@ int mmf_measure_peaks(mmf_ctx* c, double* out4) {
     MMF_HIP(hipGetDevice(&dev));
     MMF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     MMF_HIP(measure_peaks(cus, c->stream, out4));
+  });
+}
+
+int mmf_model_time_step(mmf_ctx* c, const int64_t* tokens, int warmup, int reps, double* kind_us) {
+  return guard(c, [&] {
+    Model& m = model_of(c);
+    if (!tokens || !kind_us || reps < 1 || warmup < 0) fail(MMF_ERR_ARG, "invalid tokens/reps");
+    if (m.ext_on()) fail(MMF_ERR_STATE, "timing runs the built-in kernels: clear the external matmul first");
+    if (c->timer.on) fail(MMF_ERR_STATE, "timing while the op profile is on");
+    const size_t B = m.streams, H = m.cfg.hidden_size, V = m.cfg.vocab_size;
+    check_ids(m, tokens, B);
+    RowScratch& s = m.rs;
+    int64_t* d = s.ids.as<int64_t>(B);
+    MMF_HIP(hipMemcpyAsync(d, tokens, B * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    float* h = s.h.as<float>(B * H);
+    float* lg = s.logits.as<float>(B * V);
+    int64_t* am = s.am.as<int64_t>(B);
+    auto f = [&] { step_kernels(c, m, d, h, lg, am); };
+    for (int i = 0; i < warmup; ++i) f();
+    time_kinds(c, reps, f, kind_us);
   });
 }
 

@@ -414,3 +414,32 @@ def test_generate_370m(blobs, oracle, mode):
     np.testing.assert_array_equal(e.generate(ids, 32), want)
     assert_bitexact(e.state()[:, 0, :], wst, "370M final state")
     e.close()
+
+
+def test_time_step_runs_the_step(blobs):
+    """mmf_model_time_step launches the serving step kernel by kernel: one timed step
+    (warmup 0, reps 1) leaves the streams exactly where mmf_model_step with the same tokens
+    does (states and the next step's ids bit for bit), and reports time in the GEMM kinds."""
+    from matmulfreellmcpu_amd import Engine, FIXED_Q510, read_blob
+    print("time_step", flush=True)
+    blob = read_blob(blobs("small"))
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(3, blob.config.vocab_size, 9) for _ in range(4)]
+    t1, t2, t3 = (rng.integers(3, blob.config.vocab_size, 4) for _ in range(3))
+    outs = []
+    for timed in (False, True):
+        e = Engine(0)
+        e.load_blob(blob, FIXED_Q510)
+        e.reset(4)
+        e.prefill_streams(prompts)
+        e.step(t1)
+        if timed:
+            k = e.time_step_kinds(t2, warmup=0, reps=1)
+            assert all(v >= 0 for v in k.values()) and k["gemm_ifg"] > 0 and k["gemm_down"] > 0, k
+        else:
+            e.step(t2)
+        ids = e.step(t3)
+        outs.append((ids, e.state()))
+        e.close()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert_bitexact(outs[1][1], outs[0][1], "states after a timed step")
