@@ -638,6 +638,14 @@ Plan plan_of(const GemmArgs& a) {
   // 384, one or two per CU): i/f/g 1.57 -> 1.30 ms and gate/up 2.43 -> 2.31 ms per 2048-token
   // prefill. Int8Absmax gained nothing on i/f/g and lost 5% on gate/up.
   if (a.mode == kFixed && p.wm == 2) p.wn = 2;
+  // Int8Absmax: 64 x 256 tiles where 128 x 256 tiles would give the 256 CUs between one and
+  // two tiles each: the 1.3B i/f/g GEMM (384 tiles) 1.00 -> 0.90 ms per 2048-token prefill
+  // as 768 tiles, 2048 x 5632 x 1024 (352 tiles) 26.5 -> 24.8 us. At 704 tiles (2048 x 11264
+  // x 2048) the halving measured 8% slower.
+  if (a.mode == kInt8 && p.wm == 2 && p.wn == 4) {
+    const int t = tiles_of<2, 4>(a) * nz;
+    if (t > 256 && t < 512) p.wm = 1;
+  }
   const int tiles = (p.wm == 1 ? (p.wn == 4 ? tiles_of<1, 4>(a) : tiles_of<1, 2>(a))
                                : (p.wn == 4 ? tiles_of<2, 4>(a) : tiles_of<2, 2>(a))) * nz;
   // split K until there are 128 blocks (one per two CUs; more splits measured slower, the
