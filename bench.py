@@ -406,6 +406,9 @@ def main():
     ap.add_argument("--vendor-int8", default=None, metavar="T,H,I",
                     help="only time the vendor int8 GEMM on one prefill layer's shapes (child process)")
     ap.add_argument("--cpu-leg", default=None, help="run one CPU baseline job (child process)")
+    ap.add_argument("--skip-decode", action="store_true",
+                    help="profiling runs of the other sections: no B=1 decode and no headline (the "
+                         "printed line holds only the sections run)")
     ap.add_argument("--decode-modes", default="float,fixed",
                     help="comma list of float,fixed: the batch-1 decode modes timed (float always runs: it carries the headline)")
     args = ap.parse_args()
@@ -437,7 +440,7 @@ def main():
     ids = np.random.default_rng(1234).integers(3, 32000, 16)
     gpu_ids = None
     fixed = {}
-    for name in shapes:
+    for name in ([] if args.skip_decode else shapes):
         preset = SHAPES[name]
         p = blob_path(args.blob_dir, preset)
         for mode in [m for m in (FLOAT, FIXED_Q510) if decode_modes[m]]:
@@ -476,6 +479,9 @@ def main():
                           measure_serve(args.blob_dir, "s3", 64, 128, "fixed", 32),
                           measure_serve(args.blob_dir, "s2", 32, 512, "fixed", 32)]
 
+    if args.skip_decode:
+        print(json.dumps({"metric": METRIC, "value": None, "sections": sorted(sections), **extra}), flush=True)
+        return
     head = results["370M"]
     value = 1e6 / head["step_us"]
     kern = head["kernels"]
