@@ -242,11 +242,19 @@ __device__ __forceinline__ int32_t q510_tail(float y, float qs) {
   else if (v < -32768.0f) v = -32768.0f;
   return (v != v) ? INT32_MIN : static_cast<int32_t>(v);
 }
-// int8 absmax (tools/reference.py:131-135): q = clamp(round_half_even(y * scale_a), -128, 127)
+// v_cvt_i32_f32: rounds toward zero, saturates out-of-range inputs and gives 0 for NaN (the
+// hardware conversion, written out so that its out-of-range result is defined here).
+__device__ __forceinline__ int32_t cvt_i32_sat(float v) {
+  int32_t r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+// int8 absmax (tools/reference.py:131-135): q = clamp(round_half_even(y * scale_a), -128, 127).
+// The clamp runs on the saturated integer (one v_med3_i32): the same value as a float clamp
+// before the conversion for every input, NaN (0) included.
 __device__ __forceinline__ int32_t q8_of(float y, float sa) {
-  float v = rintf(y * sa);
-  v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
-  return static_cast<int32_t>(v);
+  const int32_t c = cvt_i32_sat(rintf(y * sa));
+  return c < -128 ? -128 : (c > 127 ? 127 : c);
 }
 
 // Argmax key: order-preserving float bits in the high word (-0 folded onto +0, which the

@@ -37,6 +37,30 @@ __device__ float block_sumsq(const float* X, int Lc, int LS, int ntail, float* r
   return s;
 }
 
+// Maximum over a block of NW full waves, one barrier: a DPP butterfly within each 16-lane
+// row, the four row maxima read out of lanes 0/16/32/48, one slot per wave in red[0 .. NW).
+// The result is uniform. red must not be written again before every thread has read it:
+// callers alternate between two areas with a barrier between their uses of either.
+template <int NW>
+__device__ float block_max1(float v, float* red) {
+  auto dpp_max = [](float x, auto ctrl) {
+    const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value, 0xf, 0xf, false);
+    return fmaxf(x, __builtin_bit_cast(float, y));
+  };
+  v = dpp_max(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  v = dpp_max(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  v = dpp_max(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  v = dpp_max(v, std::integral_constant<int, 0x140>{});  // row_mirror
+  const auto lane = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+  const float m = fmaxf(fmaxf(lane(0), lane(16)), fmaxf(lane(32), lane(48)));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
 __device__ float block_max(float v, float* red) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
@@ -294,8 +318,15 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   const int tid = threadIdx.x;
   float* X = smem;
   float* S = SW ? X + 8 * LS + 8 : X;  // silu(x2), g_norm only
-  float* red = S + 8 * LS + 8;
+  float* red = S + 8 * LS + 8;         // 32 floats: the chain partials, then two block-max areas
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // unit u -> chain j = u / L8 and first position t0: j by a multiply-high with
+  // mL8 = ceil(2^32 / L8), exact while u * L8 < 2^32 (here u < Lc <= 2048, L8 >= 2)
+  const uint32_t mL8 = 0xFFFFFFFFu / static_cast<uint32_t>(L8) + 1u;
+  auto unit_jt = [&](int u, int& j, int& t0) {
+    j = static_cast<int>(__umulhi(static_cast<uint32_t>(u), mL8));
+    t0 = 8 * (u - j * L8);
+  };
   // elements 8t .. 8t+7 of a K-long vector: two float4, or for the tail group one and zeros
   // (the tail group's second load repeats its first, an address in bounds, and is replaced by
   // zeros: a select of values, not of addresses)
@@ -328,7 +359,8 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
     if constexpr (PW) {
       const int u = tid + g * BT;
       if (u < Lc) {
-        const int j = u / L8, t0 = 8 * (u - j * L8);
+        int j, t0;
+        unit_jt(u, j, t0);
 #pragma unroll
         for (int ai = 0; ai < NA; ++ai) {
           const float4* wp = reinterpret_cast<const float4*>(a.normwT[ai] + j * Lc + t0);
@@ -424,7 +456,8 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
       for (int g = 0; g < MAXG; ++g) {
         const int u = tid + g * BT;
         if (u >= Lc) continue;
-        const int j = u / L8, t0 = 8 * (u - j * L8);
+        int j, t0;
+        unit_jt(u, j, t0);
         const float4* wp = reinterpret_cast<const float4*>(a.normwT[ai] + j * Lc + t0);
         wq[set][g][0] = wp[0];
         wq[set][g][1] = wp[1];
@@ -438,7 +471,8 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   // the BitLinear norm of unit g: y = (x * rstd) * normw (bitlinear.cpp:62-70)
   auto unit_y = [&](int ai, int g, float* y) {
     const int u = tid + g * BT;
-    const int j = u / L8, t0 = 8 * (u - j * L8);
+    int j, t0;
+    unit_jt(u, j, t0);
     const float4* xp = reinterpret_cast<const float4*>(X + j * LS + t0);
     const float4 x0 = xp[0], x1 = xp[1];
     float4 w0, w1;
@@ -465,7 +499,8 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
     // unit g's eight values out: padding positions (t >= nb) as zeros in every plane
     auto unit_out = [&](int g, const float* y, float sa) {
       const int u = tid + g * BT;
-      const int j = u / L8, t0 = 8 * (u - j * L8);
+      int j, t0;
+      unit_jt(u, j, t0);
       const int nv = nb - t0;
       if (MODE == kFloat) {
         float o[8];
@@ -486,7 +521,8 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
           h0 = pack_low4(cd);
           h1 = pack_low4(cd + 4);
         }
-        if (nv < 8) {
+        // (Int8Absmax padding codes are 0 already: zero x and normw give y = 0, or NaN -> 0)
+        if (MODE == kFixed && nv < 8) {
           const uint32_t m0 = nv >= 4 ? ~0u : (nv <= 0 ? 0u : (1u << (8 * nv)) - 1u);
           const uint32_t m1 = nv <= 4 ? 0u : (1u << (8 * (nv - 4))) - 1u;
           h0 &= m0;
@@ -514,7 +550,7 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) m = fmaxf(m, fabsf(y[g][c]));
       }
-      m = block_max(m, red);
+      m = block_max1<BT / 64>(m, red + 16 * (ai & 1));
       sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
       if (tid == 0) act.sa[ar] = sa;
 #pragma unroll
@@ -1457,7 +1493,7 @@ hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStr
   const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);
   const size_t lds = (2 * rowf + 16) * sizeof(float);
   const bool sw = a.pre == kPreSwish || a.pre == kPreMixSwish;
-  const size_t lds4 = ((sw ? 2 : 1) * rowf + 16) * sizeof(float);  // k_rowpro
+  const size_t lds4 = ((sw ? 2 : 1) * rowf + 32) * sizeof(float);  // k_rowpro
   bool fast = act.K % 4 == 0 && rowpro_fits(act) && aligned16(a.x) && (a.na == 1 || a.na == 3);
   if (a.pre != kPreNone) fast = fast && aligned16(a.pre_w);
   if (sw) fast = fast && aligned16(a.x2);
