@@ -36,6 +36,14 @@ __device__ float block_sumsq(const float* X, int Lc, int LS, int ntail, float* r
   __syncthreads();
   return s;
 }
+// The same with the ring-buffered chains (rows zero to a multiple of 32).
+__device__ float block_sumsq_ring(const float* X, int Lc, int LS, int ntail, float* red) {
+  chain_ring(X, Lc, LS, red);
+  __syncthreads();
+  const float s = chain_end(X, LS, ntail, red);
+  __syncthreads();
+  return s;
+}
 
 // Maximum over a block of NW full waves, one barrier: a DPP butterfly within each 16-lane
 // row, the four row maxima read out of lanes 0/16/32/48, one slot per wave in red[0 .. NW).
@@ -275,7 +283,7 @@ __device__ __forceinline__ float f4el(const float4& f, int c) {
 }
 
 // Waves per SIMD of the row prologue: 8 (64 VGPRs; 8 rows resident per CU, so 2048 rows run
-// in one round; chains in batches of 16 values) where what a thread keeps -- the row inputs
+// in one round; chains through a ring of 8 float4) where what a thread keeps -- the row inputs
 // and stage-1 weight through the first chain, two sets of norm weights (and the Int8
 // values, through the absmax) in the encoding -- fits without spilling, else the compiler's
 // choice.
@@ -306,7 +314,6 @@ template <int MODE, int PRE, int NA, int MAXG, bool PW, int BT>
 __global__ __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(rowpro_waves<MODE, PRE, NA, MAXG, BT>())))
 void k_rowpro(PrologueArgs a, ActBuf act) {
   extern __shared__ float smem[];
-  constexpr int CU = rowpro_waves<MODE, PRE, NA, MAXG, BT>() == 8 ? 4 : 8;  // float4 per chain batch
   constexpr bool SW = PRE == kPreSwish || PRE == kPreMixSwish, MIX = PRE == kPreMixSwish;
   constexpr int NX = SW ? 2 : 1;  // x, and x2 for the swish gate
   constexpr bool PWG = PRE != kPreNone;  // the stage-1 weight is loaded at entry with the row
@@ -429,7 +436,7 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   // norms are known
   if (tid < 64) __builtin_amdgcn_s_setprio(3);
   if (PRE != kPreNone) {
-    const float r1 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
+    const float r1 = rstd_of(block_sumsq_ring(X, Lc, LS, nt, red), K, a.eps);
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
       const int t = tid + g * BT;
@@ -465,7 +472,7 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
     }
   };
   load_w(0, 0);
-  const float r2 = rstd_of(block_sumsq<CU>(X, Lc, LS, nt, red), K, a.eps);
+  const float r2 = rstd_of(block_sumsq_ring(X, Lc, LS, nt, red), K, a.eps);
   if (tid < 64) __builtin_amdgcn_s_setprio(0);
 
   // the BitLinear norm of unit g: y = (x * rstd) * normw (bitlinear.cpp:62-70)
