@@ -140,31 +140,32 @@ __device__ inline void chain_begin(const float* X, int Lc, int LS, float* red) {
 
 // chain_begin through a ring of 8 float4 registers: a slot is refilled as soon as its four
 // values are summed, so seven LDS reads stay in flight ahead of the FMAs instead of the two
-// register sets' one batch. Reads whole rounds of 32 values (rows are zero to a multiple
-// of 32); the sums and their order are chain_begin's. The last round's refills read up to
-// 32 floats past the end of row j (row j + 1, or for row 7 the tail and the 32 floats after
-// it, which the LDS area must hold) and are never used.
-__device__ inline void chain_ring(const float* X, int Lc, int LS, float* red) {
-  if (threadIdx.x < 8) {
-    constexpr int R = 8;
-    const float4* c = reinterpret_cast<const float4*>(X + threadIdx.x * LS);
-    const int n4 = (Lc + 4 * R - 1) / (4 * R) * R;
-    float a = 0.0f;
-    float4 V[R];
+// register sets' one batch. chain_ring_part sums positions [0, n) of row j (thread j < 8)
+// onto a and returns it, reading whole rounds of 32 values (rows are zero from n to a
+// multiple of 32); the last round's refills read up to 32 floats past that (row j + 1, or
+// for row 7 the tail and the 32 floats after it, which the LDS area must hold) and are never
+// used. The sums and their order are chain_begin's.
+__device__ inline float chain_ring_part(const float* X, int n, int LS, float a) {
+  constexpr int R = 8;
+  const float4* c = reinterpret_cast<const float4*>(X + threadIdx.x * LS);
+  const int n4 = (n + 4 * R - 1) / (4 * R) * R;
+  float4 V[R];
 #pragma unroll
-    for (int k = 0; k < R; ++k) V[k] = c[k];
-    for (int b = 0; b < n4; b += R) {
+  for (int k = 0; k < R; ++k) V[k] = c[k];
+  for (int b = 0; b < n4; b += R) {
 #pragma unroll
-      for (int k = 0; k < R; ++k) {
-        a = __builtin_fmaf(V[k].x, V[k].x, a);
-        a = __builtin_fmaf(V[k].y, V[k].y, a);
-        a = __builtin_fmaf(V[k].z, V[k].z, a);
-        a = __builtin_fmaf(V[k].w, V[k].w, a);
-        V[k] = c[b + R + k];
-      }
+    for (int k = 0; k < R; ++k) {
+      a = __builtin_fmaf(V[k].x, V[k].x, a);
+      a = __builtin_fmaf(V[k].y, V[k].y, a);
+      a = __builtin_fmaf(V[k].z, V[k].z, a);
+      a = __builtin_fmaf(V[k].w, V[k].w, a);
+      V[k] = c[b + R + k];
     }
-    red[threadIdx.x] = a;
   }
+  return a;
+}
+__device__ inline void chain_ring(const float* X, int Lc, int LS, float* red) {
+  if (threadIdx.x < 8) red[threadIdx.x] = chain_ring_part(X, Lc, LS, 0.0f);
 }
 
 __device__ inline float chain_end(const float* X, int LS, int nt, const float* red) {

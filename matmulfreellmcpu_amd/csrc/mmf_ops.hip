@@ -579,6 +579,171 @@ void k_rowpro(PrologueArgs a, ActBuf act) {
   }
 }
 
+// The row prologue of long rows without a stage-1 norm (the MLP down projection's input,
+// K = 5632 or 6912: 3 or 4 groups per thread), with half of the row in LDS at a time. The
+// whole chain-transposed row takes 8 * (Lc + 4) floats (22.7 KB at K = 5632): 7 rows per CU,
+// so 2048 rows need two rounds. Here LDS holds positions [0, 512) (pass A: groups g < 2) and
+// then positions [512, Lc) (pass B): 16.7 KB, 8 rows per CU, one round. Each thread keeps its
+// groups in registers from the entry loads:
+//  - thread j < 8 sums chain j over pass A, and after the LDS holds pass B continues from the
+//    same running sum (the reference's order and rounding, as in k_rowpro);
+//  - the units of pass B are encoded from LDS, then pass A goes back into LDS and its units
+//    are encoded.
+// Unit, group and output layouts and the arithmetic are k_rowpro's (kPreNone, one
+// projection). Needs nb >= 512 and 256 * MAXG >= max(Lc, G). Float and FixedQ510 only:
+// 20.6 / 21.2 us against k_rowpro's 23.2 / 23.5 us at 2048 x 5632. (Int8Absmax, whose row
+// maximum must precede every code, measured 23.5 us against 20.7: a second pass over both
+// halves or the maximum from registers with spills.)
+template <int MODE, int MAXG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MAXG == 3 ? 8 : 1)))
+void k_rowpro_split(PrologueArgs a, ActBuf act) {
+  static_assert(MODE == kFloat || MODE == kFixed, "Int8Absmax needs the row maximum first: k_rowpro");
+  constexpr int BT = 256, P = 2 * BT;  // pass B starts at position P
+  extern __shared__ float smem[];
+  const int row = xcd_row(blockIdx.x);
+  if (row >= act.rows) return;
+  const int Lc = act.Lc, K = act.K, K8 = act.K8, nb = act.nb, nt = act.ntail, L8 = Lc / 8;
+  const int G = nb + (nt > 0 ? 1 : 0);
+  const int LS = lds_stride(P > Lc - P ? P : Lc - P);
+  const int tid = threadIdx.x;
+  float* X = smem;
+  float* red = X + 8 * LS + 8;  // chain partials [0, 8); block maximum [16, 32)
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto ld8 = [&](const float* p, int t, float4* o) {
+    const float4* p4 = reinterpret_cast<const float4*>(p) + 2 * t;
+    const float4 h = p4[t < nb ? 1 : 0];
+    o[0] = p4[0];
+    o[1] = t < nb ? h : z4;
+  };
+  const uint32_t mL8 = 0xFFFFFFFFu / static_cast<uint32_t>(L8) + 1u;  // as in k_rowpro
+  auto unit_jt = [&](int u, int& j, int& t0) {
+    j = static_cast<int>(__umulhi(static_cast<uint32_t>(u), mL8));
+    t0 = 8 * (u - j * L8);
+  };
+
+  float4 v[MAXG][2];
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g)
+    if (tid + g * BT < G) ld8(a.x + static_cast<size_t>(row) * K, tid + g * BT, v[g]);
+  // groups [g0, g1) into the LDS rows at position t - base (the tail group to the tail slots)
+  auto put = [&](int g0, int g1, int base) {
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const int t = tid + g * BT;
+      if (g < g0 || g >= g1 || t >= G) continue;
+      if (t < nb) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) X[c * LS + t - base] = f4el(v[g][c >> 2], c & 3);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c < nt) X[8 * LS + c] = f4el(v[g][c >> 2], c & 3);
+      }
+    }
+  };
+  put(0, 2, 0);
+  __syncthreads();
+  if (tid < 64) __builtin_amdgcn_s_setprio(3);
+  float acc = 0.0f;
+  if (tid < 8) acc = chain_ring_part(X, P, LS, 0.0f);
+  __syncthreads();
+  // pass B into LDS: its groups, rows zero from nb - P to a multiple of 32, the tail slots
+  auto fill_b = [&]() {
+    put(2, MAXG, P);
+    const int LB = (Lc - P + 31) / 32 * 32;
+    for (int jr = 0; jr < 8; ++jr)
+      for (int t = nb - P + tid; t < LB; t += BT) X[jr * LS + t] = 0.0f;
+    for (int t = nt + tid; t < 8; t += BT) X[8 * LS + t] = 0.0f;
+  };
+  fill_b();
+  __syncthreads();
+  if (tid < 8) red[tid] = chain_ring_part(X, Lc - P, LS, acc);
+  __syncthreads();
+  const float r2 = rstd_of(chain_end(X, LS, nt, red), K, a.eps);
+  if (tid < 64) __builtin_amdgcn_s_setprio(0);
+
+  // the norm weights of the thread's units (chain-transposed)
+  float4 wq[MAXG][2];
+  auto load_w = [&]() {
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const int u = tid + g * BT;
+      if (u >= Lc) continue;
+      int j, t0;
+      unit_jt(u, j, t0);
+      const float4* wp = reinterpret_cast<const float4*>(a.normwT[0] + j * Lc + t0);
+      wq[g][0] = wp[0];
+      wq[g][1] = wp[1];
+    }
+  };
+  load_w();
+  float* yo = act.y + static_cast<size_t>(row) * act.ystride();
+  int8_t* q = act.q + act.qoff(0, 0, row, 0);  // plane 0 of this row; plane 1 at + qplane
+  const size_t lop = act.qplane();
+  // unit g's normed values y = (x * rstd) * normw (bitlinear.cpp:62-70) from LDS position
+  // t0 - base of row j
+  auto unit_y = [&](int g, int j, int t0, int base, float* y) {
+    const float4* xp = reinterpret_cast<const float4*>(X + j * LS + t0 - base);
+    const float4 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      y[c] = (f4el(x0, c) * r2) * f4el(wq[g][0], c);
+      y[4 + c] = (f4el(x1, c) * r2) * f4el(wq[g][1], c);
+    }
+  };
+  // the units whose positions lie in [lo, hi), read from LDS at position t0 - base
+  auto encode = [&](int lo, int hi, int base) {
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const int u = tid + g * BT;
+      if (u >= Lc) continue;
+      int j, t0;
+      unit_jt(u, j, t0);
+      if (t0 < lo || t0 >= hi) continue;
+      float y[8];
+      unit_y(g, j, t0, base, y);
+      const int nv = nb - t0;
+      if (MODE == kFloat) {
+        float o[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[c] = c < nv ? y[c] : 0.0f;
+        float4* yp = reinterpret_cast<float4*>(yo + j * Lc + t0);
+        yp[0] = make_float4(o[0], o[1], o[2], o[3]);
+        yp[1] = make_float4(o[4], o[5], o[6], o[7]);
+      } else {
+        int32_t cd[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) cd[c] = q510_body(y[c], a.qs);
+        uint32_t h0, h1, l0, l1;
+        pack_split4(cd, h0, l0);
+        pack_split4(cd + 4, h1, l1);
+        if (nv < 8) {
+          const uint32_t m0 = nv >= 4 ? ~0u : (nv <= 0 ? 0u : (1u << (8 * nv)) - 1u);
+          const uint32_t m1 = nv <= 4 ? 0u : (1u << (8 * (nv - 4))) - 1u;
+          h0 &= m0;
+          h1 &= m1;
+          l0 &= m0;
+          l1 &= m1;
+        }
+        const size_t o = ActBuf::qpos(j * Lc + t0);
+        *reinterpret_cast<uint2*>(q + o) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(q + lop + o) = make_uint2(l0, l1);
+      }
+    }
+  };
+  // the tail elements, one per lane c < ntail (in the LDS tail slots from pass B on)
+  if (tid < 8) {
+    const float yt = tid < nt ? (X[8 * LS + tid] * r2) * a.normw[0][K8 + tid] : 0.0f;
+    if (MODE == kFloat) yo[8 * Lc + tid] = yt;
+    else act.ct[static_cast<size_t>(row) * 8 + tid] = tid < nt ? q510_tail(yt, a.qs) : 0;
+  }
+  encode(P, Lc, P);
+  __syncthreads();
+  put(0, 2, 0);
+  __syncthreads();
+  encode(0, P, 0);
+}
+
 // int16-range codes -> split planes (the TernaryBackend path: codes arrive quantised)
 __global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
   const int row = xcd_row(blockIdx.x), Lc = act.Lc, nb = act.nb;
@@ -1465,9 +1630,20 @@ static bool rowpro_fits(const ActBuf& act) {
   return rowpro_need(act) <= (act.rows <= kPrologueFewRows ? 2048 : 1024);
 }
 
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 template <int MODE, int PRE, int NA>
 static hipError_t rowpro_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
   const int need = rowpro_need(act), grid = row_grid(act.rows);
+  if constexpr (PRE == kPreNone && NA == 1 && MODE != kInt8) {
+    // long rows of many-row launches: half of the row in LDS at a time (k_rowpro_split)
+    if (act.rows > kPrologueFewRows && need > 512 && need <= 1024 && act.nb >= 512 && aligned16(a.normw[0])) {
+      const size_t lds_split = (8 * static_cast<size_t>(host_lds_stride(std::max(512, act.Lc - 512))) + 8 + 32) * sizeof(float);
+      if (need <= 768) k_rowpro_split<MODE, 3><<<grid, 256, lds_split, s>>>(a, act);
+      else k_rowpro_split<MODE, 4><<<grid, 256, lds_split, s>>>(a, act);
+      return hipGetLastError();
+    }
+  }
   if (act.rows <= kPrologueFewRows) {
     if (need <= 1024) k_rowpro<MODE, PRE, NA, 1, true, 1024><<<grid, 1024, lds, s>>>(a, act);
     else k_rowpro<MODE, PRE, NA, 2, true, 1024><<<grid, 1024, lds, s>>>(a, act);
@@ -1493,8 +1669,6 @@ static hipError_t rowpro_mode(const PrologueArgs& a, ActBuf& act, size_t lds, hi
   if (a.pre == kPreNone && a.na == 3) return rowpro_inst<MODE, kPreNone, 3>(a, act, lds, s);
   return hipErrorNotSupported;
 }
-
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 hipError_t launch_prologue(Mode mode, const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   const size_t rowf = static_cast<size_t>(8 * host_lds_stride(act.Lc) + 8);

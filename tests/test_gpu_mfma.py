@@ -36,6 +36,33 @@ def test_bitlinear_rows(eng, oracle, rows, K, N, mode):  # noqa: F811
     assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
 
 
+# Many-row Float and FixedQ510 prologues of long rows take the half-row LDS kernel (nb >=
+# 512; Int8Absmax keeps the whole-row kernel): 4100 (pass B is only the tail group), 4231 (a
+# 7-element tail; K % 4 != 0 takes the general prologue), 5632 and 6912 (the MLP down widths:
+# 3 and 4 groups per thread), 4104 (one position past pass A, chain rows padded to 16).
+@pytest.mark.parametrize("K", [4100, 4231, 4104, 5632, 6912])
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_bitlinear_long_rows(eng, oracle, K, mode):  # noqa: F811
+    rows, N = 600, 64
+    print(f"long-row bitlinear rows={rows} K={K} N={N} mode={mode}", flush=True)
+    rng = np.random.default_rng(K * 3 + mode)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    x[rows // 3] *= 40.0  # saturating Q5.10 codes in one row
+    x[rows // 2, : K // 2] = 0.0  # a row whose first half is zero
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, mode)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    dacc = Dev(eng, shape=(rows, N), dtype=np.int32)
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=mode, acc=dacc.ptr if mode else None)
+    eng.sync()
+    if mode:
+        np.testing.assert_array_equal(dacc.get(), want["acc"])
+    assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
+
+
 def test_cluster_rows(eng, oracle):  # noqa: F811
     rng = np.random.default_rng(55)
     rows, K, N = 70, 512, 160
