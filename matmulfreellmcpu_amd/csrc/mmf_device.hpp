@@ -287,6 +287,20 @@ __device__ __forceinline__ int32_t q8_of(float y, float sa) {
   return c < -128 ? -128 : (c > 127 ? 127 : c);
 }
 
+// a / d, correctly rounded, from y = RN(1/d) (Markstein's correction: a first quotient
+// RN(a * y), then q + r * y with the exact remainder r = fma(-d, q, a); two corrections).
+// Used for the Int8Absmax dequantisation acc / (scale_w * scale_a), where a is an integer
+// with |a| <= 2^21 and d, 1/d are normal: for 2000 divisors (the scales' range and random
+// ones over 2^-60 .. 2^60) every such a gave the quotient of the division, bit for bit,
+// already after one correction.
+__device__ __forceinline__ float div_by_recip(float a, float d, float y) {
+  float q = a * y;
+  float r = __builtin_fmaf(-d, q, a);
+  q = __builtin_fmaf(r, y, q);
+  r = __builtin_fmaf(-d, q, a);
+  return __builtin_fmaf(r, y, q);
+}
+
 // Argmax key: order-preserving float bits in the high word (-0 folded onto +0, which the
 // reference's `>` cannot tell apart), 0xFFFFFFFF - index in the low word, so the largest key
 // is the first index of the largest value (hgrn_model.cpp:270-273).

@@ -133,12 +133,17 @@ template <int MODE, int WM, int WN, int FM, int FN, int KQ>
 __host__ __device__ constexpr int stage_bytes() {
   return ((MODE == kFixed) ? 2 : 1) * FM * WM * KQ * 1024 + FN * WN * KQ * 256;
 }
+// LDS bytes of a block beside its stage ring: the int8 row divisors and their reciprocals.
+template <int MODE, int WM, int FM>
+__host__ __device__ constexpr int row_scale_bytes() {
+  return (MODE == kInt8 ? 2 : 1) * 32 * FM * WM * 4;
+}
 // Depth of the stage ring: as many slots (at most 6) as fit the LDS of the blocks a CU
 // holds (two for blocks of at most four waves, else one), with the int8 row scales.
 template <int MODE, int WM, int WN, int FM, int FN, int KQ, int KW>
 __host__ __device__ constexpr int ring_depth() {
   constexpr int per_cu = 160 * 1024, blocks = (WM * WN * KW > 4) ? 1 : 2;
-  constexpr int d = (per_cu / blocks - 32 * FM * WM * 4 - 256) / (KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>());
+  constexpr int d = (per_cu / blocks - row_scale_bytes<MODE, WM, FM>() - 256) / (KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>());
   return d > 6 ? 6 : d;
 }
 
@@ -269,7 +274,8 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   constexpr int QB = KW * SS;
   __shared__ __align__(16) unsigned char q0[QB], q1[QB], q2[QB], q3[D > 3 ? QB : 16], q4[D > 4 ? QB : 16],
       q5[D > 5 ? QB : 16];
-  __shared__ float srow[BM];  // Int8: the block's activation scales
+  __shared__ float srow[BM];  // Int8: the divisor of each row, scale_w * scale_a
+  __shared__ float srcp[MODE == kInt8 ? BM : 1];  // Int8: its correctly rounded reciprocal
   auto slot = [&](auto sc) -> unsigned char* {
     constexpr int S = decltype(sc)::value;
     if constexpr (S == 0) return q0;
@@ -356,9 +362,19 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   // reused or the block ends
   wait_lds();
   wait_vm<0>();
+  // Int8: the rows' divisors and their reciprocals. The fast epilogue divides through the
+  // reciprocal (div_by_recip: the same quotient) when the whole block allows it: |acc| <=
+  // 2^21 (K < 16384) and every divisor and reciprocal normal.
+  bool rcp_ok = false;
   if (MODE == kInt8) {
-    if (kg == 0 && wave * 64 < BM) srow[wave * 64 + lane] = sv;
-    __syncthreads();
+    bool ok = true;
+    if (kg == 0 && wave * 64 < BM) {
+      const float dn = scw * sv, y = 1.0f / dn;
+      srow[wave * 64 + lane] = dn;
+      srcp[wave * 64 + lane] = y;
+      ok = dn >= 0x1p-100f && dn <= 0x1p100f;
+    }
+    rcp_ok = __syncthreads_and(ok) && act.K < 16384;
   }
   if constexpr (KW > 1) {
     // K-group reduction: FixedQ510 folds its planes first (hi * 256 + lo into plane 1, as
@@ -442,7 +458,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
   // below measured several times slower per tile).
   const bool fast = row0 + BM <= act.rows && (cgb + BG) * 32 <= N && !accz && !rawacc && ntail == 0 &&
                     (EPI != kEpiSwigluPair || static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
-  if (fast) {
+  auto fast_epi = [&](auto use_rcp) {
 #pragma unroll
     for (int ai = 0; ai < FM; ++ai) {
       const int rbase = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5);
@@ -450,12 +466,15 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
       for (int i = 0; i < 16; ++i) {
         const int r = rbase + 8 * (i >> 2) + (i & 3);
         const size_t grow = static_cast<size_t>(r);
-        const float den = (MODE == kInt8) ? scw * srow[r - row0] : 1.0f;
+        const float den = (MODE == kInt8) ? srow[r - row0] : 1.0f;
+        const float rcp = (MODE == kInt8 && decltype(use_rcp)::value) ? srcp[r - row0] : 1.0f;
         float val[FN];
 #pragma unroll
         for (int bj = 0; bj < FN; ++bj) {
           const int32_t s = (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] + csum[bj] : acc[0][ai][bj][i];
-          val[bj] = (MODE == kFixed) ? static_cast<float>(s) * invf : static_cast<float>(s) / den;
+          if constexpr (MODE == kFixed) val[bj] = static_cast<float>(s) * invf;
+          else if constexpr (decltype(use_rcp)::value) val[bj] = div_by_recip(static_cast<float>(s), den, rcp);
+          else val[bj] = static_cast<float>(s) / den;
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -466,6 +485,10 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
         }
       }
     }
+  };
+  if (fast) {
+    if (MODE == kInt8 && rcp_ok) fast_epi(std::true_type{});
+    else fast_epi(std::false_type{});
     return;
   }
 #pragma unroll
@@ -474,7 +497,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void
     float den[16];
     if (MODE == kInt8) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) den[i] = scw * srow[rbase - row0 + 8 * (i >> 2) + (i & 3)];
+      for (int i = 0; i < 16; ++i) den[i] = srow[rbase - row0 + 8 * (i >> 2) + (i & 3)];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -609,7 +632,7 @@ template <int MODE, int EPI, int TM, int TN, int KQ, int KW>
 bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
   constexpr int WM = TM, WN = TN, FM = 2, FN = 2;
   constexpr int bytes =
-      ring_depth<MODE, WM, WN, FM, FN, KQ, KW>() * KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>() + 32 * FM * WM * 4;
+      ring_depth<MODE, WM, WN, FM, FN, KQ, KW>() * KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>() + row_scale_bytes<MODE, WM, FM>();
   if (bytes > lds_limit()) return false;
   k_mfma<MODE, EPI, WM, WN, FM, FN, KQ, KW><<<grid, dim3(64 * WM * WN * KW), 0, s>>>(a, act);
   return true;
