@@ -147,8 +147,18 @@ __host__ __device__ constexpr int ring_depth() {
   return d > 6 ? 6 : d;
 }
 
+// Minimum waves per SIMD the compiler must fit (the second launch bound): 2 for blocks of
+// up to four waves; 4 for the Int8Absmax 8-wave 128 x 256 tiles without a residual (at most
+// 128 VGPRs, so two blocks share a CU: they measured 7% slower at 136 VGPRs, one block per
+// CU); else 1.
+template <int MODE, int EPI, int WM, int WN, int KW>
+constexpr int mfma_min_waves() {
+  if (MODE == kInt8 && EPI != kEpiAdd && WM * WN == 8 && KW == 1) return 4;
+  return (WM * WN * KW > 4) ? 1 : 2;
+}
+
 template <int MODE, int EPI, int WM, int WN, int FM, int FN, int KQ, int KW>
-__global__ __launch_bounds__(64 * WM * WN * KW, (WM * WN * KW > 4) ? 1 : 2) void k_mfma(GemmArgs a, ActBuf act) {
+__global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, WN, KW>())) void k_mfma(GemmArgs a, ActBuf act) {
   constexpr int P = (MODE == kFixed) ? 2 : 1;  // activation planes
   constexpr int NW = WM * WN;                   // waves per K-group (one tile)
   constexpr int BM = 32 * FM * WM;              // rows per block
