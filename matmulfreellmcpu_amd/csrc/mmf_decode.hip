@@ -58,6 +58,9 @@ __device__ __forceinline__ void load_seg(const float* p, int l, float4 (&d)[RC],
 //   float           only part 0 runs the GEMV (a chain is one reference lane, in order); the
 //                   other parts share the loads, the normalisation and the encoding.
 //
+// W4 (float mode, not kLM): the GEMV reads the fp4 slab pk4 (8 codes per word, one conversion
+// per two codes) instead of the 2-bit slab (a byte permute per two codes into fp16 pairs).
+//
 // RC > 0 (the chain length Lc is 32 RC, no row padding): wave 0 runs both norm chains from
 // registers. Lane 8j + s holds segment s (4 RC consecutive steps) of chain j of the input
 // row and of the stage-1 weights; each chain runs segment by segment, every lane summing its
@@ -65,8 +68,9 @@ __device__ __forceinline__ void load_seg(const float* p, int l, float4 (&d)[RC],
 // step costs one dependent FMA (about 6.4 cycles) instead of an LDS round trip. Wave 0 then
 // writes the stage-1 output to LDS for the encoding pass; the row norm needs no barrier of
 // its own. RC == 0 runs the same chains over LDS rows (any Lc).
-template <int MODE, int KIND, int NV, int KS, int RC>
+template <int MODE, int KIND, int NV, int KS, int RC, bool W4>
 __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(DecArgs a) {
+  static_assert(!W4 || (MODE == kFloat && KIND != kLM), "fp4 words are for the float layer GEMVs");
   constexpr int NM = KindTraits<KIND>::NM, NA = KindTraits<KIND>::NA, NP = KindTraits<KIND>::NP;
   constexpr int BM = kBlock * NM;  // threads of one part
   constexpr int BS = BM * KS;
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   const ProjDev& Pa = a.p[KIND == kIFG ? mis : 0];
   const Geom& g0 = a.p[0].g;
   const int gN = g0.N, gK = g0.K, Lc = g0.Lc, nt = g0.ntail, Wc = g0.Wc, gng = g0.ngroups;
-  const uint32_t* const pk = Pa.pk;
+  const uint32_t* const pk = W4 ? Pa.pk4 : Pa.pk;
   const int8_t* const ptail = Pa.tail;
   const int32_t* const prowsum = Pa.rowsum;
   const float pscale = Pa.scale_w, pinv = Pa.inv_scale_w, invfx = a.inv_fixed[KIND == kIFG ? mis : 0];
@@ -121,8 +125,9 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   else
     MMF_PIN(MMF_PIN_BASE, "s"(apre), "s"(akeys));
 #undef MMF_PIN_BASE
+  const int Ww = W4 ? 2 * Wc : Wc;  // slab words per chain
   const int W = 8 * Lc + 8;  // floats of a chain-transposed vector in global memory
-  const int W4 = W / 4;
+  const int F4 = W / 4;  // float4s of a chain-transposed vector
   // LDS copies pad each chain row by 16 bytes so that the 8 chain lanes of a wave read
   // different banks: float rows LS floats apart, int8 plane rows LQ bytes apart.
   const int L32 = (Lc + 31) / 32 * 32;  // rows zero-filled to whole 32-value chain batches
@@ -219,14 +224,14 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = tid + i * BS;
-      v[s][i] = (e < W4) ? reinterpret_cast<const float4*>(src[s])[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[s][i] = (e < F4) ? reinterpret_cast<const float4*>(src[s])[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   // the weight words of the block's output groups (after the input, which the norms need
   // first): straight into LDS in the slab order, 16 bytes per lane, so one instruction of a
   // wave moves 1 KB (two slab rows); the 2 KS waves of a matrix take every 2 KS-th KB. A slab
   // of an odd number of rows ends in half a KB, which lanes 32..63 skip.
   {
-    const int nwords = Wc * 128, wv = part * 2 + (lt >> 6), lane = lt & 63;
+    const int nwords = Ww * 128, wv = part * 2 + (lt >> 6), lane = lt & 63;
     for (int gi = 0; gi < G; ++gi) {
       const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
       if (og_i >= ngroups_out) break;
@@ -284,7 +289,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = tid + i * BS;
-      if (e < W4) {
+      if (e < F4) {
         reinterpret_cast<float4*>(X)[li[i]] = v[0][i];
         if (KIND == kO) reinterpret_cast<float4*>(S)[li[i]] = v[1][i];
       }
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int e = tid + i * BS;
-        if (e < W4) {
+        if (e < F4) {
           float4 x = reinterpret_cast<float4*>(X)[li[i]];
           const float4 w = v[PW][i];
           x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
@@ -328,7 +333,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int e = tid + i * BS;
-        if (e < W4) {
+        if (e < F4) {
           const float4 x = reinterpret_cast<float4*>(X)[li[i]];
           const float4 w = v[NW0 + aa][i];
           yo[li[i]] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           const int e = tid + i * BS;
-          if (e < W4) {
+          if (e < F4) {
             const float4 x = reinterpret_cast<float4*>(X)[li[i]];
             const float4 w = v[NW0 + aa][i];
             m = fmaxf(m, fmaxf(fmaxf(fabsf((x.x * r2) * w.x), fabsf((x.y * r2) * w.y)),
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int e = tid + i * BS;
-        if (e < W4) {
+        if (e < F4) {
           const float4 x = reinterpret_cast<float4*>(X)[li[i]];
           const float4 w = v[NW0 + aa][i];
           const float y[4] = {(x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w};
@@ -398,15 +403,16 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   // One word = 16 codes of chain j against 16 activations: act_of reads the activations from
   // LDS, word_of runs the chain over them.
   struct Act {
-    float4 f[MODE == kFloat ? 4 : 1];
+    float4 f[MODE == kFloat ? (W4 ? 2 : 4) : 1];
     uint4 h, l;
   };
   auto act_of = [&](int m) {
     Act r;
     if (MODE == kFloat) {
-      const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS + 16 * m);
+      constexpr int NF = W4 ? 2 : 4;  // float4s of one word's activations
+      const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS + 4 * NF * m);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) r.f[q] = yl[q];
+      for (int q = 0; q < NF; ++q) r.f[q] = yl[q];
     } else {
       const int8_t* ql = Q + ai * 16 * LQ + j * LQ + 16 * m;
       r.h = *reinterpret_cast<const uint4*>(ql);
@@ -418,7 +424,9 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   // float in facc, integer planes in hacc / lacc.
   auto gemv = [&](int og, int gi, int m0, int m1, float& facc, int32_t& hacc, int32_t& lacc) {
     auto word_of = [&](uint32_t w, const Act& x) {
-      if (MODE == kFloat) {
+      if constexpr (W4) {
+        facc = word_dot_f4(w, x.f[0], x.f[W4 ? 1 : 0], facc);
+      } else if (MODE == kFloat) {
         const float y[16] = {x.f[0].x, x.f[0].y, x.f[0].z, x.f[0].w, x.f[1].x, x.f[1].y, x.f[1].z, x.f[1].w,
                              x.f[2].x, x.f[2].y, x.f[2].z, x.f[2].w, x.f[3].x, x.f[3].y, x.f[3].z, x.f[3].w};
         facc = word_dot_f(w, y, facc);
@@ -428,8 +436,65 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
         if (MODE == kFixed) lacc = dot4(w3, x.l.w, dot4(w2, x.l.z, dot4(w1, x.l.y, dot4(w0, x.l.x, lacc))));
       }
     };
-    if (G > 0) {  // words in LDS: 4 at a time, all their reads issued before the chain
-      const uint32_t* wl = WX + (mi * G + gi) * Wc * 128 + lt;
+    if (W4 && G > 0 && RC > 0) {
+      // fp4 words in LDS at a model width: the chain's 4 RC words fully unrolled, so the
+      // compiler issues each word's reads (one word, two float4 of activations) well ahead
+      // of its FMAs and the chain waits on no LDS round trip
+      constexpr int NC4 = RC > 0 ? RC : 1;  // chunks of 4 words (32 codes); Ww = 4 RC
+      const uint32_t* wl = WX + (mi * G + gi) * 4 * NC4 * 128 + lt;
+      const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS);
+      // chunk c + 1's reads are issued before chunk c's FMAs; the scheduling barriers keep the
+      // compiler from sinking them to their uses (it otherwise reads one float4 ahead)
+      uint32_t wa[4];
+      float4 xa[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        wa[u] = wl[u * 128];
+        xa[2 * u] = yl[2 * u];
+        xa[2 * u + 1] = yl[2 * u + 1];
+      }
+#pragma unroll
+      for (int c = 0; c < NC4; ++c) {
+        uint32_t wb[4];
+        float4 xb[8];
+        if (c + 1 < NC4) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int m = 4 * (c + 1) + u;
+            wb[u] = wl[m * 128];
+            xb[2 * u] = yl[2 * m];
+            xb[2 * u + 1] = yl[2 * m + 1];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) facc = word_dot_f4(wa[u], xa[2 * u], xa[2 * u + 1], facc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 1 < NC4) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            wa[u] = wb[u];
+            xa[2 * u] = xb[2 * u];
+            xa[2 * u + 1] = xb[2 * u + 1];
+          }
+        }
+      }
+    } else if (W4 && G > 0) {  // any other width: 4 words at a time
+      const uint32_t* wl = WX + (mi * G + gi) * Ww * 128 + lt;
+      const float4* yl = reinterpret_cast<const float4*>(Y + ai * WL + j * LS);
+      int m = m0;
+      for (; m + 4 <= m1; m += 4) {
+        const uint32_t w0 = wl[m * 128], w1 = wl[(m + 1) * 128], w2 = wl[(m + 2) * 128], w3 = wl[(m + 3) * 128];
+        const float4 a0 = yl[2 * m], a1 = yl[2 * m + 1], a2 = yl[2 * m + 2], a3 = yl[2 * m + 3];
+        const float4 a4 = yl[2 * m + 4], a5 = yl[2 * m + 5], a6 = yl[2 * m + 6], a7 = yl[2 * m + 7];
+        facc = word_dot_f4(w0, a0, a1, facc);
+        facc = word_dot_f4(w1, a2, a3, facc);
+        facc = word_dot_f4(w2, a4, a5, facc);
+        facc = word_dot_f4(w3, a6, a7, facc);
+      }
+      for (; m < m1; ++m) facc = word_dot_f4(wl[m * 128], yl[2 * m], yl[2 * m + 1], facc);
+    } else if (G > 0) {  // words in LDS: 4 at a time, all their reads issued before the chain
+      const uint32_t* wl = WX + (mi * G + gi) * Ww * 128 + lt;
       int m = m0;
       for (; m + 4 <= m1; m += 4) {
         const uint32_t w0 = wl[m * 128], w1 = wl[(m + 1) * 128], w2 = wl[(m + 2) * 128], w3 = wl[(m + 3) * 128];
@@ -441,7 +506,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
       }
       for (; m < m1; ++m) word_of(wl[m * 128], act_of(m));
     } else {  // LDS too small for the words: read them from global memory, 8 at a time
-      const uint32_t* slab = pk + static_cast<size_t>(og + mrow) * Wc * 128 + lt;
+      const uint32_t* slab = pk + static_cast<size_t>(og + mrow) * Ww * 128 + lt;
       constexpr int U = 8;
       for (int mb = m0; mb < m1; mb += U) {
         uint32_t w[U];
@@ -485,7 +550,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
          gi += KS, og += KS * static_cast<int>(gridDim.x)) {
       float facc = 0.0f;
       int32_t hacc = 0, lacc = 0;
-      gemv(og, gi, 0, Wc, facc, hacc, lacc);
+      gemv(og, gi, 0, Ww, facc, hacc, lacc);
       const int o = og * kGroup + ol;
       int32_t sum = 0;
       if (MODE == kFloat) {
@@ -521,7 +586,7 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
     float facc = 0.0f;
     int32_t hacc = 0, lacc = 0;
     if (KSPLIT) gemv(og, 0, part * Wc / KS, (part + 1) * Wc / KS, facc, hacc, lacc);
-    else if (part == 0) gemv(og, 0, 0, Wc, facc, hacc, lacc);
+    else if (part == 0) gemv(og, 0, 0, Ww, facc, hacc, lacc);
     int32_t sum = 0;
     if (MODE == kFloat) {
       facc = hsum8_lanes(facc);
@@ -578,59 +643,62 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
 template <int MODE, int KIND>
 constexpr int kParts = (MODE == kFloat) ? 1 : ((KIND == kO || KIND == kDown) ? 4 : 2);
 
-constexpr int nv_for(int W4, int BS) { return W4 <= 2 * BS ? 2 : (W4 <= 4 * BS ? 4 : (W4 <= 8 * BS ? 8 : 16)); }
+constexpr int nv_for(int F4, int BS) { return F4 <= 2 * BS ? 2 : (F4 <= 4 * BS ? 4 : (F4 <= 8 * BS ? 8 : 16)); }
 
-template <int MODE, int KIND, int KS, int RC>
+template <int MODE, int KIND, int KS, int RC, bool W4>
 hipError_t dec_rc(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
   constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
-  constexpr int W4 = (8 * 32 * RC + 8) / 4;
-  static_assert(W4 <= 16 * BS, "row too long for the block layout");
-  k_decode<MODE, KIND, nv_for(W4, BS), KS, RC><<<grid, BS, lds, s>>>(a);
+  constexpr int F4 = (8 * 32 * RC + 8) / 4;  // float4s of a chain-transposed vector
+  static_assert(F4 <= 16 * BS, "row too long for the block layout");
+  k_decode<MODE, KIND, nv_for(F4, BS), KS, RC, W4><<<grid, BS, lds, s>>>(a);
   return hipGetLastError();
 }
 
-template <int MODE, int KIND, int KS>
+template <int MODE, int KIND, int KS, bool W4>
 hipError_t dec_ks(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
   constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
   const int Lc = a.p[0].g.Lc;
   if (Lc % 32 == 0) {  // register chains at the model widths: H 1024/2048/2560, I 2816/5632/6912
     if constexpr (KIND == kDown) {
       switch (Lc / 32) {
-        case 11: return dec_rc<MODE, KIND, KS, 11>(a, lds, grid, s);
-        case 22: return dec_rc<MODE, KIND, KS, 22>(a, lds, grid, s);
-        case 27: return dec_rc<MODE, KIND, KS, 27>(a, lds, grid, s);
+        case 11: return dec_rc<MODE, KIND, KS, 11, W4>(a, lds, grid, s);
+        case 22: return dec_rc<MODE, KIND, KS, 22, W4>(a, lds, grid, s);
+        case 27: return dec_rc<MODE, KIND, KS, 27, W4>(a, lds, grid, s);
         default: break;
       }
     } else {
       switch (Lc / 32) {
-        case 4: return dec_rc<MODE, KIND, KS, 4>(a, lds, grid, s);
-        case 8: return dec_rc<MODE, KIND, KS, 8>(a, lds, grid, s);
-        case 10: return dec_rc<MODE, KIND, KS, 10>(a, lds, grid, s);
+        case 4: return dec_rc<MODE, KIND, KS, 4, W4>(a, lds, grid, s);
+        case 8: return dec_rc<MODE, KIND, KS, 8, W4>(a, lds, grid, s);
+        case 10: return dec_rc<MODE, KIND, KS, 10, W4>(a, lds, grid, s);
         default: break;
       }
     }
   }
-  const int W4 = (8 * Lc + 8) / 4;
-  if (W4 <= 2 * BS) k_decode<MODE, KIND, 2, KS, 0><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 4 * BS) k_decode<MODE, KIND, 4, KS, 0><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 8 * BS) k_decode<MODE, KIND, 8, KS, 0><<<grid, BS, lds, s>>>(a);
-  else if (W4 <= 16 * BS) k_decode<MODE, KIND, 16, KS, 0><<<grid, BS, lds, s>>>(a);
+  const int F4 = (8 * Lc + 8) / 4;
+  if (F4 <= 2 * BS) k_decode<MODE, KIND, 2, KS, 0, W4><<<grid, BS, lds, s>>>(a);
+  else if (F4 <= 4 * BS) k_decode<MODE, KIND, 4, KS, 0, W4><<<grid, BS, lds, s>>>(a);
+  else if (F4 <= 8 * BS) k_decode<MODE, KIND, 8, KS, 0, W4><<<grid, BS, lds, s>>>(a);
+  else if (F4 <= 16 * BS) k_decode<MODE, KIND, 16, KS, 0, W4><<<grid, BS, lds, s>>>(a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 template <int MODE, int KIND>
-hipError_t dec_kind(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
+hipError_t dec_kind(const DecArgs& a, size_t lds, int grid, bool w4, hipStream_t s) {
   if constexpr (KIND == kLM) {
     switch (a.wgroups) {  // one part per group held in LDS, at most 4
       case 0:
-      case 1: return dec_ks<MODE, KIND, 1>(a, lds, grid, s);
-      case 2: return dec_ks<MODE, KIND, 2>(a, lds, grid, s);
-      case 3: return dec_ks<MODE, KIND, 3>(a, lds, grid, s);
-      default: return dec_ks<MODE, KIND, 4>(a, lds, grid, s);
+      case 1: return dec_ks<MODE, KIND, 1, false>(a, lds, grid, s);
+      case 2: return dec_ks<MODE, KIND, 2, false>(a, lds, grid, s);
+      case 3: return dec_ks<MODE, KIND, 3, false>(a, lds, grid, s);
+      default: return dec_ks<MODE, KIND, 4, false>(a, lds, grid, s);
     }
+  } else if constexpr (MODE == kFloat) {
+    if (w4) return dec_ks<MODE, KIND, kParts<MODE, KIND>, true>(a, lds, grid, s);
+    return dec_ks<MODE, KIND, kParts<MODE, KIND>, false>(a, lds, grid, s);
   } else {
-    return dec_ks<MODE, KIND, kParts<MODE, KIND>>(a, lds, grid, s);
+    return dec_ks<MODE, KIND, kParts<MODE, KIND>, false>(a, lds, grid, s);
   }
 }
 
@@ -653,16 +721,24 @@ hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
   const int nm = kind == kIFG ? 3 : (kind == kGate ? 2 : 1);
   const int G = (kind == kLM) ? (((nout + kGroup - 1) / kGroup) + grid - 1) / grid : 1;
   const size_t wx = static_cast<size_t>(nm) * G * g.Wc * 128 * sizeof(uint32_t);
-  if (lds + wx <= static_cast<size_t>(lds_limit())) {
+  // float layer GEMVs: the fp4 slab (twice the words) when every matrix has one and its words
+  // fit in LDS beside the rest; otherwise the 2-bit slab
+  bool w4 = MODE == kFloat && kind != kLM;
+  for (int z = 0; z < nm; ++z) w4 = w4 && a.p[z].pk4 != nullptr;
+  w4 = w4 && lds + 2 * wx <= static_cast<size_t>(lds_limit());
+  if (w4) {
+    b.wgroups = G;
+    lds += 2 * wx;
+  } else if (lds + wx <= static_cast<size_t>(lds_limit())) {
     b.wgroups = G;
     lds += wx;
   }
   switch (kind) {
-    case kIFG: return dec_kind<MODE, kIFG>(b, lds, grid, s);
-    case kO: return dec_kind<MODE, kO>(b, lds, grid, s);
-    case kGate: return dec_kind<MODE, kGate>(b, lds, grid, s);
-    case kDown: return dec_kind<MODE, kDown>(b, lds, grid, s);
-    default: return dec_kind<MODE, kLM>(b, lds, grid, s);
+    case kIFG: return dec_kind<MODE, kIFG>(b, lds, grid, w4, s);
+    case kO: return dec_kind<MODE, kO>(b, lds, grid, w4, s);
+    case kGate: return dec_kind<MODE, kGate>(b, lds, grid, w4, s);
+    case kDown: return dec_kind<MODE, kDown>(b, lds, grid, w4, s);
+    default: return dec_kind<MODE, kLM>(b, lds, grid, false, s);
   }
 }
 

@@ -58,6 +58,28 @@ __device__ __forceinline__ float word_dot_f(uint32_t w, const float (&y)[16], fl
   return acc;
 }
 
+// An fp4 word (8 codes, code t in nibble t as an E2M1 value: 0x0 = 0, 0x2 = +1, 0xA = -1)
+// against 8 activations, acc = fma(y_t, w_t, acc) for t = 0..7: each
+// v_cvt_scalef32_pk_f32_fp4 (scale 1) turns byte b into the exact fp32 codes 2b and 2b + 1,
+// so a code costs one FMA and half a conversion. The product y_t * w_t is exact and each step
+// rounds once, as the reference's fmadd lane does.
+typedef float mmf_float2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float word_dot_f4(uint32_t w, const float4& a, const float4& b, float acc) {
+  const mmf_float2 c0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+  const mmf_float2 c1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+  const mmf_float2 c2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+  const mmf_float2 c3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  acc = __builtin_fmaf(a.x, c0.x, acc);
+  acc = __builtin_fmaf(a.y, c0.y, acc);
+  acc = __builtin_fmaf(a.z, c1.x, acc);
+  acc = __builtin_fmaf(a.w, c1.y, acc);
+  acc = __builtin_fmaf(b.x, c2.x, acc);
+  acc = __builtin_fmaf(b.y, c2.y, acc);
+  acc = __builtin_fmaf(b.z, c3.x, acc);
+  acc = __builtin_fmaf(b.w, c3.y, acc);
+  return acc;
+}
+
 // weights t = 4i..4i+3 as four int8 lanes: v_perm_b32 with the byte table {0, +1, 0, -1}
 __device__ __forceinline__ uint32_t w4_i8(uint32_t w, int i) {
   return __builtin_amdgcn_perm(0u, 0xFF000100u, (w >> (2 * i)) & 0x03030303u);

@@ -68,7 +68,8 @@ struct DBuf {
 
 struct Proj {
   ProjDev d;
-  void* mem = nullptr;  // pk | tail | rowsum | normw in one allocation
+  void* mem = nullptr;   // pk | tail | rowsum | normw in one allocation
+  void* mem4 = nullptr;  // pk4 (float-mode models only)
 };
 
 struct DevTensor {
@@ -247,6 +248,14 @@ int register_proj(mmf_ctx* c, const int8_t* wq_dev, size_t N, size_t K, float sc
   MMF_HIP(launch_pack_mfma(P.d.pk, g, false, const_cast<uint32_t*>(P.d.pkm), c->stream));
   c->projs.push_back(P);
   return static_cast<int>(c->projs.size() - 1);
+}
+
+// The fp4 slab of a projection for the float-mode decode kernels, built once from its 2-bit slab.
+void ensure_pk4(mmf_ctx* c, Proj& P) {
+  if (P.d.pk4) return;
+  MMF_HIP(hipMalloc(&P.mem4, pk4_words(P.d.g) * 4));
+  MMF_HIP(launch_pack4(P.d.pk, P.d.g, static_cast<uint32_t*>(P.mem4), c->stream));
+  P.d.pk4 = static_cast<const uint32_t*>(P.mem4);
 }
 
 void tbeg(mmf_ctx* c, int kind) {
@@ -955,7 +964,10 @@ void mmf_destroy(mmf_ctx* c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   drop_graph(c->model);
-  for (auto& p : c->projs) (void)hipFree(p.mem);
+  for (auto& p : c->projs) {
+    (void)hipFree(p.mem);
+    if (p.mem4) (void)hipFree(p.mem4);
+  }
   for (auto& kv : c->model.tensors)
     if (kv.second.p) (void)hipFree(kv.second.p);
   Model& m = c->model;
@@ -1036,6 +1048,7 @@ int mmf_proj_update(mmf_ctx* c, int id, const int8_t* wq) {
     if (e == hipErrorInvalidValue) fail(MMF_ERR_ARG, "projection weights must be ternary (-1, 0, +1)");
     MMF_HIP(e);
     MMF_HIP(launch_pack_mfma(P.d.pk, g, P.d.pair != 0, const_cast<uint32_t*>(P.d.pkm), c->stream));
+    if (P.d.pk4) MMF_HIP(launch_pack4(P.d.pk, g, const_cast<uint32_t*>(P.d.pk4), c->stream));
   });
 }
 
@@ -1394,6 +1407,9 @@ int mmf_model_finalize(mmf_ctx* c, int mode, int frac) {
       Ld.gnT = tr(Ld.gn, false);
       for (int j = 0; j < 6; ++j) c->projs[Ld.proj[j]].d.normwT = tr(c->projs[Ld.proj[j]].d.normw, j == 5);
     }
+    if (mode == kFloat)  // the batch-1 float GEMVs read fp4 codes (one conversion per two codes)
+      for (size_t l = 0; l < L; ++l)
+        for (int j = 0; j < 6; ++j) ensure_pk4(c, c->projs[m.layers[l].proj[j]]);
     m.mode = mode;
     m.frac = frac;
     m.qs = static_cast<float>(1u << frac);

@@ -48,6 +48,7 @@ __host__ __device__ inline Geom make_geom(int N, int K) {
 struct ProjDev {
   const uint32_t* pk = nullptr;
   const uint32_t* pkm = nullptr;  // the same words in the matrix-core tile order (mmf_mfma.hip)
+  const uint32_t* pk4 = nullptr;  // float-mode decode: the slab with fp4 codes (launch_pack4), or null
   int pair = 0;                   // pkm interleaves the two halves (MLP gate/up) by 32-column group
   const int8_t* tail = nullptr;
   const int32_t* rowsum = nullptr;
@@ -269,5 +270,10 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
 size_t pkm_words(const Geom& g);
 bool pkm_pairable(const Geom& g);
 hipError_t launch_pack_mfma(const uint32_t* pk, const Geom& g, bool pair, uint32_t* pkm, hipStream_t s);
+// slab words -> the fp4 slab of the float-mode decode GEMV: the same groups and lanes with 8 codes
+// per word (2 Wc words per chain, code t of a word in nibble t: 0 -> 0x0, +1 -> 0x2, -1 -> 0xA,
+// E2M1 values that v_cvt_scalef32_pk_f32_fp4 converts exactly); pk4 holds pk4_words(g) words.
+size_t pk4_words(const Geom& g);
+hipError_t launch_pack4(const uint32_t* pk, const Geom& g, uint32_t* pk4, hipStream_t s);
 
 }  // namespace mmf

@@ -139,6 +139,29 @@ __global__ void k_pack(const int8_t* __restrict__ wq, Geom g, uint32_t* __restri
   }
 }
 
+// 2-bit slab -> fp4 slab (float-mode decode): word m of a chain in pk (16 codes) becomes words
+// 2m and 2m + 1 of pk4 (codes 0..7 and 8..15), code t of a word in nibble t as an E2M1 value
+// (0 -> 0x0, +1 -> 0x2, -1 -> 0xA; all exact), so one v_cvt_scalef32_pk_f32_fp4 turns byte b
+// into the fp32 codes 2b and 2b + 1.
+__global__ void k_pack4(const uint32_t* __restrict__ pk, size_t nwords, int Wc, uint32_t* __restrict__ pk4) {
+  for (size_t w = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; w < nwords;
+       w += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint32_t src = pk[w];
+    const size_t gm = w >> 7;  // og * Wc + m
+    const size_t og = gm / Wc, m = gm % Wc;
+    const size_t lane = w & 127;
+    uint32_t half[2] = {0u, 0u};
+    for (int t = 0; t < 16; ++t) {
+      const uint32_t c = (src >> code_shift(t)) & 3u;
+      const uint32_t n = c == 1u ? 0x2u : (c == 3u ? 0xAu : 0x0u);
+      half[t >> 3] |= n << (4 * (t & 7));
+    }
+    const size_t base = ((og * 2 * Wc + 2 * m) << 7) + lane;
+    pk4[base] = half[0];
+    pk4[base + 128] = half[1];
+  }
+}
+
 // Per output row (one block each, rows padded to whole groups): the exact int32 sum of the
 // body codes (order-free) and the tail codes. One thread per row walking K codes in turn
 // took 0.7 ms for a 5632 x 1024 matrix; a block reads the row in 256-byte steps.
@@ -1623,6 +1646,15 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
   (void)hipFree(bad);
   if (e == hipSuccess && hbad) return hipErrorInvalidValue;
   return e;
+}
+
+size_t pk4_words(const Geom& g) { return static_cast<size_t>(g.ngroups) * 2 * g.Wc * kGroup * 8; }
+
+hipError_t launch_pack4(const uint32_t* pk, const Geom& g, uint32_t* pk4, hipStream_t s) {
+  const size_t nwords = static_cast<size_t>(g.ngroups) * g.Wc * kGroup * 8;
+  const int blocks = static_cast<int>(std::min<size_t>((nwords + 255) / 256, 65536));
+  k_pack4<<<blocks, 256, 0, s>>>(pk, nwords, g.Wc, pk4);
+  return hipGetLastError();
 }
 
 static int host_lds_stride(int Lc) { return (Lc + 31) / 32 * 32 + 4; }
