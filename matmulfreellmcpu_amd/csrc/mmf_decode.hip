@@ -19,6 +19,8 @@
 //    grid-wide synchronisation is needed inside a launch.
 // Thread (ol, j) of a matrix's 128 threads sums chain j of output og*16+ol, which is the
 // reference's AVX2 lane j (16 outputs x 8 chains per output group).
+#include <cstdlib>
+
 #include "mmf_device.hpp"
 #include "mmf_internal.hpp"
 
@@ -637,6 +639,273 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   }
 }
 
+// Float-mode layer kinds (kIFG, kO, kGate, kDown) at the model widths (chain length Lc = 32 RC),
+// with no barrier before the GEMV. A block is NM waves, wave mi holding matrix mi for the 8
+// outputs 8 blockIdx.x + ol (half of a 16-output slab group): lane 8 ol + j runs the
+// reference's lane chain j of output ol. Every wave works on its own:
+//  * it loads its lane segments of the input row, the stage-1 weight (kO: and silu of the
+//    recurrence) and its matrix's BitLinear norm weight (lane 8j + s: segment s of chain j);
+//    the pointers of these first loads are the leading kernel parameters, which the launch
+//    preloads into scalar registers, so the loads do not wait for the argument block;
+//  * it copies its own slab words (64 per word row, fp4) into its own LDS slice by DMA;
+//  * it runs both norm chains from registers (a DPP row shift hands each running sum to the
+//    next segment's lane), the same sums in the same order in every wave, and encodes its
+//    activation row y = (x * r2) * w into its own LDS slice from registers;
+//  * it waits for its own DMA and runs its 64 chains over fp4 words.
+// Only the epilogue of the multi-matrix kinds meets in LDS (one barrier). Outputs, epilogues
+// and the layer-0 token gather are k_decode's.
+template <int KIND, int RC>
+__global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float* __restrict__ xin,
+                                                                   const float* __restrict__ prew,
+                                                                   const float* __restrict__ xg,
+                                                                   const float* __restrict__ nwa,
+                                                                   const float* __restrict__ nwb,
+                                                                   const float* __restrict__ nwc, DecArgs a) {
+  static_assert(KIND != kLM, "the lm_head runs k_decode");
+  constexpr int NM = KindTraits<KIND>::NM;
+  constexpr int Lc = 32 * RC, LS = Lc + 4, WL = 8 * LS + 8, NW = 4 * RC;  // NW fp4 words per chain
+  constexpr int SLICE = WL + NW * 64;                                       // floats of a wave's LDS slice
+  extern __shared__ float smem[];
+  const int mi = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave = matrix
+  const int lane = threadIdx.x & 63, ol = lane >> 3, j = lane & 7;
+  float* Y = smem + mi * SLICE;
+  uint32_t* WXw = reinterpret_cast<uint32_t*>(Y + WL);
+  float* vals = smem + NM * SLICE;  // [NM][8]
+  const ProjDev& Pa = a.p[KIND == kIFG ? mi : 0];
+  const Geom& g0 = a.p[0].g;
+  const int gK = g0.K, nt = g0.ntail, gN = g0.N, gng = g0.ngroups;
+  const uint32_t* const pk = Pa.pk4;
+  const int8_t* const ptail = Pa.tail;
+  const float pinv = Pa.inv_scale_w;
+  const float aeps = a.eps;
+  const int nout = (KIND == kGate) ? gN / 2 : gN;
+  const int W = 8 * Lc + 8;
+
+  // layer 0: the token is the argmax over the previous lm_head's per-block keys (every wave
+  // reduces all keys itself)
+  const float* src0 = xin;
+  if (KIND == kIFG && xin == nullptr) {
+    const unsigned long long* keys = a.keys;
+    const int nkeys = a.nkeys;
+    unsigned long long best = 0ull;
+    for (int e0 = lane; e0 < nkeys; e0 += 8 * 64) {
+      unsigned long long k[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) k[u] = e0 + u * 64 < nkeys ? keys[e0 + u * 64] : 0ull;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) best = k[u] > best ? k[u] : best;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const unsigned long long other = __shfl_xor(best, off);
+      best = other > best ? other : best;
+    }
+    int64_t tok = key_index(best);
+    if (tok < 0 || tok >= a.vocab) tok = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.hist) {
+      const int pos = *a.hist_pos;
+      if (pos < a.hist_cap) a.hist[pos] = tok;
+      *a.hist_pos = pos + 1;
+    }
+    src0 = a.embT + static_cast<size_t>(tok) * W;
+  }
+  // ---- this wave's lane segments (independent of the argument block except at layer 0) ------
+  float4 xs[RC], ws[RC], gs[RC], ns[RC];
+  float xt[8], wt[8], gt[8], nt8[8];
+  load_seg<RC>(src0, lane, xs, xt);
+  if constexpr (KIND != kDown) load_seg<RC>(prew, lane, ws, wt);
+  if constexpr (KIND == kO) load_seg<RC>(xg, lane, gs, gt);
+  load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
+  // these loads issue first: nothing below (the DMA addresses need argument-block fields) may
+  // move above them
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- this wave's slab words: rows m of the half group, 4 rows of 64 words per DMA ---------
+  {
+    const int og = static_cast<int>(blockIdx.x) >> 1, h = static_cast<int>(blockIdx.x) & 1;
+    const int mrow = (KIND == kGate && mi == 1) ? gng / 2 : 0;  // gate: the up half
+    const uint32_t* sw = pk + static_cast<size_t>(og + mrow) * NW * 128 + 64 * h;
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const int m = 4 * c + (lane >> 4);
+      __builtin_amdgcn_global_load_lds(sw + m * 128 + 4 * (lane & 15), (lds_void*)(WXw + 4 * c * 64), 16, 0, 0);
+    }
+  }
+  // ---- epilogue operands (lanes j == 0 of wave 0) ---------------------------------------------
+  const int o = 8 * static_cast<int>(blockIdx.x) + ol;
+  const bool epi = mi == 0 && j == 0 && o < nout;
+  const int po = epi ? ((o < a.oK8) ? (o & 7) * a.oLc + (o >> 3) : 8 * a.oLc + (o - a.oK8)) : 0;
+  float e_lb = 0.0f, e_st = 0.0f, e_hin = 0.0f;
+  if (epi) {
+    if (KIND == kIFG) {
+      if (a.lb) e_lb = a.lb[o];
+      e_st = a.state[o];
+    }
+    if (KIND == kO || KIND == kDown) e_hin = a.hin[po];
+  }
+  // ---- both norm chains in every wave, then this wave's activation row -----------------------
+  if constexpr (KIND != kDown) {
+    const float r1 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      float4 x = xs[c];
+      const float4 w = ws[c];
+      x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
+      if (KIND == kO) {
+        const float4 sg = gs[c];
+        x.x = x.x * sg.x; x.y = x.y * sg.y; x.z = x.z * sg.z; x.w = x.w * sg.w;
+      }
+      xs[c] = x;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xt[t] = (xt[t] * r1) * wt[t];
+      if (KIND == kO) xt[t] = xt[t] * gt[t];
+    }
+  }
+  const float r2 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
+  {
+    // lane 8c + s holds segment s of chain c: row c, floats [4 RC s, 4 RC (s + 1))
+    float4* yr = reinterpret_cast<float4*>(Y + (lane >> 3) * LS + 4 * RC * (lane & 7));
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const float4 x = xs[c], w = ns[c];
+      yr[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) Y[8 * LS + t] = (xt[t] * r2) * nt8[t];
+    }
+  }
+  // the wave's own DMA and LDS writes are complete before any of its lanes reads them
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- GEMV: chunks of 4 fp4 words, the reads of chunk c + 1 issued before chunk c's FMAs ----
+  float facc = 0.0f;
+  {
+    const uint32_t* wl = WXw + lane;
+    const float4* yl = reinterpret_cast<const float4*>(Y + j * LS);
+    uint32_t wa[4];
+    float4 xa[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      wa[u] = wl[u * 64];
+      xa[2 * u] = yl[2 * u];
+      xa[2 * u + 1] = yl[2 * u + 1];
+    }
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      uint32_t wb[4];
+      float4 xb[8];
+      if (c + 1 < RC) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int m = 4 * (c + 1) + u;
+          wb[u] = wl[m * 64];
+          xb[2 * u] = yl[2 * m];
+          xb[2 * u + 1] = yl[2 * m + 1];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) facc = word_dot_f4(wa[u], xa[2 * u], xa[2 * u + 1], facc);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < RC) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          wa[u] = wb[u];
+          xa[2 * u] = xb[2 * u];
+          xa[2 * u + 1] = xb[2 * u + 1];
+        }
+      }
+    }
+  }
+  facc = hsum8_lanes(facc);  // lane j == 0: the 8 chains of output ol in the hsum_ps order
+  float val = 0.0f;
+  if (j == 0 && o < nout) {
+    const int oo = o + ((KIND == kGate && mi == 1) ? nout : 0);
+    float s = facc;
+    const float* yt = Y + 8 * LS;
+    for (int t = 0; t < nt; ++t) {
+      const int8_t w8 = ptail[oo * 8 + t];
+      if (w8 > 0) s += yt[t];
+      else if (w8 < 0) s -= yt[t];
+    }
+    val = s * pinv;
+  }
+  float v1 = 0.0f, v2 = 0.0f;
+  if constexpr (NM > 1) {  // the other matrices' results for the same outputs
+    if (j == 0) vals[mi * 8 + ol] = val;
+    __syncthreads();
+    v1 = vals[8 + ol];
+    if (NM > 2) v2 = vals[16 + ol];
+  }
+  if (!epi) return;
+  const int p = po;
+  if (KIND == kIFG) {
+    const int aH = a.H;
+    const bool tl = o >= (aH & ~7);
+    float f = sigmoid_of(v1, tl);
+    if (a.lb) f = __builtin_fmaf(1.0f - e_lb, f, e_lb);
+    const float in = swiglu_of(val, 1.0f - f, tl);
+    const float s = __builtin_fmaf(f, e_st, in);
+    a.state[o] = s;
+    a.recur[p] = silu_of(s, tl);
+    a.gout[p] = v2;
+    if (a.out) a.out[p] = src0[p];  // layer 0: the embedding row becomes h
+  } else if (KIND == kO || KIND == kDown) {
+    a.out[p] = e_hin + val;
+  } else {  // kGate
+    a.out[p] = swiglu_of(val, v1, o >= (nout & ~7));
+  }
+}
+
+template <int KIND, int RC>
+hipError_t decf_rc(const DecArgs& a, hipStream_t s) {
+  constexpr int NM = KindTraits<KIND>::NM;
+  constexpr int Lc = 32 * RC, WL = 8 * (Lc + 4) + 8, NW = 4 * RC;
+  const size_t lds = (static_cast<size_t>(NM) * (WL + NW * 64) + NM * 8) * sizeof(float);
+  const int nout = (KIND == kGate) ? a.p[0].g.N / 2 : a.p[0].g.N;
+  const int grid = (nout + 7) / 8;
+  const float* prew = (KIND == kDown) ? nullptr : a.pre_w;
+  const float* xg = (KIND == kO) ? a.x2 : nullptr;
+  k_decf<KIND, RC><<<grid, 64 * NM, lds, s>>>(a.x, prew, xg, a.p[0].normwT, a.p[1].normwT, a.p[2].normwT, a);
+  return hipGetLastError();
+}
+
+// k_decf for a float layer kind when every matrix has its fp4 slab and the width is a model
+// width; hipErrorNotSupported (nothing launched) otherwise.
+// i/f/g runs it up to hidden size 2048: at 2560 its three waves' own loads of three 10 KB
+// vectors (320 blocks) cost more than k_decode's barriers (measured 9.3 -> 10.1 us per launch).
+// o and down run it at every width.
+template <int KIND>
+hipError_t decf_kind(const DecArgs& a, hipStream_t s) {
+  constexpr int NP = (KIND == kIFG) ? 3 : 1;  // projections (the gate matrix holds gate and up)
+  for (int z = 0; z < NP; ++z)
+    if (!a.p[z].pk4 || !a.p[z].normwT) return hipErrorNotSupported;
+  const int Lc = a.p[0].g.Lc;
+  if (Lc % 32 != 0 || a.p[0].g.Wc * 2 != Lc / 8) return hipErrorNotSupported;
+  if (KIND == kIFG && Lc > 256) return hipErrorNotSupported;
+  // gate/up stays on k_decode: with 2I outputs it takes 352 to 864 blocks, and their own
+  // loads cost more than the barriers saved (370M 4.9 -> 5.0, 2.7B 10.0 -> 13.7 us per launch)
+  if (KIND == kGate) return hipErrorNotSupported;
+  if constexpr (KIND == kDown) {
+    switch (Lc / 32) {
+      case 11: return decf_rc<KIND, 11>(a, s);
+      case 22: return decf_rc<KIND, 22>(a, s);
+      case 27: return decf_rc<KIND, 27>(a, s);
+      default: return hipErrorNotSupported;
+    }
+  } else {
+    switch (Lc / 32) {
+      case 4: return decf_rc<KIND, 4>(a, s);
+      case 8: return decf_rc<KIND, 8>(a, s);
+      case 10: return decf_rc<KIND, 10>(a, s);
+      default: return hipErrorNotSupported;
+    }
+  }
+}
+
 // Parts per block (see k_decode): integer modes split each chain's words over 2 (i/f/g,
 // gate/up) or 4 (o, down) parts; float keeps one part, except that the lm_head runs its groups
 // side by side in every mode.
@@ -702,8 +971,29 @@ hipError_t dec_kind(const DecArgs& a, size_t lds, int grid, bool w4, hipStream_t
   }
 }
 
+// MMF_DECF=0 keeps the float layer kinds on k_decode (for comparisons); default on.
+bool decf_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("MMF_DECF");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 template <int MODE>
 hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
+  if constexpr (MODE == kFloat) {
+    if (kind != kLM && decf_enabled()) {
+      hipError_t e = hipErrorNotSupported;
+      switch (kind) {
+        case kIFG: e = decf_kind<kIFG>(a, s); break;
+        case kO: e = decf_kind<kO>(a, s); break;
+        case kGate: e = decf_kind<kGate>(a, s); break;
+        default: e = decf_kind<kDown>(a, s); break;
+      }
+      if (e != hipErrorNotSupported) return e;
+    }
+  }
   const Geom& g = a.p[0].g;
   const int Lc = g.Lc;
   const int na = kind == kIFG ? 3 : 1;
