@@ -9,16 +9,20 @@ and after). The 1.3B and 2.7B shapes are reported beside it (`decode_tok_s`).
 
 roofline: the decode kernel with the most time per token, its algorithmic bytes per launch
 (2-bit packed weights + the fp32 vectors it must read and write once) over its average
-launch duration, measured with an event pair around each launch; peak = 8 TB/s HBM.
+launch duration, measured with an event pair around each launch (a child process with HIP
+graphs off, MMF_GRAPH=0: `bench.py --roofline-leg`, the command the committed rocprofv3
+summary traces); peak = 8 TB/s HBM. `traffic` (HBM bytes per launch from the calibrated
+FETCH_SIZE/WRITE_SIZE runs in profiles/pmc_traffic.json) is written only while the digest of
+the decode kernel sources recorded there matches the sources in this tree.
 
 cpu_baseline: the reference engine compiled from its own sources (oracle/_ref/mmfree-cli,
 built by oracle/Makefile) timed on this host's cores with its own --bench harness on the
 same blob and prompt, on one socket's physical cores (OMP_PROC_BIND=close, one place per
 core; `all_cpus`: every cpu this process may use); its greedy id stream is also compared
-with the GPU's. `cpu_baselines` holds the same reference beside the other workloads, on
-bounded samples that each entry names: the op sweep's integer matmul (CpuBackend), the
-1.3B prefill and decode (a 64-token prompt), and two lockstep serving steps per serving
-configuration.
+with the GPU's at every shape and mode (`parity`). `cpu_baselines` holds the same reference
+beside the other workloads, each entry naming what was timed: the op sweep's integer matmul
+(CpuBackend), the 1.3B prefill of 2048 tokens and decode of 256 (in full, as the reference's
+own --bench harness runs it), and two lockstep serving steps per serving configuration.
 
 Beside the headline (all on seeded synthetic weights of the named shapes):
   op_sweep  BitLinear with int8-absmax activations: x ~N(0,1) [M, K], M in {1, 16, 256,
@@ -43,6 +47,7 @@ Beside the headline (all on seeded synthetic weights of the named shapes):
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import re
@@ -60,6 +65,18 @@ HBM_PEAK_GBS = 8000.0
 SHAPES = {"370M": "s0", "1.3B": "s2", "2.7B": "s3"}
 DIMS = {"s0": (32000, 1024, 24, 2816), "s2": (32000, 2048, 24, 5632), "s3": (32000, 2560, 32, 6912)}
 KINDS = ("ifg", "o", "gate", "down", "lm")
+MODE_NAMES = {0: "float", 1: "fixed"}
+# the sources of the batch-1 decode kernels; profiles/pmc_traffic.json records their digest
+DECODE_SOURCES = ("matmulfreellmcpu_amd/csrc/mmf_decode.hip", "matmulfreellmcpu_amd/csrc/mmf_device.hpp",
+                  "matmulfreellmcpu_amd/csrc/mmf_internal.hpp")
+
+
+def decode_sources_digest():
+    h = hashlib.sha256()
+    for p in DECODE_SOURCES:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def log(*a):
@@ -87,6 +104,18 @@ def blob_path(d, preset):
         make_blob(p, preset=preset, seed=1234)
         log(f"[bench] wrote {p} in {time.time() - t:.1f}s")
     return p
+
+
+def roofline_leg(blob_dir, reps):
+    """370M float decode, every launch between its own event pair (run with MMF_GRAPH=0, so no
+    HIP graph): prints the microseconds per launch of each kind."""
+    from matmulfreellmcpu_amd import FLOAT, Engine
+    e = Engine(0)
+    e.load_blob(blob_path(blob_dir, "s0"), FLOAT)
+    e.generate(np.random.default_rng(1234).integers(3, 32000, 16), 8)
+    _, kind_us = e.time_decode(warmup=4, reps=reps)
+    e.close()
+    print(json.dumps({k: round(v, 3) for k, v in kind_us.items()}))
 
 
 def measure(eng, preset, steps, warmup):
@@ -345,20 +374,32 @@ def run_cpu_leg(job, cpus, timeout=600):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
-def cpu_baselines(blob_dir, ids, gen):
+def ref_cli_ids(blob, ids, gen, mode, env):
+    """Greedy ids from the reference CLI (prompt and generated tokens, as --print-ids prints them)."""
+    r = subprocess.run([REF_CLI, "--blob", blob, "--ids", ",".join(str(int(i)) for i in ids), "--gen", str(gen),
+                        "--mode", mode, "--print-ids"], capture_output=True, text=True, env=env, check=True,
+                       timeout=600)
+    return np.array([int(t) for t in r.stdout.split()], np.int64)
+
+
+def cpu_baselines(blob_dir, ids, gen, gpu_ids):
     """The reference engine on this host's cores beside every workload: one socket's
     physical cores (OMP_PROC_BIND=close, one place per core), and for the headline also every
-    allowed cpu. Bounded samples; each dict says what was timed."""
+    allowed cpu. Each dict says what was timed. gpu_ids[(shape, mode)]: the GPU's greedy ids
+    for the 16-token prompt, compared with the reference CLI's."""
     if not os.path.exists(REF_CLI):
-        return None, None, {}
+        return None, None, {}, None
     sock, allc = cpu_sets()
     env_s, env_a = omp_env(sock), omp_env(allc)
     res = {}
+    parity = {"against": "reference mmfree-cli (oracle/_ref), 16-token prompt, greedy", "tokens": gen, "shapes": {}}
+    for (name, mode), got in sorted(gpu_ids.items()):
+        want = ref_cli_ids(blob_path(blob_dir, SHAPES[name]), ids, gen, mode, env_s)
+        parity["shapes"].setdefault(name, {})[mode] = bool(np.array_equal(want, got))
+    parity["ids_identical"] = all(v for d in parity["shapes"].values() for v in d.values())
+    log(f"[bench] parity with the reference CLI: {parity['shapes']}")
     # config 0: the reference CLI's --bench on the 370M blob, float, as the GPU headline
     blob0 = blob_path(blob_dir, "s0")
-    r = subprocess.run([REF_CLI, "--blob", blob0, "--ids", ",".join(str(int(i)) for i in ids), "--gen", str(gen),
-                        "--mode", "float", "--print-ids"], capture_output=True, text=True, env=env_s, check=True)
-    ref_ids = np.array([int(t) for t in r.stdout.split()], np.int64)
     _, tps, wall = ref_cli_bench(blob0, ids, gen, "float", env_s)
     _, tps_all, wall_all = ref_cli_bench(blob0, ids, gen, "float", env_a)
     head = {"value": tps, "unit": "tok/s", "cores": len(sock), "kind": "reference",
@@ -367,17 +408,17 @@ def cpu_baselines(blob_dir, ids, gen):
                       "OMP_WAIT_POLICY=active",
             "all_cpus": {"value": tps_all, "cores": len(allc), "wall_s": round(wall_all, 1)}}
     log(f"[bench] cpu reference 370M float: {tps} tok/s on {len(sock)} cores, {tps_all} on {len(allc)} cpus")
-    # config 2: 1.3B prefill (64-token sample) + decode, float and fixed
+    # config 2 in full: 1.3B, 2048-token prefill then 256 greedy tokens, float and fixed
     blob2 = blob_path(blob_dir, "s2")
-    ids64 = np.random.default_rng(77).integers(3, 32000, 64)
+    ids2k = np.random.default_rng(77).integers(3, 32000, 2048)
     c2 = {}
     for mode in ("float", "fixed"):
-        pre_ms, dec, wall = ref_cli_bench(blob2, ids64, 16, mode, env_s, reps=1, warmup=0)
-        c2[mode] = {"prefill_tok_s": round(64 / pre_ms * 1e3, 2) if pre_ms else None, "decode_tok_s": dec,
-                    "wall_s": round(wall, 1)}
+        pre_ms, dec, wall = ref_cli_bench(blob2, ids2k, 256, mode, env_s, reps=1, warmup=0)
+        c2[mode] = {"prefill_ms": pre_ms, "prefill_tok_s": round(2048 / pre_ms * 1e3, 2) if pre_ms else None,
+                    "decode_tok_s": dec, "wall_s": round(wall, 1)}
     res["prefill_decode_1.3B"] = {"kind": "reference", "cores": len(sock), "modes": c2,
-                                  "sample": "1.3B, 64-token prompt (a sample of the 2048-token prefill), 16 "
-                                            "greedy tokens, reference mmfree-cli --bench warmup 0 reps 1"}
+                                  "sample": "1.3B, 2048-token prompt + 256 greedy tokens (configuration 2 in full), "
+                                            "reference mmfree-cli --bench warmup 0 reps 1"}
     log(f"[bench] cpu reference 1.3B: {c2}")
     # config 1: the op sweep's integer matmul through the reference's CpuBackend
     res["op_sweep"] = {"kind": "reference", "cores": len(sock), "shapes": run_cpu_leg("op_sweep", sock),
@@ -390,7 +431,7 @@ def cpu_baselines(blob_dir, ids, gen):
                         sample=f"Model::generate_serve, {B} one-token prompts, 2 lockstep steps timed (3 new tokens "
                                "minus 1)")
         log(f"[bench] cpu reference {key}: {r}")
-    return ref_ids, head, res
+    return head, res, parity
 
 
 def main():
@@ -406,6 +447,9 @@ def main():
     ap.add_argument("--vendor-int8", default=None, metavar="T,H,I",
                     help="only time the vendor int8 GEMM on one prefill layer's shapes (child process)")
     ap.add_argument("--cpu-leg", default=None, help="run one CPU baseline job (child process)")
+    ap.add_argument("--roofline-leg", action="store_true",
+                    help="only the 370M float decode with an event pair around every launch (run with "
+                         "MMF_GRAPH=0; child process of the roofline, and the command rocprofv3 traces)")
     ap.add_argument("--skip-decode", action="store_true",
                     help="profiling runs of the other sections: no B=1 decode and no headline (the "
                          "printed line holds only the sections run)")
@@ -414,6 +458,10 @@ def main():
     args = ap.parse_args()
     if args.cpu_leg:
         cpu_leg(args.cpu_leg)
+        return
+    if args.roofline_leg:
+        os.makedirs(args.blob_dir, exist_ok=True)
+        roofline_leg(args.blob_dir, max(16, args.steps // 4))
         return
     if args.vendor_int8:
         T, H, I = (int(x) for x in args.vendor_int8.split(","))
@@ -438,7 +486,7 @@ def main():
         shapes.insert(0, "370M")
     results = {}
     ids = np.random.default_rng(1234).integers(3, 32000, 16)
-    gpu_ids = None
+    gpu_ids = {}  # (shape, mode name) -> greedy ids of the 16-token prompt, 128 tokens
     fixed = {}
     for name in ([] if args.skip_decode else shapes):
         preset = SHAPES[name]
@@ -449,11 +497,8 @@ def main():
             eng = Engine(0)
             eng.load_blob(p, mode)
             log(f"[bench] {name} mode {mode}: loaded + repacked in {time.time() - t:.1f}s")
-            if name == "370M" and mode == FLOAT:
-                gpu_ids = eng.generate(ids, 128)
-                eng.generate(ids, 16)
-            else:
-                eng.generate(ids, 8)
+            gpu_ids[(name, MODE_NAMES[mode])] = eng.generate(ids, 128)
+            eng.generate(ids, 16)
             steps = args.steps if (name == "370M" and mode == FLOAT) else max(64, args.steps // 4)
             eng.sync()
             t0 = time.perf_counter()
@@ -486,28 +531,45 @@ def main():
     value = 1e6 / head["step_us"]
     kern = head["kernels"]
     dom = max(KINDS, key=lambda k: kern[k]["us_per_launch"] * kern[k]["launches_per_token"])
-    achieved = kern[dom]["GBps"]
+    # that kind's average launch, each launch between its own event pair, graphs off (a child
+    # process: MMF_GRAPH is read once per process)
+    leg_us = None
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--roofline-leg", "--steps", str(args.steps),
+                            "--blob-dir", args.blob_dir], capture_output=True, text=True, timeout=300, check=True,
+                           env=dict(os.environ, MMF_GRAPH="0"))
+        leg_us = json.loads(r.stdout.strip().splitlines()[-1])
+    except Exception as ex:  # the graph-replay figure stands in, and the line says so
+        log(f"[bench] roofline leg failed: {ex}")
+    us = leg_us[dom] if leg_us else kern[dom]["us_per_launch"]
+    achieved = round(kern[dom]["bytes_per_launch"] / us / 1e3, 1)
     # HBM bytes per launch of that kernel from the committed PMC summary (FETCH_SIZE and
-    # WRITE_SIZE runs, calibrated on a copy kernel of known size), when it covers the kernel
-    traffic = None
+    # WRITE_SIZE runs, calibrated on a copy kernel of known size), only while it describes the
+    # kernels of this tree (the digest of their sources recorded with it)
+    traffic, traffic_kernel = None, None
     try:
         with open(os.path.join(ROOT, "profiles", "pmc_traffic.json")) as f:
-            traffic = json.load(f)["kernels"][dom]["traffic_bytes"]
+            pmc = json.load(f)
+        if pmc.get("sources_sha256") == decode_sources_digest():
+            traffic = pmc["kernels"][dom]["traffic_bytes"]
+            traffic_kernel = pmc["kernels"][dom]["kernel"]
+        else:
+            log("[bench] profiles/pmc_traffic.json describes other decode sources: traffic left null")
     except (OSError, KeyError, ValueError):
         pass
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": f"k_decode<float,{dom}> (370M)", "bytes_per_launch": kern[dom]["bytes_per_launch"],
-                "us_per_launch": kern[dom]["us_per_launch"]}
+                "kernel": f"370M float {dom}" + (f" ({traffic_kernel})" if traffic_kernel else ""),
+                "bytes_per_launch": kern[dom]["bytes_per_launch"], "us_per_launch": us,
+                "timing": "event pair around each launch, HIP graphs off" if leg_us else
+                          "graph replay (the event-pair leg failed)",
+                "us_per_launch_graph_replay": kern[dom]["us_per_launch"]}
 
     cpu = None
     parity = None
     cpu_configs = {}
     if not args.no_cpu:
-        ref_ids, cpu, cpu_configs = cpu_baselines(args.blob_dir, ids, 128)
-        if ref_ids is not None:
-            parity = {"against": "reference mmfree-cli (oracle/_ref)", "tokens": 128,
-                      "ids_identical": bool(np.array_equal(ref_ids, gpu_ids))}
+        cpu, cpu_configs, parity = cpu_baselines(args.blob_dir, ids, 128, gpu_ids)
 
     out = {
         "metric": METRIC,

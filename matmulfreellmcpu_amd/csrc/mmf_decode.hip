@@ -19,6 +19,8 @@
 //    grid-wide synchronisation is needed inside a launch.
 // Thread (ol, j) of a matrix's 128 threads sums chain j of output og*16+ol, which is the
 // reference's AVX2 lane j (16 outputs x 8 chains per output group).
+#include <hip/hip_ext.h>
+
 #include <cstdlib>
 
 #include "mmf_device.hpp"
@@ -26,7 +28,19 @@
 
 namespace mmf {
 
+thread_local LaunchEvents g_launch_events;
+
 namespace {
+
+// kernel<<<grid, block, lds, s>>>(args...), or with g_launch_events recorded at the kernel's
+// start and end
+template <class K, class... A>
+hipError_t launch_k(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, A... args) {
+  const LaunchEvents ev = g_launch_events;
+  if (ev.start && ev.stop) hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, ev.start, ev.stop, 0, args...);
+  else kernel<<<grid, block, lds, s>>>(args...);
+  return hipGetLastError();
+}
 
 template <int KIND> struct KindTraits;
 // NM matrices (one wave pair each), NA activation vectors, NP prologue source vectors
@@ -869,8 +883,8 @@ hipError_t decf_rc(const DecArgs& a, hipStream_t s) {
   const int grid = (nout + 7) / 8;
   const float* prew = (KIND == kDown) ? nullptr : a.pre_w;
   const float* xg = (KIND == kO) ? a.x2 : nullptr;
-  k_decf<KIND, RC><<<grid, 64 * NM, lds, s>>>(a.x, prew, xg, a.p[0].normwT, a.p[1].normwT, a.p[2].normwT, a);
-  return hipGetLastError();
+  return launch_k(k_decf<KIND, RC>, grid, 64 * NM, lds, s, a.x, prew, xg, a.p[0].normwT, a.p[1].normwT,
+                  a.p[2].normwT, a);
 }
 
 // k_decf for a float layer kind when every matrix has its fp4 slab and the width is a model
@@ -919,8 +933,7 @@ hipError_t dec_rc(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
   constexpr int BS = kBlock * KindTraits<KIND>::NM * KS;
   constexpr int F4 = (8 * 32 * RC + 8) / 4;  // float4s of a chain-transposed vector
   static_assert(F4 <= 16 * BS, "row too long for the block layout");
-  k_decode<MODE, KIND, nv_for(F4, BS), KS, RC, W4><<<grid, BS, lds, s>>>(a);
-  return hipGetLastError();
+  return launch_k(k_decode<MODE, KIND, nv_for(F4, BS), KS, RC, W4>, grid, BS, lds, s, a);
 }
 
 template <int MODE, int KIND, int KS, bool W4>
@@ -945,12 +958,11 @@ hipError_t dec_ks(const DecArgs& a, size_t lds, int grid, hipStream_t s) {
     }
   }
   const int F4 = (8 * Lc + 8) / 4;
-  if (F4 <= 2 * BS) k_decode<MODE, KIND, 2, KS, 0, W4><<<grid, BS, lds, s>>>(a);
-  else if (F4 <= 4 * BS) k_decode<MODE, KIND, 4, KS, 0, W4><<<grid, BS, lds, s>>>(a);
-  else if (F4 <= 8 * BS) k_decode<MODE, KIND, 8, KS, 0, W4><<<grid, BS, lds, s>>>(a);
-  else if (F4 <= 16 * BS) k_decode<MODE, KIND, 16, KS, 0, W4><<<grid, BS, lds, s>>>(a);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (F4 <= 2 * BS) return launch_k(k_decode<MODE, KIND, 2, KS, 0, W4>, grid, BS, lds, s, a);
+  if (F4 <= 4 * BS) return launch_k(k_decode<MODE, KIND, 4, KS, 0, W4>, grid, BS, lds, s, a);
+  if (F4 <= 8 * BS) return launch_k(k_decode<MODE, KIND, 8, KS, 0, W4>, grid, BS, lds, s, a);
+  if (F4 <= 16 * BS) return launch_k(k_decode<MODE, KIND, 16, KS, 0, W4>, grid, BS, lds, s, a);
+  return hipErrorInvalidValue;
 }
 
 template <int MODE, int KIND>
@@ -1013,8 +1025,10 @@ hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
   const size_t wx = static_cast<size_t>(nm) * G * g.Wc * 128 * sizeof(uint32_t);
   // float layer GEMVs: the fp4 slab (twice the words) when every matrix has one and its words
   // fit in LDS beside the rest; otherwise the 2-bit slab
-  bool w4 = MODE == kFloat && kind != kLM;
-  for (int z = 0; z < nm; ++z) w4 = w4 && a.p[z].pk4 != nullptr;
+  // (gate/up keeps the 2-bit slab: its four GEMV waves per CU are bound by the LDS reads of the
+  // activations, not by the code conversion -- 4.88 us per 370M launch either way)
+  bool w4 = MODE == kFloat && (kind == kIFG || kind == kO || kind == kDown);
+  for (int z = 0; z < (kind == kIFG ? 3 : 1); ++z) w4 = w4 && a.p[z].pk4 != nullptr;
   w4 = w4 && lds + 2 * wx <= static_cast<size_t>(lds_limit());
   if (w4) {
     b.wgroups = G;

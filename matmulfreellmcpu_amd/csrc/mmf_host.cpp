@@ -1407,9 +1407,9 @@ int mmf_model_finalize(mmf_ctx* c, int mode, int frac) {
       Ld.gnT = tr(Ld.gn, false);
       for (int j = 0; j < 6; ++j) c->projs[Ld.proj[j]].d.normwT = tr(c->projs[Ld.proj[j]].d.normw, j == 5);
     }
-    if (mode == kFloat)  // the batch-1 float GEMVs read fp4 codes (one conversion per two codes)
+    if (mode == kFloat)  // the batch-1 float GEMVs of i/f/g, o and down read fp4 codes
       for (size_t l = 0; l < L; ++l)
-        for (int j = 0; j < 6; ++j) ensure_pk4(c, c->projs[m.layers[l].proj[j]]);
+        for (int j : {0, 1, 2, 3, 5}) ensure_pk4(c, c->projs[m.layers[l].proj[j]]);
     m.mode = mode;
     m.frac = frac;
     m.qs = static_cast<float>(1u << frac);
@@ -1755,8 +1755,8 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
     if (kind_us) {
       // Per kind: the kernels of that kind for all layers, back to back, `reps` times. With
       // graphs the launches are captured and replayed, so the average per launch is the
-      // kernel's execution time (graph nodes run without host submission gaps); without
-      // graphs an event pair around every launch measures each kernel on the stream.
+      // kernel's execution time plus the graph's launch gap; without graphs every kernel
+      // records an event pair at its own start and end (what a profiler's kernel trace reads).
       const size_t L = m.layers.size();
       for (int k = 0; k < 5; ++k) {
         const size_t nl = (k == 4) ? 1 : L;
@@ -1784,9 +1784,14 @@ int mmf_model_time_decode(mmf_ctx* c, int warmup, int reps, double* step_us, dou
         double total = 0.0;
         for (int r = 0; r < reps + 1; ++r) {
           for (size_t l = 0; l < nl; ++l) {
-            MMF_HIP(hipEventRecord(ev[2 * l], c->stream));
-            decode_one(c, m, static_cast<DecKind>(k), l);
-            MMF_HIP(hipEventRecord(ev[2 * l + 1], c->stream));
+            g_launch_events = LaunchEvents{ev[2 * l], ev[2 * l + 1]};
+            try {
+              decode_one(c, m, static_cast<DecKind>(k), l);
+            } catch (...) {
+              g_launch_events = LaunchEvents{};
+              throw;
+            }
+            g_launch_events = LaunchEvents{};
           }
           MMF_HIP(hipEventSynchronize(ev[2 * nl - 1]));
           if (r == 0) continue;  // warm-up pass

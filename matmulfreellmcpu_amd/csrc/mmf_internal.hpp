@@ -102,6 +102,13 @@ inline int lm_blocks(int groups, int K) {
   return groups < cap ? groups : cap;
 }
 hipError_t launch_decode(DecKind kind, Mode mode, const DecArgs& a, hipStream_t s);
+// Timing runs: while both events are set, launch_decode records them at its kernel's own start
+// and end (hipExtLaunchKernelGGL), the timestamps a profiler's kernel trace reports, instead of
+// around the launch on the stream.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
 // rows of x [rows, K] -> chain-transposed rows out [rows, 8*Lc + 8]
 hipError_t launch_to_chain(const float* x, float* out, int rows, int K, int Lc, hipStream_t s);
 
