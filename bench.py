@@ -364,6 +364,53 @@ def cpu_leg(job):
         rm.close()
         step = max(t3 - t1, 1e-9) / 2
         print(json.dumps({"ms_per_step": round(step * 1e3, 1), "tok_s": round(B / step, 1)}))
+    elif kind == "seam":  # the reference Model with HipTernaryBackend at its TernaryBackend seam
+        import ctypes as C
+        from oracle.oracle import Ref
+        so = os.path.join(ROOT, "oracle", "_ref", "libmmfree_ref_hipbe.so")
+        r = Ref(so)
+        L = r.lib
+        L.ref_model_ptr.restype = C.c_void_p
+        L.ref_model_ptr.argtypes = [C.c_void_p]
+        L.ref_model_weights.restype = C.c_void_p
+        L.ref_model_weights.argtypes = [C.c_void_p]
+        L.ref_hipbe_attach.restype = C.c_void_p
+        L.ref_hipbe_attach.argtypes = [C.c_void_p, C.c_int]
+        L.ref_hipbe_attach_registered.restype = C.c_void_p
+        L.ref_hipbe_attach_registered.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.ref_hipbe_detach.argtypes = [C.c_void_p, C.c_void_p]
+        blob, n = arg.split(",")
+        n = int(n)
+        ids = np.random.default_rng(1234).integers(3, 32000, 16)
+
+        def rate(m, gen):  # decode tok/s: (gen - 1) tokens over the time beyond a 1-token run
+            m.generate(ids, 2)
+            t = time.perf_counter()
+            m.generate(ids, 1)
+            t1 = time.perf_counter() - t
+            t = time.perf_counter()
+            out = m.generate(ids, gen)
+            tn = time.perf_counter() - t
+            return (gen - 1) / max(tn - t1, 1e-9), out
+
+        res = {}
+        m = r.model(blob, FIXED)
+        cpu_rate, want = rate(m, n)
+        res["cpu"] = round(cpu_rate, 1)
+        for label, attach, gen in (("registered", "reg", n), ("proj_id_minus_1", "raw", max(8, n // 8))):
+            mp = L.ref_model_ptr(m.h)
+            be = (L.ref_hipbe_attach_registered(mp, L.ref_model_weights(m.h), 0) if attach == "reg"
+                  else L.ref_hipbe_attach(mp, 0))
+            if not be:
+                raise SystemExit("attaching HipTernaryBackend failed")
+            try:
+                g, got = rate(m, gen)
+            finally:
+                L.ref_hipbe_detach(mp, be)
+            res[label] = {"decode_tok_s": round(g, 1), "tokens": gen,
+                          "ids_identical": bool(np.array_equal(got, want[:got.size]))}
+        m.close()
+        print(json.dumps(res))
     else:
         raise SystemExit(f"unknown cpu job {job}")
 
@@ -423,6 +470,18 @@ def cpu_baselines(blob_dir, ids, gen, gpu_ids):
     # config 1: the op sweep's integer matmul through the reference's CpuBackend
     res["op_sweep"] = {"kind": "reference", "cores": len(sock), "shapes": run_cpu_leg("op_sweep", sock),
                        "sample": "CpuBackend::matmul_batch on int8-range codes at every (M, K, N), one call each"}
+    # the drop-in at the seam: the reference Model (FixedQ510, 370M) with its integer
+    # projections through HipTernaryBackend, beside the same Model on the CPU
+    try:
+        seam = run_cpu_leg(f"seam:{blob_path(blob_dir, 's0')},64", sock)
+        res["seam_370M_fixed"] = dict(seam, kind="reference", cores=len(sock),
+                                      sample="reference Model::generate, 370M FixedQ510, 16-token prompt: decode "
+                                             "tok/s on the CPU (CpuBackend) and with HipTernaryBackend, registered "
+                                             "(tag registry of resident projections) and proj_id -1 (exact "
+                                             "check of the weights at each call); ids compared with the CPU run")
+        log(f"[bench] seam: {seam}")
+    except Exception as ex:
+        log(f"[bench] seam leg failed: {ex}")
     # configs 3 and 4: lockstep serving steps
     for key, preset, B, mode in (("serve_2.7B_x64_float", "s3", 64, "float"), ("serve_2.7B_x64_fixed", "s3", 64, "fixed"),
                                  ("serve_1.3B_x32_fixed", "s2", 32, "fixed")):

@@ -77,11 +77,24 @@ int mmf_proj_register(mmf_ctx* ctx, const int8_t* wq, size_t N, size_t K, float 
 int mmf_proj_update(mmf_ctx* ctx, int proj_id, const int8_t* wq);
 /* Shape of a registered projection. */
 int mmf_proj_shape(mmf_ctx* ctx, int proj_id, size_t* N, size_t* K);
+/* Free a registered projection's device memory; proj_id is invalid afterwards (calls that
+ * pass it fail with MMF_ERR_ARG). For callers that re-register a buffer whose weights, scale
+ * or norm weight changed (the host operator functions of kernels.hpp:29-68, which cache
+ * projections by host pointer), so that replaced projections do not accumulate. */
+int mmf_proj_release(mmf_ctx* ctx, int proj_id);
 
 /* TernaryBackend::matmul_batch (ternary_backend.hpp:43-48, 96-103):
  * acc[i*N + o] = sum_k x[i*K + k] * wq[o, k] for b rows; x holds int16-range Q5.10 codes
  * stored as int32 (ternary_backend.hpp:8-13). dev pointers. */
 int mmf_ternary_matmul(mmf_ctx* ctx, int proj_id, const int32_t* x, int32_t* acc, size_t b);
+/* The same for k projections on host buffers in one round trip: x[z] holds b rows of K_z
+ * codes and acc[z] receives b rows of N_z accumulators for proj_ids[z] (host memory). All
+ * codes go to the device in one copy through pinned staging the context keeps, the k matmuls
+ * run back to back, and all accumulators return in one copy before the call returns (one
+ * synchronisation). TernaryBackend::matmul_batch and matmul_seq (ternary_backend.hpp:43-90)
+ * on host buffers, as HipTernaryBackend calls it. */
+int mmf_ternary_matmul_host(mmf_ctx* ctx, int k, const int* proj_ids, const int32_t* const* x,
+                            int32_t* const* acc, size_t b);
 
 /* ---- operators (kernels.hpp:29-68), dev pointers ----------------------------------------- */
 /* bitlinear (kernels.hpp:41-44, bitlinear.cpp:21-117) with the projection's registered

@@ -62,6 +62,8 @@ def load_library(path: str = LIB_PATH):
         "mmf_proj_register": (i, [_vp, _vp, _sz, _sz, C.c_float, _vp, C.POINTER(i)]),
         "mmf_proj_shape": (i, [_vp, i, C.POINTER(_sz), C.POINTER(_sz)]),
         "mmf_ternary_matmul": (i, [_vp, i, _vp, _vp, _sz]),
+        "mmf_ternary_matmul_host": (i, [_vp, i, C.POINTER(i), C.POINTER(_vp), C.POINTER(_vp), _sz]),
+        "mmf_proj_release": (i, [_vp, i]),
         "mmf_bitlinear": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
         "mmf_bitlinear_noalloc": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
         "mmf_bitlinear_cluster": (i, [_vp, C.POINTER(i), i, i, i, C.c_float, _vp, C.POINTER(_vp), _sz]),
@@ -188,6 +190,21 @@ class Engine:
 
     def ternary_matmul(self, pid, x, acc, b):
         self._chk(self.lib.mmf_ternary_matmul(self.h, pid, _ptr(x), _ptr(acc), b))
+
+    def ternary_matmul_host(self, pids, xs):
+        """k projections on host arrays in one round trip: xs[z] int32 [b, K_z] -> int32 [b, N_z]."""
+        k = len(pids)
+        b = xs[0].shape[0]
+        xs = [np.ascontiguousarray(x, np.int32) for x in xs]
+        accs = [np.zeros((b, self.proj_shape(p)[0]), np.int32) for p in pids]
+        ids = (C.c_int * k)(*pids)
+        xp = (_vp * k)(*[x.ctypes.data for x in xs])
+        ap = (_vp * k)(*[a.ctypes.data for a in accs])
+        self._chk(self.lib.mmf_ternary_matmul_host(self.h, k, ids, xp, ap, b))
+        return accs
+
+    def proj_release(self, pid):
+        self._chk(self.lib.mmf_proj_release(self.h, pid))
 
     def rmsnorm(self, y, x, w, rows, cols, eps=1e-6):
         self._chk(self.lib.mmf_rmsnorm(self.h, _ptr(y), _ptr(x), _ptr(w), rows, cols, eps))

@@ -66,6 +66,29 @@ struct DBuf {
   }
 };
 
+// Grow-only pinned host buffer (hipHostMalloc) for copies that must not stage through
+// pageable memory.
+struct PinBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  void* get(size_t bytes) {
+    if (bytes > n) {
+      if (p) (void)hipHostFree(p);
+      p = nullptr;
+      n = 0;
+      MMF_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+      n = bytes;
+    }
+    return p;
+  }
+  template <class T> T* as(size_t count) { return static_cast<T*>(get(count * sizeof(T))); }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
 struct Proj {
   ProjDev d;
   void* mem = nullptr;   // pk | tail | rowsum | normw in one allocation
@@ -169,6 +192,8 @@ struct mmf_ctx {
   DBuf raw;  // staging for int8 weights before the repack
   DBuf opy, opq, opct, opsa, opstate;
   DBuf gws;  // split-K workspace of the matrix-core GEMM
+  DBuf hmx, hmacc;        // mmf_ternary_matmul_host: codes and accumulators on the device
+  PinBuf pin_x, pin_acc;  // ... and their pinned host staging
   hipDeviceProp_t prop{};
   RowTimer timer;
 };
@@ -198,6 +223,7 @@ int guard(mmf_ctx* ctx, F&& f) {
 
 const Proj& proj_of(mmf_ctx* c, int id) {
   if (id < 0 || id >= static_cast<int>(c->projs.size())) fail(MMF_ERR_ARG, "invalid proj_id " + std::to_string(id));
+  if (!c->projs[id].mem) fail(MMF_ERR_ARG, "proj_id " + std::to_string(id) + " was released");
   return c->projs[id];
 }
 
@@ -965,7 +991,7 @@ void mmf_destroy(mmf_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   drop_graph(c->model);
   for (auto& p : c->projs) {
-    (void)hipFree(p.mem);
+    if (p.mem) (void)hipFree(p.mem);
     if (p.mem4) (void)hipFree(p.mem4);
   }
   for (auto& kv : c->model.tensors)
@@ -978,7 +1004,10 @@ void mmf_destroy(mmf_ctx* c) {
   for (DBuf* b : {&s.ids, &s.h, &s.resid, &s.i, &s.f, &s.g, &s.recur, &s.scan, &s.z, &s.logits, &s.state0, &s.am,
                   &s.acty, &s.actq, &s.actct, &s.actsa, &s.segs})
     b->release();
-  for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate, &c->gws}) b->release();
+  for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate, &c->gws, &c->hmx, &c->hmacc})
+    b->release();
+  c->pin_x.release();
+  c->pin_acc.release();
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -1057,6 +1086,81 @@ int mmf_proj_shape(mmf_ctx* c, int id, size_t* N, size_t* K) {
     const Proj& p = proj_of(c, id);
     if (N) *N = p.d.g.N;
     if (K) *K = p.d.g.K;
+  });
+}
+
+int mmf_proj_release(mmf_ctx* c, int id) {
+  return guard(c, [&] {
+    (void)proj_of(c, id);
+    for (const auto& kv : c->model.tensors)
+      if (kv.second.proj == id) fail(MMF_ERR_STATE, "proj_id " + std::to_string(id) + " belongs to the loaded model");
+    MMF_HIP(hipStreamSynchronize(c->stream));
+    Proj& P = c->projs[id];
+    MMF_HIP(hipFree(P.mem));
+    if (P.mem4) MMF_HIP(hipFree(P.mem4));
+    P = Proj{};
+  });
+}
+
+int mmf_ternary_matmul_host(mmf_ctx* c, int k, const int* ids, const int32_t* const* x, int32_t* const* acc,
+                            size_t b) {
+  return guard(c, [&] {
+    if (k < 1 || k > 64 || !ids || !x || !acc) fail(MMF_ERR_ARG, "invalid arguments");
+    if (b == 0) return;
+    if (b > (1u << 24)) fail(MMF_ERR_ARG, "too many rows");
+    size_t xo[64], ao[64], in = 0, out = 0;
+    for (int z = 0; z < k; ++z) {
+      const Proj& p = proj_of(c, ids[z]);
+      if (!x[z] || !acc[z]) fail(MMF_ERR_ARG, "null buffer");
+      xo[z] = in;
+      ao[z] = out;
+      in += b * static_cast<size_t>(p.d.g.K);
+      out += b * static_cast<size_t>(p.d.g.N);
+    }
+    int32_t* hx = c->pin_x.as<int32_t>(in);
+    int32_t* ha = c->pin_acc.as<int32_t>(out);
+    int32_t* dx = c->hmx.as<int32_t>(in);
+    int32_t* da = c->hmacc.as<int32_t>(out);
+    for (int z = 0; z < k; ++z) std::memcpy(hx + xo[z], x[z], b * proj_of(c, ids[z]).d.g.K * sizeof(int32_t));
+    // few rows of projections of one shape (a decode step's i/f/g cluster, o, gate, down,
+    // lm_head): one kernel for all k that reads the codes from the pinned staging and writes the
+    // accumulators straight into it (no copy engine round trips)
+    const Geom& g0 = proj_of(c, ids[0]).d.g;
+    bool one_shape = static_cast<int>(b) <= seam_max_rows() && k <= kSeamMaxProj;
+    for (int z = 1; z < k && one_shape; ++z) {
+      const Geom& gz = proj_of(c, ids[z]).d.g;
+      one_shape = gz.N == g0.N && gz.K == g0.K;
+    }
+    if (one_shape) {
+      (void)dx;
+      SeamArgs sa{};
+      for (int z = 0; z < k; ++z) {
+        sa.pk[z] = proj_of(c, ids[z]).d.pk;
+        sa.tail[z] = proj_of(c, ids[z]).d.tail;
+        sa.rowsum[z] = proj_of(c, ids[z]).d.rowsum;
+      }
+      sa.x = hx;
+      sa.acc = ha;
+      sa.g = g0;
+      sa.b = static_cast<int>(b);
+      MMF_HIP(launch_seam_dot(sa, k, c->stream));
+      MMF_HIP(hipStreamSynchronize(c->stream));
+      for (int z = 0; z < k; ++z) std::memcpy(acc[z], ha + ao[z], b * static_cast<size_t>(g0.N) * sizeof(int32_t));
+      return;
+    }
+    MMF_HIP(hipMemcpyAsync(dx, hx, in * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    for (int z = 0; z < k; ++z) {
+      const Proj& p = proj_of(c, ids[z]);
+      ActBuf act = make_act(c->opy, c->opq, c->opct, c->opsa, kFixed, p.d.g, static_cast<int>(b), 1);
+      MMF_HIP(launch_codes_to_planes(dx + xo[z], act, c->stream));
+      GemmArgs ga = gemm_args(c, &ids[z], 1, static_cast<int>(b), kFixed, 10);
+      ga.raw_acc = true;
+      ga.acc[0] = da + ao[z];
+      run_gemm(c, ga, act, c->stream);
+    }
+    MMF_HIP(hipMemcpyAsync(ha, da, out * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+    MMF_HIP(hipStreamSynchronize(c->stream));
+    for (int z = 0; z < k; ++z) std::memcpy(acc[z], ha + ao[z], b * proj_of(c, ids[z]).d.g.N * sizeof(int32_t));
   });
 }
 

@@ -213,6 +213,22 @@ hipError_t launch_acc_epilogue(const GemmArgs& a, const ActBuf& act, hipStream_t
 bool mfma_f_ok(const GemmArgs& a);
 hipError_t launch_gemm_mfma_f(const GemmArgs& a, const ActBuf& act, hipStream_t s);
 
+// The TernaryBackend seam's few-row integer matmul (mmf_ternary_matmul_host): k projections of
+// one shape g, b rows each (b <= seam_max_rows()); x [k][b][K] int32 codes and acc [k][b][N]
+// int32 in memory the device reads and writes directly (the caller's pinned host staging).
+constexpr int kSeamMaxProj = 8;
+struct SeamArgs {
+  const uint32_t* pk[kSeamMaxProj];
+  const int8_t* tail[kSeamMaxProj];
+  const int32_t* rowsum[kSeamMaxProj];
+  const int32_t* x;
+  int32_t* acc;
+  Geom g;
+  int b;
+};
+int seam_max_rows();
+hipError_t launch_seam_dot(const SeamArgs& a, int k, hipStream_t s);
+
 // ---- device calibration (mmf_peaks.hip) ----------------------------------------------------
 // out = {HBM read GB/s, Infinity Cache read GB/s, int8 MFMA TOP/s, fp32 FMA TFLOP/s}; allocates
 // and frees 2 GiB of scratch, synchronizes the stream.

@@ -139,6 +139,84 @@ __global__ void k_pack(const int8_t* __restrict__ wq, Geom g, uint32_t* __restri
   }
 }
 
+// The TernaryBackend seam's few-row matmul (mmf_ternary_matmul_host): acc[z][r][o] =
+// sum_k x[z][r][k] * wq_z[o][k] in int32 for B <= kSeamRows rows, one launch for k projections
+// of one shape (blockIdx.y = z). x and acc are the caller's pinned host staging. A block issues
+// its first slab words, then reads its projection's rows of codes from host memory once and
+// stores each row's body as two int8 planes in the slab's chain order (x = 256 hi + lo + 128
+// with hi = x >> 8 and lo = (x & 255) - 128, the split of the Q5.10 GEMMs) and its tail as
+// int32. It runs two 16-output groups at a time: thread (ol, j) sums chain j of output ol with
+// v_dot4 on each plane (words read 8 at a time), the 8 chains are added across lanes, then
+// 256 hi + lo + 128 rowsum + tail. All sums are exact integers (the reference's int32 lanes),
+// so their order is free.
+constexpr int kSeamRows = 4;
+template <int B>
+__global__ __launch_bounds__(256) void k_seam_dot(SeamArgs a) {
+  extern __shared__ int32_t seam_lds[];
+  const int z = blockIdx.y;
+  const Geom& g = a.g;
+  const int K = g.K, LQ = g.Lc + 16;        // plane row stride in bytes (16 bytes of padding)
+  int8_t* hp = reinterpret_cast<int8_t*>(seam_lds);  // [B][2][8][LQ]: hi plane, lo plane
+  int32_t* tl = seam_lds + B * 4 * LQ;                 // [B][8] tail codes
+  const int lt = threadIdx.x & 127, ol = lt >> 3, j = lt & 7, sub = threadIdx.x >> 7;
+  const uint32_t* pk = a.pk[z];
+  int og = 2 * blockIdx.x + sub;
+  uint32_t w[8];
+  auto words = [&](int og_, int m0) {
+    const uint32_t* wp = pk + static_cast<size_t>(og_) * g.Wc * 128 + lt;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = (m0 + u < g.Wc) ? wp[(m0 + u) * 128] : 0u;  // zero words add nothing
+  };
+  if (og < g.ngroups) words(og, 0);
+  const int32_t* x = a.x + static_cast<size_t>(z) * B * K;
+  for (int r = 0; r < B; ++r) {
+    int8_t* hr = hp + r * 16 * LQ;
+    for (int e = threadIdx.x; e < 8 * LQ; e += 256) {  // chain position order: element j + 8t at row j, byte t
+      const int jj = e / LQ, t = e - jj * LQ, k = jj + 8 * t;
+      const int32_t v = (t < g.nb) ? x[static_cast<size_t>(r) * K + k] : 0;  // past the body: 0 = 256*0 + (-128) + 128
+      hr[e] = static_cast<int8_t>(v >> 8);
+      hr[8 * LQ + e] = static_cast<int8_t>((v & 255) - 128);
+    }
+    if (threadIdx.x < 8) tl[r * 8 + threadIdx.x] = (static_cast<int>(threadIdx.x) < g.ntail) ? x[static_cast<size_t>(r) * K + g.K8 + threadIdx.x] : 0;
+  }
+  __syncthreads();
+  for (; og < g.ngroups; og += 2 * gridDim.x) {
+    int32_t sh[B], sl[B];
+#pragma unroll
+    for (int r = 0; r < B; ++r) sh[r] = sl[r] = 0;
+    for (int m0 = 0; m0 < g.Wc; m0 += 8) {
+      if (m0 > 0) words(og, m0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (m0 + q >= g.Wc) break;
+        const uint32_t w0 = w4_i8(w[q], 0), w1 = w4_i8(w[q], 1), w2 = w4_i8(w[q], 2), w3 = w4_i8(w[q], 3);
+#pragma unroll
+        for (int r = 0; r < B; ++r) {
+          const int8_t* hr = hp + r * 16 * LQ + j * LQ + 16 * (m0 + q);
+          const uint4 xh = *reinterpret_cast<const uint4*>(hr);
+          const uint4 xl = *reinterpret_cast<const uint4*>(hr + 8 * LQ);
+          sh[r] = dot4(w3, xh.w, dot4(w2, xh.z, dot4(w1, xh.y, dot4(w0, xh.x, sh[r]))));
+          sl[r] = dot4(w3, xl.w, dot4(w2, xl.z, dot4(w1, xl.y, dot4(w0, xl.x, sl[r]))));
+        }
+      }
+    }
+    const int o = og * kGroup + ol;
+    const bool live = o < g.N;
+    const int32_t rs = live ? a.rowsum[z][o] : 0;
+#pragma unroll
+    for (int r = 0; r < B; ++r) {
+      const int32_t h = isum8_lanes(sh[r]), l = isum8_lanes(sl[r]);
+      if (j == 0 && live) {
+        uint32_t v = static_cast<uint32_t>(h) * 256u + static_cast<uint32_t>(l) + 128u * static_cast<uint32_t>(rs);
+        for (int t = 0; t < g.ntail; ++t)
+          v += static_cast<uint32_t>(static_cast<int32_t>(a.tail[z][o * 8 + t]) * tl[r * 8 + t]);
+        a.acc[(static_cast<size_t>(z) * B + r) * g.N + o] = static_cast<int32_t>(v);
+      }
+    }
+    if (og + 2 * static_cast<int>(gridDim.x) < g.ngroups) words(og + 2 * gridDim.x, 0);
+  }
+}
+
 // 2-bit slab -> fp4 slab (float-mode decode): word m of a chain in pk (16 codes) becomes words
 // 2m and 2m + 1 of pk4 (codes 0..7 and 8..15), code t of a word in nibble t as an E2M1 value
 // (0 -> 0x0, +1 -> 0x2, -1 -> 0xA; all exact), so one v_cvt_scalef32_pk_f32_fp4 turns byte b
@@ -1646,6 +1724,23 @@ hipError_t launch_pack(const int8_t* wq, const Geom& g, uint32_t* pk, int8_t* ta
   (void)hipFree(bad);
   if (e == hipSuccess && hbad) return hipErrorInvalidValue;
   return e;
+}
+
+int seam_max_rows() { return kSeamRows; }
+
+hipError_t launch_seam_dot(const SeamArgs& a, int k, hipStream_t s) {
+  if (a.b < 1 || a.b > kSeamRows || k < 1 || k > kSeamMaxProj) return hipErrorInvalidValue;
+  const size_t lds = static_cast<size_t>(a.b) * (16 * (a.g.Lc + 16) + 8 * sizeof(int32_t));
+  if (lds > static_cast<size_t>(lds_limit())) return hipErrorInvalidValue;
+  // each block reads the rows from host memory once (cheap: 64 blocks x 4 KB measured +0.7 us)
+  const dim3 grid(std::min((a.g.ngroups + 1) / 2, 256), k);
+  switch (a.b) {
+    case 1: k_seam_dot<1><<<grid, 256, lds, s>>>(a); break;
+    case 2: k_seam_dot<2><<<grid, 256, lds, s>>>(a); break;
+    case 3: k_seam_dot<3><<<grid, 256, lds, s>>>(a); break;
+    default: k_seam_dot<4><<<grid, 256, lds, s>>>(a); break;
+  }
+  return hipGetLastError();
 }
 
 size_t pk4_words(const Geom& g) { return static_cast<size_t>(g.ngroups) * 2 * g.Wc * kGroup * 8; }

@@ -2,7 +2,10 @@
 //
 // Host-pointer API: each call uploads its operands to the process's default context
 // (device MMFREE_DEVICE or 0), runs the gfx950 kernels and downloads the result. Projection
-// weights are registered once per distinct (pointer, shape, contents) and stay resident.
+// weights stay resident, one projection per (pointer, shape): each call compares the weights,
+// scale and norm weight at that pointer exactly with the copy last uploaded; other weights are
+// re-uploaded in place, another scale or norm weight replaces the projection (the old one is
+// released), so device memory does not grow with refills.
 // A FixedQ510 bitlinear with an external TernaryBackend follows the reference's split
 // (bitlinear.cpp:39-94): the GPU computes the RMSNorm and the Q5.10 codes, the backend the
 // integer accumulation (batch_size() rows per call, column ranges reported through on_cols),
@@ -19,7 +22,6 @@
 #include <tuple>
 #include <vector>
 
-#include "content_hash.hpp"
 #include "mmfree/hip_backend.hpp"
 #include "mmfree_hip.h"
 
@@ -29,8 +31,6 @@ namespace {
 void check(mmf_ctx* c, int rc, const char* what) {
   if (rc != MMF_OK) throw std::runtime_error(std::string(what) + ": " + mmf_last_error(c));
 }
-
-using detail::content_hash;
 
 struct DevMem {
   mmf_ctx* c;
@@ -47,7 +47,13 @@ struct DevMem {
 struct Default {
   mmf_ctx* c = nullptr;
   std::mutex mu;
-  std::map<std::tuple<const void*, std::size_t, std::size_t, std::uint64_t>, int> projs;
+  struct Cached {
+    int id;
+    std::vector<std::int8_t> wq;  // what was uploaded
+    float scale_w;
+    std::vector<float> normw;
+  };
+  std::map<std::tuple<const void*, std::size_t, std::size_t>, Cached> projs;
   Default() {
     const char* e = std::getenv("MMFREE_DEVICE");
     if (mmf_create(&c, e ? std::atoi(e) : 0) != MMF_OK)
@@ -55,15 +61,26 @@ struct Default {
   }
   ~Default() { mmf_destroy(c); }
   int proj(const int8_t* wq, std::size_t N, std::size_t K, float scale_w, const float* normw) {
-    std::uint64_t h = content_hash(wq, N * K);
-    h = content_hash(&scale_w, sizeof scale_w, h);
-    h = content_hash(normw, K * sizeof(float), h);
-    auto key = std::make_tuple(static_cast<const void*>(wq), N, K, h);
+    const auto key = std::make_tuple(static_cast<const void*>(wq), N, K);
     auto it = projs.find(key);
-    if (it != projs.end()) return it->second;
+    if (it != projs.end()) {
+      Cached& e = it->second;
+      const bool same_norm = std::memcmp(&e.scale_w, &scale_w, sizeof scale_w) == 0 &&
+                             std::memcmp(e.normw.data(), normw, K * sizeof(float)) == 0;
+      if (same_norm) {
+        if (std::memcmp(e.wq.data(), wq, N * K) != 0) {
+          check(c, mmf_proj_update(c, e.id, wq), "mmf_proj_update");
+          std::memcpy(e.wq.data(), wq, N * K);
+        }
+        return e.id;
+      }
+      check(c, mmf_proj_release(c, e.id), "mmf_proj_release");
+      projs.erase(it);
+    }
     int id = -1;
     check(c, mmf_proj_register(c, wq, N, K, scale_w, normw, &id), "mmf_proj_register");
-    projs.emplace(key, id);
+    projs.emplace(key, Cached{id, std::vector<std::int8_t>(wq, wq + N * K), scale_w,
+                              std::vector<float>(normw, normw + K)});
     return id;
   }
 };

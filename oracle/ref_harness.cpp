@@ -121,6 +121,8 @@ void ref_model_close(void* h) { delete static_cast<RefModel*>(h); }
 
 // The reference Model object itself (for attaching a TernaryBackend, ref_hipbe.cpp).
 void* ref_model_ptr(void* h) { return static_cast<RefModel*>(h)->m.get(); }
+// Its Weights (for registering the projections with a resident-weight backend).
+void* ref_model_weights(void* h) { return static_cast<RefModel*>(h)->w.get(); }
 
 // Model::generate; writes the full id stream into out_ids (capacity cap) and returns its
 // length. Sampling per model.hpp:27-31.

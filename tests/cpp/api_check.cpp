@@ -148,6 +148,23 @@ int main(int argc, char** argv) {
   hip.matmul_batch(-1, codes.data(), acc.data(), wbuf.data(), K, N, rows);
   wr(d + "hipbe_reuse_w2.i8", wbuf);
   wr(d + "hipbe_reuse_acc2.i32", acc);
+  {  // the host operator functions' projection cache: one pointer refilled with other weights,
+     // then another norm weight, then another scale (each result must follow the buffer)
+    std::vector<std::int8_t> wb = wq;
+    std::vector<float> nb = nw;
+    bitlinear(out.data(), x.data(), nb.data(), wb.data(), scale, rows, K, N, 1e-6f, nullptr, ActQuant::FixedQ510);
+    wr(d + "bl_refill0.f32", out);
+    wb = wbuf;
+    bitlinear(out.data(), x.data(), nb.data(), wb.data(), scale, rows, K, N, 1e-6f, nullptr, ActQuant::FixedQ510);
+    wr(d + "bl_refill1.f32", out);
+    for (std::size_t k = 0; k < K; ++k) nb[k] *= (k % 3 == 0) ? 1.5f : 0.75f;
+    bitlinear(out.data(), x.data(), nb.data(), wb.data(), scale, rows, K, N, 1e-6f, nullptr, ActQuant::FixedQ510);
+    wr(d + "bl_refill2.f32", out);
+    wr(d + "bl_refill_nw2.f32", nb);
+    bitlinear(out.data(), x.data(), nb.data(), wb.data(), 2.0f * scale, rows, K, N, 1e-6f, nullptr,
+              ActQuant::FixedQ510);
+    wr(d + "bl_refill3.f32", out);
+  }
   std::vector<float> y(rows * K);
   rmsnorm(y.data(), x.data(), nw.data(), rows, K, 1e-6f);
   wr(d + "rmsnorm.f32", y);

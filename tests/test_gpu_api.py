@@ -50,9 +50,42 @@ def ref_hipbe():
     r.lib.ref_model_ptr.argtypes = [C.c_void_p]
     r.lib.ref_hipbe_attach.restype = C.c_void_p
     r.lib.ref_hipbe_attach.argtypes = [C.c_void_p, C.c_int]
+    r.lib.ref_model_weights.restype = C.c_void_p
+    r.lib.ref_model_weights.argtypes = [C.c_void_p]
+    r.lib.ref_hipbe_attach_registered.restype = C.c_void_p
+    r.lib.ref_hipbe_attach_registered.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
     r.lib.ref_hipbe_detach.restype = None
     r.lib.ref_hipbe_detach.argtypes = [C.c_void_p, C.c_void_p]
     return r
+
+
+@pytest.mark.parametrize("name", ["tiny", "small", "odd"])
+def test_reference_model_with_hip_backend_registered(ref_hipbe, blobs, name):
+    """The registry deployment of the seam: every projection registered up front and the tag ->
+    proj_id map handed to the reference's Model::set_backend (model.hpp:74-79)."""
+    print(f"reference Model + HipTernaryBackend with the tag registry, blob={name}", flush=True)
+    blob = blobs(name)
+    rng = np.random.default_rng(43)
+    ids = rng.integers(3, 1000, 9).astype(np.int64)
+    cpu = ref_hipbe.model(blob, FIXED)
+    want_ids = cpu.generate(ids, 12)
+    want_state = cpu.state()
+    prompts = [ids[:5], ids, ids[2:4]]
+    want_serve = cpu.generate_serve(prompts, 6)
+    gpu = ref_hipbe.model(blob, FIXED)
+    be = ref_hipbe.lib.ref_hipbe_attach_registered(ref_hipbe.lib.ref_model_ptr(gpu.h),
+                                                   ref_hipbe.lib.ref_model_weights(gpu.h), 0)
+    assert be
+    try:
+        got_ids = gpu.generate(ids, 12)
+        got_state = gpu.state()
+        got_serve = gpu.generate_serve(prompts, 6)
+    finally:
+        ref_hipbe.lib.ref_hipbe_detach(ref_hipbe.lib.ref_model_ptr(gpu.h), be)
+    np.testing.assert_array_equal(got_ids, want_ids)
+    assert_bitexact(got_state, want_state, "recurrent state")
+    for g, w in zip(got_serve, want_serve):
+        np.testing.assert_array_equal(g, w)
 
 
 @pytest.mark.parametrize("name", ["tiny", "small", "odd"])
@@ -222,6 +255,13 @@ def test_cpp_api(blobs, oracle, ref, tmp_path):
                                   codes.astype(np.int64) @ wq.T.astype(np.int64))
     np.testing.assert_array_equal(np.fromfile(d / "hipbe_reuse_acc2.i32", np.int32).reshape(rows, N),
                                   codes.astype(np.int64) @ w2.T.astype(np.int64))
+    # the host operator functions' projection cache follows a refilled buffer: weights (updated
+    # in place), then norm weight and scale (the projection replaced)
+    nw2 = np.fromfile(d / "bl_refill_nw2.f32", np.float32)
+    for i, (w_, n_, s_) in enumerate([(wq, nw, scale), (w2, nw, scale), (w2, nw2, scale),
+                                      (w2, nw2, float(np.float32(2.0 * scale)))]):
+        assert_bitexact(f32(f"bl_refill{i}.f32", (rows, N)), oracle.bitlinear(x, n_, w_, s_, 1e-6, FIXED)["out"],
+                        f"bitlinear on a refilled buffer, step {i}")
     cl = f32("cluster_cpube.f32", (3, rows, N))
     for j, s in enumerate((scale, 2.0 * scale, 0.5 * scale)):
         assert_bitexact(cl[j], oracle.bitlinear(x, nw, wq, float(np.float32(s)), 1e-6, FIXED)["out"],

@@ -158,6 +158,50 @@ def test_ternary_matmul(eng, oracle, b, K, N):
     np.testing.assert_array_equal(dacc.get(), oracle.ternary_matmul(x, wq))
 
 
+def test_ternary_matmul_host_k_projections(eng, oracle):
+    """mmf_ternary_matmul_host: three projections of different shapes on host buffers in one
+    round trip (the seam's matmul_seq), against the exact integer product; a released
+    projection is refused afterwards and the others keep working."""
+    from matmulfreellmcpu_amd import MmfError
+    rng = np.random.default_rng(19)
+    b = 3
+    shapes = [(1024, 256), (2816, 64), (13, 5)]
+    ws = [rng.integers(-1, 2, (N, K)).astype(np.int8) for K, N in shapes]
+    xs = [rng.integers(-32768, 32768, (b, K)).astype(np.int32) for K, _ in shapes]
+    pids = [eng.register_proj(w, 1.0) for w in ws]
+    for rep in range(2):  # staging buffers reused on the second call
+        accs = eng.ternary_matmul_host(pids, xs)
+        for x, w, a in zip(xs, ws, accs):
+            np.testing.assert_array_equal(a, oracle.ternary_matmul(x, w))
+    # one shape, few rows: the single-kernel path (int32 dot on the resident slab, accumulators
+    # written into the pinned staging); K with a tail, N not a multiple of 16
+    same = [rng.integers(-1, 2, (77, 1003)).astype(np.int8) for _ in range(3)]
+    sp = [eng.register_proj(w, 1.0) for w in same]
+    for b1 in (1, 4):
+        x1 = [rng.integers(-32768, 32768, (b1, 1003)).astype(np.int32) for _ in range(3)]
+        for x, w, a in zip(x1, same, eng.ternary_matmul_host(sp, x1)):
+            np.testing.assert_array_equal(a, oracle.ternary_matmul(x, w))
+    eng.proj_release(pids[1])
+    with pytest.raises(MmfError, match="released"):
+        eng.ternary_matmul_host([pids[1]], [xs[1]])
+    with pytest.raises(MmfError):
+        eng.proj_release(pids[1])
+    accs = eng.ternary_matmul_host([pids[2], pids[0]], [xs[2], xs[0]])
+    np.testing.assert_array_equal(accs[0], oracle.ternary_matmul(xs[2], ws[2]))
+    np.testing.assert_array_equal(accs[1], oracle.ternary_matmul(xs[0], ws[0]))
+
+
+def test_model_projection_cannot_be_released(blobs):
+    from matmulfreellmcpu_amd import FLOAT, Engine, MmfError, read_blob
+    e = Engine(0)
+    try:
+        e.load_blob(read_blob(blobs("tiny")), FLOAT)
+        with pytest.raises(MmfError, match="loaded model"):
+            e.proj_release(0)
+    finally:
+        e.close()
+
+
 def test_elementwise_ops(eng, oracle):
     rng = np.random.default_rng(3)
     for n in (8, 13, 8192 + 5, 20000):
