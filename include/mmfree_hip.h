@@ -117,6 +117,11 @@ int mmf_bitlinear_cluster(mmf_ctx* ctx, const int* proj_ids, int k, int mode, in
 #define MMF_NOALLOC_SCRATCH_BYTES (64u << 20)
 int mmf_bitlinear_noalloc(mmf_ctx* ctx, int proj_id, int mode, int frac_bits, float eps, const float* x,
                           float* out, size_t rows, int32_t* acc);
+/* Device bytes of the grow-only workspace this context holds for the operator entry points
+ * (activation codes and split-K partials of mmf_bitlinear and its kin). It grows with the
+ * largest call and is freed by mmf_destroy; mmf_bitlinear_noalloc adds nothing to it. No
+ * counterpart in the reference: for callers that budget device memory. */
+int mmf_workspace_bytes(mmf_ctx* ctx, size_t* bytes);
 /* The integer input of a FixedQ510 BitLinear, for an external TernaryBackend: the RMSNorm
  * y = (x * rstd) * normw (bitlinear.cpp:62-70) and its Q5.10 codes (simd.hpp:162-187) as int32
  * codes [rows, K] (frac_bits fractional bits). dev pointers. */

@@ -64,6 +64,7 @@ def load_library(path: str = LIB_PATH):
         "mmf_ternary_matmul": (i, [_vp, i, _vp, _vp, _sz]),
         "mmf_ternary_matmul_host": (i, [_vp, i, C.POINTER(i), C.POINTER(_vp), C.POINTER(_vp), _sz]),
         "mmf_proj_release": (i, [_vp, i]),
+        "mmf_workspace_bytes": (i, [_vp, C.POINTER(_sz)]),
         "mmf_bitlinear": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
         "mmf_bitlinear_noalloc": (i, [_vp, i, i, i, C.c_float, _vp, _vp, _sz, _vp]),
         "mmf_bitlinear_cluster": (i, [_vp, C.POINTER(i), i, i, i, C.c_float, _vp, C.POINTER(_vp), _sz]),
@@ -205,6 +206,11 @@ class Engine:
 
     def proj_release(self, pid):
         self._chk(self.lib.mmf_proj_release(self.h, pid))
+
+    def workspace_bytes(self):
+        n = _sz()
+        self._chk(self.lib.mmf_workspace_bytes(self.h, C.byref(n)))
+        return n.value
 
     def rmsnorm(self, y, x, w, rows, cols, eps=1e-6):
         self._chk(self.lib.mmf_rmsnorm(self.h, _ptr(y), _ptr(x), _ptr(w), rows, cols, eps))

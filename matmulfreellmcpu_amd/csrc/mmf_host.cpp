@@ -1344,6 +1344,15 @@ int mmf_bitlinear_noalloc(mmf_ctx* c, int id, int mode, int frac, float eps, con
   });
 }
 
+int mmf_workspace_bytes(mmf_ctx* c, size_t* bytes) {
+  return guard(c, [&] {
+    if (!bytes) fail(MMF_ERR_ARG, "null output");
+    size_t n = 0;
+    for (const DBuf* b : {&c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate, &c->gws}) n += b->n;
+    *bytes = n;
+  });
+}
+
 int mmf_bitlinear_cluster(mmf_ctx* c, const int* ids, int k, int mode, int frac, float eps, const float* x,
                           float* const* outs, size_t rows) {
   return guard(c, [&] {

@@ -95,6 +95,36 @@ def test_noalloc_matches_bitlinear(eng, oracle, first, second, mode):
     _case(eng, oracle, *second, mode, seed=sum(second) + 7 * mode)
 
 
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+def test_noalloc_allocates_nothing(oracle, mode):
+    """On a fresh context the no-alloc entry point leaves the context's grow-only workspace
+    empty (the activation codes and split-K partials live in the static scratch), while one
+    mmf_bitlinear call of the same shape allocates it: the query sees allocations."""
+    from matmulfreellmcpu_amd import Engine
+    e = Engine(0)
+    try:
+        rows, K, N = 40, 2048, 512  # the integer modes split K here: partials in the scratch too
+        rng = np.random.default_rng(31 + mode)
+        x = rng.standard_normal((rows, K)).astype(np.float32)
+        nw = np.ones(K, np.float32)
+        wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+        pid = e.register_proj(wq, 25.0, nw)
+        dx, dout = Buf(e, x), Buf(e, shape=(rows, N))
+        assert e.workspace_bytes() == 0
+        for _ in range(2):
+            e.bitlinear_noalloc(pid, dx.ptr, dout.ptr, rows, mode=mode)
+            e.sync()
+            assert e.workspace_bytes() == 0, "mmf_bitlinear_noalloc allocated workspace"
+        assert_bitexact(dout.get(), oracle.bitlinear(x, nw, wq, 25.0, 1e-6, mode)["out"], "noalloc on a fresh context")
+        e.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=mode)
+        e.sync()
+        assert e.workspace_bytes() > 0
+        dx.free()
+        dout.free()
+    finally:
+        e.close()
+
+
 def test_noalloc_refuses_oversize(eng):
     """A call needing more than the static scratch fails before any launch, with a message."""
     from matmulfreellmcpu_amd import MmfError
