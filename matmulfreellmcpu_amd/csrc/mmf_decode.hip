@@ -84,8 +84,15 @@ __device__ __forceinline__ void load_seg(const float* p, int l, float4 (&d)[RC],
 // step costs one dependent FMA (about 6.4 cycles) instead of an LDS round trip. Wave 0 then
 // writes the stage-1 output to LDS for the encoding pass; the row norm needs no barrier of
 // its own. RC == 0 runs the same chains over LDS rows (any Lc).
+// Integer gate/up launches 352 to 432 blocks of 512 threads: two must share a CU (4 waves per
+// SIMD, at most 128 VGPRs) or the grid runs in two rounds (hidden 2560 needed 129 VGPRs and
+// took 13.3 us per launch). At the register-chain widths the cap costs a few spilled pointers.
+template <int MODE, int KIND, int RC>
+constexpr int kDecMinWaves = (MODE != kFloat && KIND == kGate && RC > 0) ? 4 : 1;
+
 template <int MODE, int KIND, int NV, int KS, int RC, bool W4>
-__global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(DecArgs a) {
+__global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) __attribute__((amdgpu_waves_per_eu(kDecMinWaves<MODE, KIND, RC>)))
+void k_decode(DecArgs a) {
   static_assert(!W4 || (MODE == kFloat && KIND != kLM), "fp4 words are for the float layer GEMVs");
   constexpr int NM = KindTraits<KIND>::NM, NA = KindTraits<KIND>::NA, NP = KindTraits<KIND>::NP;
   constexpr int BM = kBlock * NM;  // threads of one part
@@ -653,47 +660,64 @@ __global__ __launch_bounds__(kBlock * KindTraits<KIND>::NM * KS) void k_decode(D
   }
 }
 
-// Float-mode layer kinds (kIFG, kO, kGate, kDown) at the model widths (chain length Lc = 32 RC),
-// with no barrier before the GEMV. A block is NM waves, wave mi holding matrix mi for the 8
-// outputs 8 blockIdx.x + ol (half of a 16-output slab group): lane 8 ol + j runs the
-// reference's lane chain j of output ol. Every wave works on its own:
+// Batch-1 layer kinds (kIFG, kO, kDown; kGate stays on k_decode) at the model widths (chain
+// length Lc = 32 RC), with no barrier before the GEMV. A block is NM waves, wave mi holding
+// matrix mi for the 8 outputs 8 blockIdx.x + ol (half of a 16-output slab group): lane 8 ol + j
+// runs the reference's lane chain j of output ol. Every wave works on its own:
 //  * it loads its lane segments of the input row, the stage-1 weight (kO: and silu of the
-//    recurrence) and its matrix's BitLinear norm weight (lane 8j + s: segment s of chain j);
+//    recurrence) and its matrix's BitLinear norm weight (lane 8c + s: segment s of chain c);
 //    the pointers of these first loads are the leading kernel parameters, which the launch
 //    preloads into scalar registers, so the loads do not wait for the argument block;
-//  * it copies its own slab words (64 per word row, fp4) into its own LDS slice by DMA;
+//  * it copies its own slab words (64 per word row; float: the fp4 slab, integer modes: the
+//    2-bit slab) into its own LDS slice by DMA;
 //  * it runs both norm chains from registers (a DPP row shift hands each running sum to the
 //    next segment's lane), the same sums in the same order in every wave, and encodes its
-//    activation row y = (x * r2) * w into its own LDS slice from registers;
-//  * it waits for its own DMA and runs its 64 chains over fp4 words.
+//    activation row into its own LDS slice from registers: float y = (x * r2) * w; FixedQ510
+//    the Q5.10 code split into a high and a biased low int8 plane (q = 256 h + l + 128);
+//    Int8Absmax the int8 code at 127 / max|y| (the maximum reduced over the wave);
+//  * it waits for its own DMA and runs its 64 chains: float as in-order fp32 FMAs over fp4
+//    codes; the integer modes as v_dot4 sums (exact, so in any order) of the planes.
 // Only the epilogue of the multi-matrix kinds meets in LDS (one barrier). Outputs, epilogues
 // and the layer-0 token gather are k_decode's.
-template <int KIND, int RC>
+template <int MODE, int KIND, int RC>
+struct DecfShape {
+  static constexpr int NM = KindTraits<KIND>::NM;
+  static constexpr int Lc = 32 * RC, LS = Lc + 4, WL = 8 * LS + 8;  // float rows
+  static constexpr int LQ = Lc + 16;                                   // int8 plane rows (bytes)
+  static constexpr int NW = (MODE == kFloat) ? 4 * RC : 2 * RC;        // slab words per chain
+  // floats of a wave's activation area: float Y; integer: 2 planes, 8 tail codes, the scale
+  static constexpr int ACT = (MODE == kFloat) ? WL : (16 * LQ) / 4 + 8 + 4;
+  static constexpr int SLICE = ACT + NW * 64;  // + the wave's words
+};
+
+template <int MODE, int KIND, int RC>
 __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float* __restrict__ xin,
                                                                    const float* __restrict__ prew,
                                                                    const float* __restrict__ xg,
                                                                    const float* __restrict__ nwa,
                                                                    const float* __restrict__ nwb,
                                                                    const float* __restrict__ nwc, DecArgs a) {
-  static_assert(KIND != kLM, "the lm_head runs k_decode");
-  constexpr int NM = KindTraits<KIND>::NM;
-  constexpr int Lc = 32 * RC, LS = Lc + 4, WL = 8 * LS + 8, NW = 4 * RC;  // NW fp4 words per chain
-  constexpr int SLICE = WL + NW * 64;                                       // floats of a wave's LDS slice
+  static_assert(KIND != kLM && KIND != kGate, "the lm_head and gate/up run k_decode");
+  using S = DecfShape<MODE, KIND, RC>;
+  constexpr int NM = S::NM, LS = S::LS, LQ = S::LQ, NW = S::NW, SLICE = S::SLICE;
   extern __shared__ float smem[];
   const int mi = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // wave = matrix
   const int lane = threadIdx.x & 63, ol = lane >> 3, j = lane & 7;
-  float* Y = smem + mi * SLICE;
-  uint32_t* WXw = reinterpret_cast<uint32_t*>(Y + WL);
+  float* Y = smem + mi * SLICE;                                          // float activations
+  int8_t* Q = reinterpret_cast<int8_t*>(Y);                              // integer: [2][8][LQ] planes
+  int32_t* CT = reinterpret_cast<int32_t*>(Q + 16 * LQ);                 // integer: [8] tail codes
+  float* SA = reinterpret_cast<float*>(CT + 8);                          // Int8Absmax: the row scale
+  uint32_t* WXw = reinterpret_cast<uint32_t*>(Y + S::ACT);
   float* vals = smem + NM * SLICE;  // [NM][8]
   const ProjDev& Pa = a.p[KIND == kIFG ? mi : 0];
   const Geom& g0 = a.p[0].g;
-  const int gK = g0.K, nt = g0.ntail, gN = g0.N, gng = g0.ngroups;
-  const uint32_t* const pk = Pa.pk4;
+  const int gK = g0.K, nt = g0.ntail, gN = g0.N;
+  const uint32_t* const pk = (MODE == kFloat) ? Pa.pk4 : Pa.pk;
   const int8_t* const ptail = Pa.tail;
   const float pinv = Pa.inv_scale_w;
   const float aeps = a.eps;
-  const int nout = (KIND == kGate) ? gN / 2 : gN;
-  const int W = 8 * Lc + 8;
+  const int nout = gN;
+  const int W = 8 * S::Lc + 8;
 
   // layer 0: the token is the argmax over the previous lm_head's per-block keys (every wave
   // reduces all keys itself)
@@ -735,12 +759,12 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   // ---- this wave's slab words: rows m of the half group, 4 rows of 64 words per DMA ---------
   {
     const int og = static_cast<int>(blockIdx.x) >> 1, h = static_cast<int>(blockIdx.x) & 1;
-    const int mrow = (KIND == kGate && mi == 1) ? gng / 2 : 0;  // gate: the up half
-    const uint32_t* sw = pk + static_cast<size_t>(og + mrow) * NW * 128 + 64 * h;
+    const uint32_t* sw = pk + static_cast<size_t>(og) * NW * 128 + 64 * h;
 #pragma unroll
-    for (int c = 0; c < RC; ++c) {
+    for (int c = 0; c < (NW + 3) / 4; ++c) {
       const int m = 4 * c + (lane >> 4);
-      __builtin_amdgcn_global_load_lds(sw + m * 128 + 4 * (lane & 15), (lds_void*)(WXw + 4 * c * 64), 16, 0, 0);
+      if (m < NW)
+        __builtin_amdgcn_global_load_lds(sw + m * 128 + 4 * (lane & 15), (lds_void*)(WXw + 4 * c * 64), 16, 0, 0);
     }
   }
   // ---- epilogue operands (lanes j == 0 of wave 0) ---------------------------------------------
@@ -776,17 +800,58 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
     }
   }
   const float r2 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
-  {
-    // lane 8c + s holds segment s of chain c: row c, floats [4 RC s, 4 RC (s + 1))
+  // the BitLinear input y = (x * r2) * w of the lane's segment (lane 8c + s: chain c, floats
+  // [4 RC s, 4 RC (s + 1))) and of the tail
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const float4 x = xs[c], w = ns[c];
+    xs[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) xt[t] = (xt[t] * r2) * nt8[t];
+  float sa = 0.0f;
+  if constexpr (MODE == kFloat) {
     float4* yr = reinterpret_cast<float4*>(Y + (lane >> 3) * LS + 4 * RC * (lane & 7));
 #pragma unroll
+    for (int c = 0; c < RC; ++c) yr[c] = xs[c];
+    if (lane == 0) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) Y[8 * LS + t] = xt[t];
+    }
+  } else {
+    if constexpr (MODE == kInt8) {  // 127 / max|y| over the row (body and tail), any order
+      float m = 0.0f;
+#pragma unroll
+      for (int c = 0; c < RC; ++c)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xs[c].x), fabsf(xs[c].y)), fmaxf(fabsf(xs[c].z), fabsf(xs[c].w))));
+#pragma unroll
+      for (int t = 0; t < 8; ++t) m = fmaxf(m, fabsf(xt[t]));
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+    }
+    // the lane's 4 RC codes as RC words per plane: row (lane >> 3), bytes [4 RC s, 4 RC (s + 1))
+    uint32_t* qh = reinterpret_cast<uint32_t*>(Q + (lane >> 3) * LQ + 4 * RC * (lane & 7));
+    uint32_t* ql = reinterpret_cast<uint32_t*>(Q + 8 * LQ + (lane >> 3) * LQ + 4 * RC * (lane & 7));
+#pragma unroll
     for (int c = 0; c < RC; ++c) {
-      const float4 x = xs[c], w = ns[c];
-      yr[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+      const float y[4] = {xs[c].x, xs[c].y, xs[c].z, xs[c].w};
+      uint32_t hi = 0, lo = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (MODE == kFixed) {
+          const int32_t q = q510_body(y[u], a.qs);
+          hi |= static_cast<uint32_t>((q >> 8) & 0xFF) << (8 * u);
+          lo |= static_cast<uint32_t>(((q & 0xFF) - 128) & 0xFF) << (8 * u);
+        } else {
+          hi |= static_cast<uint32_t>(q8_of(y[u], sa) & 0xFF) << (8 * u);
+        }
+      }
+      qh[c] = hi;
+      if (MODE == kFixed) ql[c] = lo;
     }
     if (lane == 0) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) Y[8 * LS + t] = (xt[t] * r2) * nt8[t];
+      for (int t = 0; t < 8; ++t) CT[t] = (t < nt) ? ((MODE == kFixed) ? q510_tail(xt[t], a.qs) : q8_of(xt[t], sa)) : 0;
     }
   }
   // the wave's own DMA and LDS writes are complete before any of its lanes reads them
@@ -794,9 +859,10 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- GEMV: chunks of 4 fp4 words, the reads of chunk c + 1 issued before chunk c's FMAs ----
-  float facc = 0.0f;
-  {
+  float val = 0.0f;
+  if constexpr (MODE == kFloat) {
+    // ---- GEMV: chunks of 4 fp4 words, the reads of chunk c + 1 issued before chunk c's FMAs
+    float facc = 0.0f;
     const uint32_t* wl = WXw + lane;
     const float4* yl = reinterpret_cast<const float4*>(Y + j * LS);
     uint32_t wa[4];
@@ -833,19 +899,72 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
         }
       }
     }
-  }
-  facc = hsum8_lanes(facc);  // lane j == 0: the 8 chains of output ol in the hsum_ps order
-  float val = 0.0f;
-  if (j == 0 && o < nout) {
-    const int oo = o + ((KIND == kGate && mi == 1) ? nout : 0);
-    float s = facc;
-    const float* yt = Y + 8 * LS;
-    for (int t = 0; t < nt; ++t) {
-      const int8_t w8 = ptail[oo * 8 + t];
-      if (w8 > 0) s += yt[t];
-      else if (w8 < 0) s -= yt[t];
+    facc = hsum8_lanes(facc);  // lane j == 0: the 8 chains of output ol in the hsum_ps order
+    if (j == 0 && o < nout) {
+      float s = facc;
+      const float* yt = Y + 8 * LS;
+      for (int t = 0; t < nt; ++t) {
+        const int8_t w8 = ptail[o * 8 + t];
+        if (w8 > 0) s += yt[t];
+        else if (w8 < 0) s -= yt[t];
+      }
+      val = s * pinv;
     }
-    val = s * pinv;
+  } else {
+    // ---- GEMV: 2-bit words two at a time (32 codes), v_dot4 on each plane; two independent
+    // accumulators per plane (exact integer sums), the next pair's reads issued first
+    const uint32_t* wl = WXw + lane;
+    const uint4* qh = reinterpret_cast<const uint4*>(Q + j * LQ);
+    const uint4* ql = reinterpret_cast<const uint4*>(Q + 8 * LQ + j * LQ);
+    int32_t h0 = 0, h1 = 0, l0 = 0, l1 = 0;
+    auto pair = [&](uint32_t wv, const uint4& xh, const uint4& xl, int32_t& hh, int32_t& ll) {
+      const uint32_t w0 = w4_i8(wv, 0), w1 = w4_i8(wv, 1), w2 = w4_i8(wv, 2), w3 = w4_i8(wv, 3);
+      hh = dot4(w3, xh.w, dot4(w2, xh.z, dot4(w1, xh.y, dot4(w0, xh.x, hh))));
+      if (MODE == kFixed) ll = dot4(w3, xl.w, dot4(w2, xl.z, dot4(w1, xl.y, dot4(w0, xl.x, ll))));
+    };
+    uint32_t wa[2];
+    uint4 ha[2], la[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      wa[u] = wl[u * 64];
+      ha[u] = qh[u];
+      if (MODE == kFixed) la[u] = ql[u];
+    }
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {  // NW = 2 RC words: RC pairs
+      uint32_t wb[2];
+      uint4 hb[2], lb[2];
+      if (c + 1 < RC) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int m = 2 * (c + 1) + u;
+          wb[u] = wl[m * 64];
+          hb[u] = qh[m];
+          if (MODE == kFixed) lb[u] = ql[m];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      pair(wa[0], ha[0], la[0], h0, l0);
+      pair(wa[1], ha[1], la[1], h1, l1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < RC) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          wa[u] = wb[u];
+          ha[u] = hb[u];
+          if (MODE == kFixed) la[u] = lb[u];
+        }
+      }
+    }
+    int32_t sum = isum8_lanes(h0 + h1);
+    if (MODE == kFixed) sum = sum * 256 + isum8_lanes(l0 + l1);
+    if (j == 0 && o < nout) {
+      int32_t s = sum;
+      if (MODE == kFixed) s += 128 * Pa.rowsum[o];
+      for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[o * 8 + t]) * CT[t];
+      val = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[KIND == kIFG ? mi : 0]
+                             : static_cast<float>(s) / (Pa.scale_w * sa);
+    }
   }
   float v1 = 0.0f, v2 = 0.0f;
   if constexpr (NM > 1) {  // the other matrices' results for the same outputs
@@ -867,55 +986,62 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
     a.recur[p] = silu_of(s, tl);
     a.gout[p] = v2;
     if (a.out) a.out[p] = src0[p];  // layer 0: the embedding row becomes h
-  } else if (KIND == kO || KIND == kDown) {
+  } else {  // kO, kDown
     a.out[p] = e_hin + val;
-  } else {  // kGate
-    a.out[p] = swiglu_of(val, v1, o >= (nout & ~7));
   }
 }
 
-template <int KIND, int RC>
+template <int MODE, int KIND, int RC>
 hipError_t decf_rc(const DecArgs& a, hipStream_t s) {
-  constexpr int NM = KindTraits<KIND>::NM;
-  constexpr int Lc = 32 * RC, WL = 8 * (Lc + 4) + 8, NW = 4 * RC;
-  const size_t lds = (static_cast<size_t>(NM) * (WL + NW * 64) + NM * 8) * sizeof(float);
-  const int nout = (KIND == kGate) ? a.p[0].g.N / 2 : a.p[0].g.N;
-  const int grid = (nout + 7) / 8;
+  using S = DecfShape<MODE, KIND, RC>;
+  const size_t lds = (static_cast<size_t>(S::NM) * S::SLICE + S::NM * 8) * sizeof(float);
+  const int grid = (a.p[0].g.N + 7) / 8;
   const float* prew = (KIND == kDown) ? nullptr : a.pre_w;
   const float* xg = (KIND == kO) ? a.x2 : nullptr;
-  return launch_k(k_decf<KIND, RC>, grid, 64 * NM, lds, s, a.x, prew, xg, a.p[0].normwT, a.p[1].normwT,
+  return launch_k(k_decf<MODE, KIND, RC>, grid, 64 * S::NM, lds, s, a.x, prew, xg, a.p[0].normwT, a.p[1].normwT,
                   a.p[2].normwT, a);
 }
 
-// k_decf for a float layer kind when every matrix has its fp4 slab and the width is a model
-// width; hipErrorNotSupported (nothing launched) otherwise.
-// i/f/g runs it up to hidden size 2048: at 2560 its three waves' own loads of three 10 KB
-// vectors (320 blocks) cost more than k_decode's barriers (measured 9.3 -> 10.1 us per launch).
-// o and down run it at every width.
-template <int KIND>
+// k_decf for a layer kind when every matrix has its slab (float: the fp4 one) and a chain-
+// transposed norm weight and the width is a model width; hipErrorNotSupported (nothing
+// launched) otherwise. Where it runs, by measurement (per-launch microseconds, k_decode ->
+// k_decf):
+//  * float: o and down at every width; i/f/g up to hidden 2048 (at 2560 its three waves' own
+//    loads of three 10 KB vectors over 320 blocks cost more than k_decode's barriers: 9.3 ->
+//    10.1 us);
+//  * FixedQ510 and Int8Absmax: i/f/g and o up to hidden 2048 (370M FixedQ510 i/f/g 5.9 -> 4.8,
+//    o 4.2 -> 3.8 us);
+//  * gate/up never: with 2I outputs it takes 352 to 864 blocks, and their own loads cost more
+//    than the barriers saved (float 370M 4.9 -> 5.0, 2.7B 10.0 -> 13.7 us).
+template <int MODE, int KIND>
 hipError_t decf_kind(const DecArgs& a, hipStream_t s) {
-  constexpr int NP = (KIND == kIFG) ? 3 : 1;  // projections (the gate matrix holds gate and up)
-  for (int z = 0; z < NP; ++z)
-    if (!a.p[z].pk4 || !a.p[z].normwT) return hipErrorNotSupported;
-  const int Lc = a.p[0].g.Lc;
-  if (Lc % 32 != 0 || a.p[0].g.Wc * 2 != Lc / 8) return hipErrorNotSupported;
-  if (KIND == kIFG && Lc > 256) return hipErrorNotSupported;
-  // gate/up stays on k_decode: with 2I outputs it takes 352 to 864 blocks, and their own
-  // loads cost more than the barriers saved (370M 4.9 -> 5.0, 2.7B 10.0 -> 13.7 us per launch)
-  if (KIND == kGate) return hipErrorNotSupported;
-  if constexpr (KIND == kDown) {
-    switch (Lc / 32) {
-      case 11: return decf_rc<KIND, 11>(a, s);
-      case 22: return decf_rc<KIND, 22>(a, s);
-      case 27: return decf_rc<KIND, 27>(a, s);
-      default: return hipErrorNotSupported;
-    }
+  if constexpr (KIND == kGate || KIND == kLM) {
+    return hipErrorNotSupported;
   } else {
-    switch (Lc / 32) {
-      case 4: return decf_rc<KIND, 4>(a, s);
-      case 8: return decf_rc<KIND, 8>(a, s);
-      case 10: return decf_rc<KIND, 10>(a, s);
-      default: return hipErrorNotSupported;
+    constexpr int NP = (KIND == kIFG) ? 3 : 1;
+    for (int z = 0; z < NP; ++z)
+      if (!((MODE == kFloat) ? a.p[z].pk4 : a.p[z].pk) || !a.p[z].normwT) return hipErrorNotSupported;
+    const int Lc = a.p[0].g.Lc;
+    if (Lc % 32 != 0 || a.p[0].g.Wc * 2 != Lc / 8) return hipErrorNotSupported;
+    if (MODE == kFloat && KIND == kIFG && Lc > 256) return hipErrorNotSupported;
+    // the integer modes: i/f/g and o up to hidden 2048 only; down and the 2560-wide kinds keep
+    // k_decode, whose 2 to 4 parts per block split each chain's words (370M FixedQ510 down
+    // 4.77 -> 4.94 us, 2.7B i/f/g 9.1 -> 10.1, o 6.5 -> 7.0, down 8.3 -> 10.8 on k_decf)
+    if (MODE != kFloat && (KIND == kDown || Lc > 256)) return hipErrorNotSupported;
+    if constexpr (KIND == kDown) {
+      switch (Lc / 32) {
+        case 11: return decf_rc<MODE, KIND, 11>(a, s);
+        case 22: return decf_rc<MODE, KIND, 22>(a, s);
+        case 27: return decf_rc<MODE, KIND, 27>(a, s);
+        default: return hipErrorNotSupported;
+      }
+    } else {
+      switch (Lc / 32) {
+        case 4: return decf_rc<MODE, KIND, 4>(a, s);
+        case 8: return decf_rc<MODE, KIND, 8>(a, s);
+        case 10: return decf_rc<MODE, KIND, 10>(a, s);
+        default: return hipErrorNotSupported;
+      }
     }
   }
 }
@@ -983,7 +1109,7 @@ hipError_t dec_kind(const DecArgs& a, size_t lds, int grid, bool w4, hipStream_t
   }
 }
 
-// MMF_DECF=0 keeps the float layer kinds on k_decode (for comparisons); default on.
+// MMF_DECF=0 keeps every layer kind on k_decode (for comparisons); default on.
 bool decf_enabled() {
   static const bool on = [] {
     const char* e = std::getenv("MMF_DECF");
@@ -994,17 +1120,15 @@ bool decf_enabled() {
 
 template <int MODE>
 hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
-  if constexpr (MODE == kFloat) {
-    if (kind != kLM && decf_enabled()) {
-      hipError_t e = hipErrorNotSupported;
-      switch (kind) {
-        case kIFG: e = decf_kind<kIFG>(a, s); break;
-        case kO: e = decf_kind<kO>(a, s); break;
-        case kGate: e = decf_kind<kGate>(a, s); break;
-        default: e = decf_kind<kDown>(a, s); break;
-      }
-      if (e != hipErrorNotSupported) return e;
+  if (kind != kLM && decf_enabled()) {
+    hipError_t e = hipErrorNotSupported;
+    switch (kind) {
+      case kIFG: e = decf_kind<MODE, kIFG>(a, s); break;
+      case kO: e = decf_kind<MODE, kO>(a, s); break;
+      case kGate: e = decf_kind<MODE, kGate>(a, s); break;
+      default: e = decf_kind<MODE, kDown>(a, s); break;
     }
+    if (e != hipErrorNotSupported) return e;
   }
   const Geom& g = a.p[0].g;
   const int Lc = g.Lc;
