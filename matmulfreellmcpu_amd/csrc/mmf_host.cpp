@@ -447,6 +447,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.x = h;
     pa.pre = kPreNorm;
     pa.pre_w = L.attn;
+    pa.pre_wT = L.attnT;
     pa.na = 3;
     for (int k = 0; k < 3; ++k) {
       pa.normw[k] = proj_of(c, L.proj[k]).d.normw;
@@ -507,6 +508,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.x2 = rb;
     pa.pre = kPreSwish;
     pa.pre_w = L.gn;
+    pa.pre_wT = L.gnT;
     pa.na = 1;
     pa.normw[0] = proj_of(c, L.proj[3]).d.normw;
     pa.normwT[0] = proj_of(c, L.proj[3]).d.normwT;
@@ -551,6 +553,7 @@ void layer_rows(mmf_ctx* c, Model& m, int l, int rows, float* h, float* state, b
     pa.x = resid;
     pa.pre = kPreNorm;
     pa.pre_w = L.mlp;
+    pa.pre_wT = L.mlpT;
     pa.na = 1;
     pa.normw[0] = proj_of(c, L.proj[4]).d.normw;
     pa.normwT[0] = proj_of(c, L.proj[4]).d.normwT;
@@ -602,6 +605,7 @@ void lm_rows(mmf_ctx* c, Model& m, int rows, const float* h, float* logits) {
   pa.x = h;
   pa.pre = kPreNorm;
   pa.pre_w = m.norm_w;
+  pa.pre_wT = m.norm_wT;
   pa.na = 1;
   pa.normw[0] = proj_of(c, m.lm).d.normw;
   pa.normwT[0] = proj_of(c, m.lm).d.normwT;

@@ -160,6 +160,7 @@ struct PrologueArgs {
   const float* x;      // [rows, K]
   const float* x2;     // kPreSwish: recurrence output rows [rows, K]; kPreMixSwish: i rows
   const float* pre_w;  // stage-1 norm weight
+  const float* pre_wT; // the same, chain-transposed [8*Lc + 8] (null: not for k_rowseg)
   const float* normw[3];
   const float* normwT[3];  // the same, chain-transposed [8*Lc + 8] (null: the general kernel)
   int na;

@@ -388,8 +388,10 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   }
   if constexpr (KW > 1) {
     // K-group reduction: FixedQ510 folds its planes first (hi * 256 + lo into plane 1, as
-    // the split-K partials do), then groups 1..KW-1 in turn hand their tiles to group 0,
-    // one fragment at a time, through slot 0 (free once every wave has passed a barrier)
+    // the split-K partials do); then in each round groups 1..KW-1 store as many fragments as
+    // a ring slot holds (all of them for the FixedQ510 few-row tiles), group r into slot
+    // r - 1 (free once every wave has passed the barrier that precedes the stores), and after
+    // one more barrier group 0 adds them: 16 bytes per lane per access
     if constexpr (MODE == kFixed) {
 #pragma unroll
       for (int ai = 0; ai < FM; ++ai)
@@ -401,20 +403,39 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
             acc[0][ai][bj][i] = 0;
           }
     }
-    static_assert(NW * 16 * 64 * 4 <= QB, "a fragment of every wave fits one slot");
-    int32_t* red = reinterpret_cast<int32_t*>(q0);  // [NW][16 values][64 lanes]
+    static_assert(KW - 1 <= D, "a ring slot per reduced group");
+    // fragments per round: as many of every wave of a group as one slot holds
+    constexpr int FB = (QB / (NW * 4096)) < FM * FN ? (QB / (NW * 4096)) : FM * FN;
+    static_assert(FB >= 1, "a fragment of every wave of a group fits one slot");
+    auto red_slot = [&](int r) -> v4i* {  // [wave][fragment of the round][quad][lane] as int4
+      return reinterpret_cast<v4i*>(r == 1 ? q0 : (r == 2 ? q1 : (r == 3 ? q2 : q3)));
+    };
 #pragma unroll
-    for (int f = 0; f < FM * FN; ++f) {
-      for (int r = 1; r < KW; ++r) {
-        __syncthreads();
-        if (kg == r) {
+    for (int f0 = 0; f0 < FM * FN; f0 += FB) {
+      __syncthreads();
+      if (kg != 0) {
+        v4i* red = red_slot(kg);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * 64 + lane] = acc[P - 1][f / FN][f % FN][i];
-        }
-        __syncthreads();
-        if (kg == 0) {
+        for (int f = f0; f < f0 + FB && f < FM * FN; ++f)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc[P - 1][f / FN][f % FN][i] += red[(wave * 16 + i) * 64 + lane];
+          for (int q = 0; q < 4; ++q) {
+            const v16i& v = acc[P - 1][f / FN][f % FN];
+            red[((wave * FB + f - f0) * 4 + q) * 64 + lane] = v4i{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+          }
+      }
+      __syncthreads();
+      if (kg == 0) {
+#pragma unroll
+        for (int r = 1; r < KW; ++r) {
+          const v4i* red = red_slot(r);
+#pragma unroll
+          for (int f = f0; f < f0 + FB && f < FM * FN; ++f)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v4i t = red[((wave * FB + f - f0) * 4 + q) * 64 + lane];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[P - 1][f / FN][f % FN][4 * q + e] += t[e];
+            }
         }
       }
     }
@@ -767,7 +788,6 @@ size_t gemm_workspace_bytes(const GemmArgs& a) {
   if (p.ksplit == 1) return 0;
   return static_cast<size_t>(p.ksplit) * a.nmat * a.rows * static_cast<size_t>(a.p[0].g.N) * sizeof(int32_t);
 }
-
 hipError_t launch_gemm_mfma(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   return a.mode == kFixed ? mfma_mode<kFixed>(a, act, s) : mfma_mode<kInt8>(a, act, s);
 }

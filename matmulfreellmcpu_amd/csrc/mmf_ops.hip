@@ -855,6 +855,111 @@ void k_rowpro_split(PrologueArgs a, ActBuf act) {
   encode(0, P, 0);
 }
 
+// The row prologue of a few rows at the model widths (K = 256 RC: no tail, no padding) for
+// the stage kinds without element-wise work (kPreNorm, kPreNone), one wave per row and no
+// wait on other waves. The wave loads its row coalesced (float4 q of lane l is q = l + 64 k)
+// and turns it through LDS into the lane-segment layout of the register chains: lane 8j + s
+// holds steps [4 RC s, 4 RC (s + 1)) of chain j, i.e. chain-transposed floats
+// [4 RC l, 4 RC (l + 1)), the layout in which the stage-1 weight pre_wT and the norm weights
+// normwT are stored. Both order-fixed norm chains then run from registers (seg_sumsq: one
+// dependent FMA per step and a DPP shift between segments), and each lane encodes its own
+// steps, consecutive chain positions: float4 stores of y, or one word of four codes per
+// plane and step quad. Arithmetic and order are those of k_rowpro. (The swish-gate kinds
+// stay on k_rowpro: their silu, sigmoid and swiglu per element on one wave per row measured
+// 13.8 us against k_rowpro's 10.7 us for 64 rows at K = 2560.)
+template <int MODE, int PRE, int NA, int RC>
+__global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
+  static_assert(PRE == kPreNorm || PRE == kPreNone, "element-wise stage kinds run in k_rowpro");
+  constexpr int Lc = 32 * RC, K = 8 * Lc, LS = Lc + 4;
+  __shared__ float X[8 * LS];
+  const int row = xcd_row(blockIdx.x);
+  if (row >= act.rows) return;
+  const int lane = threadIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(a.x + static_cast<size_t>(row) * K);
+
+  // entry loads: the row (natural layout) and the stage-1 weight (segment layout)
+  float4 nx[RC];
+#pragma unroll
+  for (int k = 0; k < RC; ++k) nx[k] = xr[lane + 64 * k];
+  float4 ws[PRE != kPreNone ? RC : 1];
+  if constexpr (PRE != kPreNone) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) ws[c] = reinterpret_cast<const float4*>(a.pre_wT)[lane * RC + c];
+  }
+  // natural float4 q holds elements 4q .. 4q+3: step q / 2 of chains 4 (q % 2) .. 4 (q % 2) + 3
+#pragma unroll
+  for (int k = 0; k < RC; ++k) {
+    const int q = lane + 64 * k, t = q >> 1, j0 = 4 * (q & 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) X[(j0 + c) * LS + t] = f4el(nx[k], c);
+  }
+  __syncthreads();  // one wave: orders the LDS writes before the reads below
+  const int j = lane >> 3, sg = lane & 7;
+  float4 xs[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c) xs[c] = reinterpret_cast<const float4*>(X + j * LS + 4 * RC * sg)[c];
+  const float zt[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if constexpr (PRE != kPreNone) {
+    const float r1 = rstd_of(seg_sumsq<RC>(xs, zt, 0), K, a.eps);
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      float4 x = xs[c];
+      const float4 w = ws[c];
+      x.x = (x.x * r1) * w.x; x.y = (x.y * r1) * w.y; x.z = (x.z * r1) * w.z; x.w = (x.w * r1) * w.w;
+      xs[c] = x;
+    }
+  }
+  const float r2 = rstd_of(seg_sumsq<RC>(xs, zt, 0), K, a.eps);
+
+#pragma unroll
+  for (int ai = 0; ai < NA; ++ai) {
+    const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+    float4 y[RC];
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const float4 w = reinterpret_cast<const float4*>(a.normwT[ai])[lane * RC + c];
+      const float4 x = xs[c];
+      y[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+    }
+    if constexpr (MODE == kFloat) {
+      float* yo = act.y + ar * act.ystride();
+#pragma unroll
+      for (int c = 0; c < RC; ++c) reinterpret_cast<float4*>(yo)[lane * RC + c] = y[c];
+      if (lane < 8) yo[8 * Lc + lane] = 0.0f;
+    } else {
+      float sa = 0.0f;
+      if constexpr (MODE == kInt8) {
+        float m = 0.0f;
+#pragma unroll
+        for (int c = 0; c < RC; ++c)
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(y[c].x), fabsf(y[c].y)), fmaxf(fabsf(y[c].z), fabsf(y[c].w))));
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+        sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+        if (lane == 0) act.sa[ar] = sa;
+      }
+      int8_t* q = act.q + act.qoff(ai, 0, row, 0);
+      const size_t lop = act.qplane();
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        int32_t cd[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cd[e] = (MODE == kFixed) ? q510_body(f4el(y[c], e), a.qs) : q8_of(f4el(y[c], e), sa);
+        const size_t o = ActBuf::qpos(4 * (lane * RC + c));
+        if constexpr (MODE == kFixed) {
+          uint32_t h, l;
+          pack_split4(cd, h, l);
+          *reinterpret_cast<uint32_t*>(q + o) = h;
+          *reinterpret_cast<uint32_t*>(q + lop + o) = l;
+        } else {
+          *reinterpret_cast<uint32_t*>(q + o) = pack_low4(cd);
+        }
+      }
+      if (lane < 8) act.ct[ar * 8 + lane] = 0;
+    }
+  }
+}
+
 // int16-range codes -> split planes (the TernaryBackend path: codes arrive quantised)
 __global__ void k_codes(const int32_t* __restrict__ x, ActBuf act) {
   const int row = xcd_row(blockIdx.x), Lc = act.Lc, nb = act.nb;
@@ -1770,8 +1875,62 @@ static bool rowpro_fits(const ActBuf& act) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// MMF_ROWSEG=0 keeps few-row prologues on k_rowpro (for comparisons); default on.
+static bool rowseg_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("MMF_ROWSEG");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// k_rowseg at the model widths (K = 256 RC: hidden 1024/2048/2560, and without a stage-1
+// norm also 2816/5632/6912), one wave per row: kPreNorm up to kSegRows rows (64 rows at
+// K = 2560: 5.5 us against k_rowpro's 7.1 us), kPreNone (the operator API's BitLinear) up to
+// kSegRowsNone rows (the MLP down projection's 64-row input at K = 6912 measured 8.9 us
+// against k_rowpro's 8.1 us).
+constexpr int kSegRows = 512, kSegRowsNone = 16;
+
+template <int MODE, int PRE, int NA, int RC>
+static hipError_t rowseg_inst(const PrologueArgs& a, ActBuf& act, hipStream_t s) {
+  if constexpr (PRE == kPreNorm || PRE == kPreNone) {
+    k_rowseg<MODE, PRE, NA, RC><<<row_grid(act.rows), 64, 0, s>>>(a, act);
+    return hipGetLastError();
+  } else {
+    return hipErrorNotSupported;
+  }
+}
+
+template <int MODE, int PRE, int NA>
+static hipError_t rowseg_launch(const PrologueArgs& a, ActBuf& act, hipStream_t s) {
+  if (PRE != kPreNorm && PRE != kPreNone) return hipErrorNotSupported;
+  if (act.rows > (PRE == kPreNone ? kSegRowsNone : kSegRows) || act.Lc % 32 != 0 || act.K != 8 * act.Lc ||
+      act.nb != act.Lc || act.ntail != 0)
+    return hipErrorNotSupported;
+  if (PRE != kPreNone && !(a.pre_wT && aligned16(a.pre_wT))) return hipErrorNotSupported;
+  switch (act.Lc / 32) {
+    case 4: return rowseg_inst<MODE, PRE, NA, 4>(a, act, s);
+    case 8: return rowseg_inst<MODE, PRE, NA, 8>(a, act, s);
+    case 10: return rowseg_inst<MODE, PRE, NA, 10>(a, act, s);
+    default: break;
+  }
+  if constexpr (PRE == kPreNone) {
+    switch (act.Lc / 32) {
+      case 11: return rowseg_inst<MODE, PRE, NA, 11>(a, act, s);
+      case 22: return rowseg_inst<MODE, PRE, NA, 22>(a, act, s);
+      case 27: return rowseg_inst<MODE, PRE, NA, 27>(a, act, s);
+      default: break;
+    }
+  }
+  return hipErrorNotSupported;
+}
+
 template <int MODE, int PRE, int NA>
 static hipError_t rowpro_inst(const PrologueArgs& a, ActBuf& act, size_t lds, hipStream_t s) {
+  if (rowseg_enabled()) {
+    const hipError_t e = rowseg_launch<MODE, PRE, NA>(a, act, s);
+    if (e != hipErrorNotSupported) return e;
+  }
   const int need = rowpro_need(act), grid = row_grid(act.rows);
   if constexpr (PRE == kPreNone && NA == 1 && MODE != kInt8) {
     // long rows of many-row launches: half of the row in LDS at a time (k_rowpro_split)
