@@ -188,6 +188,9 @@ void k_decode(DecArgs a) {
     }
     if (KIND == kO || KIND == kDown) e_hin = ahin[po];
   }
+  // FixedQ510 with one group per block: the 128 * rowsum term of lane j == 0's output, now
+  const int32_t e_rs =
+      (MODE == kFixed && !LMG && j == 0 && o0 < nout) ? 128 * prowsum[o0 + ((KIND == kGate && mi == 1) ? nout : 0)] : 0;
 
   // layer 0: the token is the argmax over the previous lm_head's per-block keys
   int64_t tok = 0;
@@ -394,16 +397,11 @@ void k_decode(DecArgs a) {
           const float y[4] = {(x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w};
           if (4 * e < 8 * Lc) {
             uint32_t hi = 0, lo = 0;
+            int32_t cd[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              if (MODE == kFixed) {
-                const int32_t c = q510_body(y[u], aqs);
-                hi |= static_cast<uint32_t>((c >> 8) & 0xFF) << (8 * u);
-                lo |= static_cast<uint32_t>(((c & 0xFF) - 128) & 0xFF) << (8 * u);
-              } else {
-                hi |= static_cast<uint32_t>(q8_of(y[u], sa) & 0xFF) << (8 * u);
-              }
-            }
+            for (int u = 0; u < 4; ++u) cd[u] = (MODE == kFixed) ? q510_body(y[u], aqs) : q8_of(y[u], sa);
+            if (MODE == kFixed) pack_split4(cd, hi, lo);
+            else hi = pack_low4(cd);
             const int jj = (4 * e) / Lc, qp = jj * LQ + (4 * e - jj * Lc);  // byte position
             *reinterpret_cast<uint32_t*>(q + qp) = hi;
             if (MODE == kFixed) *reinterpret_cast<uint32_t*>(q + 8 * LQ + qp) = lo;
@@ -559,7 +557,7 @@ void k_decode(DecArgs a) {
       val = s * pinv;
     } else if (j == 0 && o < nout) {
       int32_t s = sum;
-      if (MODE == kFixed) s += 128 * prowsum[oo];
+      if (MODE == kFixed) s += LMG ? 128 * prowsum[oo] : e_rs;
       for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[oo * 8 + t]) * CT[ai * 8 + t];
       val = (MODE == kFixed) ? static_cast<float>(s) * invfx : static_cast<float>(s) / (pscale * SA[ai]);
     }
@@ -579,8 +577,7 @@ void k_decode(DecArgs a) {
       if (MODE == kFloat) {
         facc = hsum8_lanes(facc);
       } else {
-        sum = isum8_lanes(hacc);
-        if (MODE == kFixed) sum = sum * 256 + isum8_lanes(lacc);
+        sum = isum8_lanes(MODE == kFixed ? hacc * 256 + lacc : hacc);  // one reduction of both planes
       }
       const float val = finish(o, facc, sum);
       if (j != 0 || o >= nout) continue;
@@ -614,8 +611,7 @@ void k_decode(DecArgs a) {
     if (MODE == kFloat) {
       facc = hsum8_lanes(facc);
     } else {
-      sum = isum8_lanes(hacc);
-      if (MODE == kFixed) sum = sum * 256 + isum8_lanes(lacc);
+      sum = isum8_lanes(MODE == kFixed ? hacc * 256 + lacc : hacc);  // one reduction of both planes
       if (KSPLIT) {  // the parts' partial sums meet in LDS, added by part 0
         int32_t* ps = reinterpret_cast<int32_t*>(vals);
         if (j == 0) ps[(part * NM + mi) * 16 + ol] = sum;
@@ -779,6 +775,8 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
     }
     if (KIND == kO || KIND == kDown) e_hin = a.hin[po];
   }
+  // FixedQ510: the output's 128 * rowsum term (lane j == 0 of every matrix), fetched now
+  const int32_t e_rs = (MODE == kFixed && j == 0 && o < nout) ? 128 * Pa.rowsum[o] : 0;
   // ---- both norm chains in every wave, then this wave's activation row -----------------------
   if constexpr (KIND != kDown) {
     const float r1 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
@@ -835,19 +833,17 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
       const float y[4] = {xs[c].x, xs[c].y, xs[c].z, xs[c].w};
-      uint32_t hi = 0, lo = 0;
+      int32_t cd[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (MODE == kFixed) {
-          const int32_t q = q510_body(y[u], a.qs);
-          hi |= static_cast<uint32_t>((q >> 8) & 0xFF) << (8 * u);
-          lo |= static_cast<uint32_t>(((q & 0xFF) - 128) & 0xFF) << (8 * u);
-        } else {
-          hi |= static_cast<uint32_t>(q8_of(y[u], sa) & 0xFF) << (8 * u);
-        }
+      for (int u = 0; u < 4; ++u) cd[u] = (MODE == kFixed) ? q510_body(y[u], a.qs) : q8_of(y[u], sa);
+      if constexpr (MODE == kFixed) {
+        uint32_t hi, lo;
+        pack_split4(cd, hi, lo);
+        qh[c] = hi;
+        ql[c] = lo;
+      } else {
+        qh[c] = pack_low4(cd);
       }
-      qh[c] = hi;
-      if (MODE == kFixed) ql[c] = lo;
     }
     if (lane == 0) {
 #pragma unroll
@@ -956,11 +952,11 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
         }
       }
     }
-    int32_t sum = isum8_lanes(h0 + h1);
-    if (MODE == kFixed) sum = sum * 256 + isum8_lanes(l0 + l1);
+    // both planes in one reduction (per-lane partials stay far inside int32: |hi sum| <= 128 Lc)
+    const int32_t sum = isum8_lanes(MODE == kFixed ? (h0 + h1) * 256 + (l0 + l1) : h0 + h1);
     if (j == 0 && o < nout) {
       int32_t s = sum;
-      if (MODE == kFixed) s += 128 * Pa.rowsum[o];
+      if (MODE == kFixed) s += e_rs;
       for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[o * 8 + t]) * CT[t];
       val = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[KIND == kIFG ? mi : 0]
                              : static_cast<float>(s) / (Pa.scale_w * sa);

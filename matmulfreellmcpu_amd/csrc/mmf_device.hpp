@@ -96,18 +96,31 @@ __device__ __forceinline__ float hsum8(const float* a) {
   return (s0 + s1) + (s2 + s3);
 }
 
+// Lane i + N's value in lane i within each row of 16 lanes (DPP row_shl:N, no memory
+// round trip); lanes whose source lies past their row get zero.
+template <int N>
+__device__ __forceinline__ int dpp_shl(int v) {
+  static_assert(N >= 1 && N <= 15, "row shift");
+  return __builtin_amdgcn_update_dpp(0, v, 0x100 + N, 0xf, 0xf, false);
+}
+template <int N>
+__device__ __forceinline__ float dpp_shl(float v) {
+  return __builtin_bit_cast(float, dpp_shl<N>(__builtin_bit_cast(int, v)));
+}
+
 // The same tree across the 8 consecutive lanes that hold the 8 chain partials of one
-// output (lane j holds a_j). Valid in lane j == 0 of each group of 8.
+// output (lane j holds a_j). Valid in lane j == 0 of each group of 8 (the groups of 8 lie
+// inside the DPP rows of 16, so every source of such a lane is in its row).
 __device__ __forceinline__ float hsum8_lanes(float a) {
-  float s = a + __shfl_down(a, 4, 8);  // lanes 0..3: a_j + a_{j+4}
-  s = s + __shfl_down(s, 1, 8);        // lane 0: s0+s1, lane 2: s2+s3
-  return s + __shfl_down(s, 2, 8);     // lane 0: (s0+s1)+(s2+s3)
+  float s = a + dpp_shl<4>(a);  // lanes 0..3: a_j + a_{j+4}
+  s = s + dpp_shl<1>(s);        // lane 0: s0+s1, lane 2: s2+s3
+  return s + dpp_shl<2>(s);     // lane 0: (s0+s1)+(s2+s3)
 }
 
 __device__ __forceinline__ int32_t isum8_lanes(int32_t a) {
-  a += __shfl_down(a, 4, 8);
-  a += __shfl_down(a, 2, 8);
-  return a + __shfl_down(a, 1, 8);
+  a += dpp_shl<4>(a);
+  a += dpp_shl<2>(a);
+  return a + dpp_shl<1>(a);
 }
 
 // rstd = 1 / sqrt(sumsq / n + eps) (bitlinear.cpp:69, rmsnorm.cpp:19)
@@ -307,6 +320,22 @@ __device__ __forceinline__ int32_t cvt_i32_sat(float v) {
 __device__ __forceinline__ int32_t q8_of(float y, float sa) {
   const int32_t c = cvt_i32_sat(rintf(y * sa));
   return c < -128 ? -128 : (c > 127 ? 127 : c);
+}
+
+// Byte packing of four codes (code 0 in byte 0) for the int8 planes: FixedQ510 hi = bits
+// 8..15 of each code, lo = bits 0..7 minus 128 (the top bit flipped); Int8 the low byte.
+// __builtin_amdgcn_perm(a, b, sel) is v_perm_b32: result byte i = byte sel[i] of the
+// eight bytes b[0..3], a[0..3] (selector 0x0c gives zero).
+__device__ __forceinline__ void pack_split4(const int32_t* c, uint32_t& hi, uint32_t& lo) {
+  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x04000501u);
+  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x04000501u);
+  hi = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+  lo = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+}
+__device__ __forceinline__ uint32_t pack_low4(const int32_t* c) {
+  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x0c0c0400u);
+  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x0c0c0400u);
+  return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
 }
 
 // a / d, correctly rounded, from y = RN(1/d) (Markstein's correction: a first quotient

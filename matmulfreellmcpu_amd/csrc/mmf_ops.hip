@@ -373,22 +373,6 @@ __global__ void k_prologue(PrologueArgs a, ActBuf act) {
   }
 }
 
-// Byte packing of four codes (code 0 in byte 0) for the int8 planes: FixedQ510 hi = bits
-// 8..15 of each code, lo = bits 0..7 minus 128 (the top bit flipped); Int8 the low byte.
-// __builtin_amdgcn_perm(a, b, sel) is v_perm_b32: result byte i = byte sel[i] of the
-// eight bytes b[0..3], a[0..3] (selector 0x0c gives zero).
-__device__ __forceinline__ void pack_split4(const int32_t* c, uint32_t& hi, uint32_t& lo) {
-  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x04000501u);
-  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x04000501u);
-  hi = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-  lo = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
-}
-__device__ __forceinline__ uint32_t pack_low4(const int32_t* c) {
-  const uint32_t p01 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[1]), static_cast<uint32_t>(c[0]), 0x0c0c0400u);
-  const uint32_t p23 = __builtin_amdgcn_perm(static_cast<uint32_t>(c[3]), static_cast<uint32_t>(c[2]), 0x0c0c0400u);
-  return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-}
-
 __device__ __forceinline__ float f4el(const float4& f, int c) {
   return c == 0 ? f.x : (c == 1 ? f.y : (c == 2 ? f.z : f.w));
 }
