@@ -203,10 +203,7 @@ void k_decode(DecArgs a) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) best = k[u] > best ? k[u] : best;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const unsigned long long other = __shfl_xor(best, off);
-      best = other > best ? other : best;
-    }
+    best = wave_max_u64(best);
     unsigned long long* r64 = reinterpret_cast<unsigned long long*>(vals);
     if ((tid & 63) == 0) r64[tid >> 6] = best;
     __syncthreads();
@@ -379,7 +376,7 @@ void k_decode(DecArgs a) {
                                fmaxf(fabsf((x.z * r2) * w.z), fabsf((x.w * r2) * w.w))));
           }
         }
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = wave_max(m);
         if ((tid & 63) == 0) red[8 + (tid >> 6)] = m;
         __syncthreads();
         m = red[8];
@@ -586,10 +583,7 @@ void k_decode(DecArgs a) {
       best = kk > best ? kk : best;
     }
     if (akeys) {  // one partial key per block, reduced by the consumer
-      for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long other = __shfl_xor(best, off);
-        best = other > best ? other : best;
-      }
+      best = wave_max_u64(best);
       unsigned long long* r64 = reinterpret_cast<unsigned long long*>(red);
       if ((tid & 63) == 0) r64[tid >> 6] = best;
       __syncthreads();
@@ -729,10 +723,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
 #pragma unroll
       for (int u = 0; u < 8; ++u) best = k[u] > best ? k[u] : best;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const unsigned long long other = __shfl_xor(best, off);
-      best = other > best ? other : best;
-    }
+    best = wave_max_u64(best);
     int64_t tok = key_index(best);
     if (tok < 0 || tok >= a.vocab) tok = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0 && a.hist) {
@@ -824,7 +815,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
         m = fmaxf(m, fmaxf(fmaxf(fabsf(xs[c].x), fabsf(xs[c].y)), fmaxf(fabsf(xs[c].z), fabsf(xs[c].w))));
 #pragma unroll
       for (int t = 0; t < 8; ++t) m = fmaxf(m, fabsf(xt[t]));
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      m = wave_max(m);
       sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
     }
     // the lane's 4 RC codes as RC words per plane: row (lane >> 3), bytes [4 RC s, 4 RC (s + 1))

@@ -10,6 +10,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <cstdint>
 
 namespace mmf {
@@ -106,6 +108,53 @@ __device__ __forceinline__ int dpp_shl(int v) {
 template <int N>
 __device__ __forceinline__ float dpp_shl(float v) {
   return __builtin_bit_cast(float, dpp_shl<N>(__builtin_bit_cast(int, v)));
+}
+
+// Wave-wide maxima, in every lane, without a memory round trip: butterflies inside each row
+// of 16 lanes (DPP quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8), then the four
+// row maxima by readlane. Call from all 64 lanes of a wave. (Any order gives the same
+// maximum; fmaxf ignores a NaN unless every value is one.)
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  auto step = [](float x, auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    return fmaxf(x, __builtin_bit_cast(float, dpp_mov<C>(__builtin_bit_cast(int, x))));
+  };
+  v = step(v, std::integral_constant<int, 0xB1>{});
+  v = step(v, std::integral_constant<int, 0x4E>{});
+  v = step(v, std::integral_constant<int, 0x124>{});
+  v = step(v, std::integral_constant<int, 0x128>{});
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  auto step = [](unsigned long long x, auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    const unsigned lo = static_cast<unsigned>(dpp_mov<C>(static_cast<int>(x)));
+    const unsigned hi = static_cast<unsigned>(dpp_mov<C>(static_cast<int>(x >> 32)));
+    const unsigned long long y = (static_cast<unsigned long long>(hi) << 32) | lo;
+    return y > x ? y : x;
+  };
+  v = step(v, std::integral_constant<int, 0xB1>{});
+  v = step(v, std::integral_constant<int, 0x4E>{});
+  v = step(v, std::integral_constant<int, 0x124>{});
+  v = step(v, std::integral_constant<int, 0x128>{});
+  unsigned long long best = 0ull;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v), 16 * r));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), 16 * r));
+    const unsigned long long y = (static_cast<unsigned long long>(hi) << 32) | lo;
+    best = y > best ? y : best;
+  }
+  return best;
 }
 
 // The same tree across the 8 consecutive lanes that hold the 8 chain partials of one

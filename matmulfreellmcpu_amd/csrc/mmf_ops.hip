@@ -70,7 +70,7 @@ __device__ float block_max1(float v, float* red) {
 }
 
 __device__ float block_max(float v, float* red) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  v = wave_max(v);
   const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
   if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();
@@ -917,8 +917,7 @@ __global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
 #pragma unroll
         for (int c = 0; c < RC; ++c)
           m = fmaxf(m, fmaxf(fmaxf(fabsf(y[c].x), fabsf(y[c].y)), fmaxf(fabsf(y[c].z), fabsf(y[c].w))));
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+        m = wave_max(m);
         sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
         if (lane == 0) act.sa[ar] = sa;
       }
@@ -1747,10 +1746,7 @@ __global__ void k_argmax_rows(const float* __restrict__ lg, int V, int64_t* __re
       best = k > best ? k : best;
     }
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long other = __shfl_xor(best, o);
-    best = other > best ? other : best;
-  }
+  best = wave_max_u64(best);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
