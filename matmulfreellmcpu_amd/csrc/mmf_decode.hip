@@ -739,7 +739,11 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   load_seg<RC>(src0, lane, xs, xt);
   if constexpr (KIND != kDown) load_seg<RC>(prew, lane, ws, wt);
   if constexpr (KIND == kO) load_seg<RC>(xg, lane, gs, gt);
-  load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
+  // kDown at RC >= 22: row, norm weight and slab words would be 3 RC > 63 loads in flight,
+  // and the wave would stall issuing them until the first ones return; the norm weight's
+  // loads are issued in the middle of the norm chain instead (they are needed after it)
+  constexpr bool DEFER_NW = KIND == kDown && 3 * RC > 60;
+  if constexpr (!DEFER_NW) load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
   // these loads issue first: nothing below (the DMA addresses need argument-block fields) may
   // move above them
   __builtin_amdgcn_sched_barrier(0);
@@ -788,7 +792,9 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
       if (KIND == kO) xt[t] = xt[t] * gt[t];
     }
   }
-  const float r2 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
+  float r2;
+  if constexpr (DEFER_NW) r2 = rstd_of(seg_sumsq_at<RC, 3>(xs, xt, nt, [&] { load_seg<RC>(nwa, lane, ns, nt8); }), gK, aeps);
+  else r2 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
   // the BitLinear input y = (x * r2) * w of the lane's segment (lane 8c + s: chain c, floats
   // [4 RC s, 4 RC (s + 1))) and of the tail
 #pragma unroll

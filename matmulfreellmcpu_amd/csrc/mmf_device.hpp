@@ -267,8 +267,16 @@ __device__ inline float chain_end(const float* X, int LS, int nt, const float* r
 // the lane of the next segment; after round 7 lane 8j + 7 holds chain j. Lanes outside
 // their round sum data that the next shift overwrites. Returns hsum_ps of the 8 chains plus
 // the tail tv[0..nt) (uniform over the wave). Call from all 64 lanes of one wave.
+// seg_sumsq_at runs hook() between rounds HR and HR + 1 (HR < 0: never), fenced against
+// scheduling so that what it issues (loads deferred so as not to fill the wave's 63
+// outstanding memory requests at entry) stays there.
+struct NoHook {
+  __device__ void operator()() const {}
+};
 template <int RC>
-__device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&tv)[8], int nt) {
+__device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&tv)[8], int nt);
+template <int RC, int HR, class F>
+__device__ __forceinline__ float seg_sumsq_at(const float4 (&v)[RC], const float (&tv)[8], int nt, F&& hook) {
   float a = 0.0f;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
@@ -278,6 +286,11 @@ __device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&
       a = __builtin_fmaf(v[c].y, v[c].y, a);
       a = __builtin_fmaf(v[c].z, v[c].z, a);
       a = __builtin_fmaf(v[c].w, v[c].w, a);
+    }
+    if (s == HR) {
+      __builtin_amdgcn_sched_barrier(0);
+      hook();
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (s < 7)
       a = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), 0x111 /* row_shr:1 */,
@@ -291,6 +304,10 @@ __device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&
   for (int t = 0; t < 7; ++t)
     if (t < nt) s = __builtin_fmaf(tv[t], tv[t], s);
   return s;
+}
+template <int RC>
+__device__ __forceinline__ float seg_sumsq(const float4 (&v)[RC], const float (&tv)[8], int nt) {
+  return seg_sumsq_at<RC, -1>(v, tv, nt, NoHook{});
 }
 
 // ---- Cephes exp (simd.hpp:212-249) ----------------------------------------------------
