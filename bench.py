@@ -246,6 +246,24 @@ def measure_prefill(blob_dir, T=2048, modes=("fixed", "int8", "float")):
     return res
 
 
+def serve_leg(blob_dir, cfgs):
+    """Serving steps only, untimed (PRESET:MODE:B:T:STEPS per config): the program of the
+    serving-step counter runs."""
+    from matmulfreellmcpu_amd import MODES, Engine
+    os.makedirs(blob_dir, exist_ok=True)
+    for cfg in cfgs.split(","):
+        preset, mode, B, T, steps = cfg.split(":")
+        B, T, steps = int(B), int(T), int(steps)
+        e = Engine(0)
+        e.load_blob(blob_path(blob_dir, preset), MODES[mode])
+        e.reset(B)
+        cur = e.prefill_streams(np.random.default_rng(1).integers(3, 32000, (B, T)))
+        for _ in range(steps):
+            cur = e.step(cur)
+        e.close()
+        log(f"[bench] serve leg {cfg} done")
+
+
 def measure_serve(blob_dir, preset, B, T, mode_name, steps):
     from matmulfreellmcpu_amd import MODES, Engine
     p = blob_path(blob_dir, preset)
@@ -509,6 +527,9 @@ def main():
     ap.add_argument("--roofline-leg", action="store_true",
                     help="only the 370M float decode with an event pair around every launch (run with "
                          "MMF_GRAPH=0; child process of the roofline, and the command rocprofv3 traces)")
+    ap.add_argument("--serve-leg", default=None, metavar="PRESET:MODE:B:T:STEPS[,...]",
+                    help="only run serving steps (prefill B prompts of T tokens, then STEPS lockstep steps) "
+                         "for each listed config, untimed: the program the serving counter runs profile")
     ap.add_argument("--skip-decode", action="store_true",
                     help="profiling runs of the other sections: no B=1 decode and no headline (the "
                          "printed line holds only the sections run)")
@@ -521,6 +542,9 @@ def main():
     if args.roofline_leg:
         os.makedirs(args.blob_dir, exist_ok=True)
         roofline_leg(args.blob_dir, max(16, args.steps // 4))
+        return
+    if args.serve_leg:
+        serve_leg(args.blob_dir, args.serve_leg)
         return
     if args.vendor_int8:
         T, H, I = (int(x) for x in args.vendor_int8.split(","))
