@@ -45,6 +45,7 @@
 // WM x WN waves that take equal runs of the stages of the same tile, each through its own
 // LDS slots; group 0 adds the others' int32 tiles from LDS and runs the epilogue. That
 // gives more waves per SIMD (or no partials through memory) with the same tile traffic.
+#include <cstdlib>
 #include <type_traits>
 
 #include "mmf_device.hpp"
@@ -403,12 +404,22 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
             acc[0][ai][bj][i] = 0;
           }
     }
-    static_assert(KW - 1 <= D, "a ring slot per reduced group");
-    // fragments per round: as many of every wave of a group as one slot holds
-    constexpr int FB = (QB / (NW * 4096)) < FM * FN ? (QB / (NW * 4096)) : FM * FN;
-    static_assert(FB >= 1, "a fragment of every wave of a group fits one slot");
+    // fragments per round: the most (up to all of them) for which every wave's fragments of
+    // groups 1..KW-1 fit the first min(D, 4) ring slots, GPS groups sharing a slot
+    constexpr int NS = D < 4 ? D : 4;
+    constexpr int FB = [] {
+      for (int fb = FM * FN; fb >= 1; --fb) {
+        const int gps = QB / (NW * fb * 4096);
+        if (gps >= 1 && (KW - 1 + gps - 1) / gps <= NS) return fb;
+      }
+      return 0;
+    }();
+    static_assert(FB >= 1, "the reduced groups fit the ring slots");
+    constexpr int GB = NW * FB * 4096;  // bytes of one group's round
+    constexpr int GPS = QB / GB;
     auto red_slot = [&](int r) -> v4i* {  // [wave][fragment of the round][quad][lane] as int4
-      return reinterpret_cast<v4i*>(r == 1 ? q0 : (r == 2 ? q1 : (r == 3 ? q2 : q3)));
+      const int sl = (r - 1) / GPS, off = ((r - 1) % GPS) * GB;
+      return reinterpret_cast<v4i*>((sl == 0 ? q0 : (sl == 1 ? q1 : (sl == 2 ? q2 : q3))) + off);
     };
 #pragma unroll
     for (int f0 = 0; f0 < FM * FN; f0 += FB) {
@@ -672,12 +683,13 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 // Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
 // that still gives every CU a block (all blocks of all matrices), else 128. Then K is
 // split in powers of two until there are 128 blocks (each split >= 4 stages). A GEMM of
-// 49-64 rows with at least kKGroupTiles tiles replaces its split by four K-groups in one
-// block (kw), whose partial tiles meet in LDS: no partials through memory and no split-K
-// epilogue launch. With fewer tiles each block would stream the whole activation range
-// through one CU, which measured slower than the split (64 x 2560 x 2560: 17.8 against
-// 14.1 us; 64 x 2560 x 13824 with 108 tiles: 18.2 against 21.5 us); at 32-48 rows the
-// split was faster on every shape measured (32 x 2048 x 6144: 12.9 against 16.5 us).
+// 49-64 rows with at least kKGroupTiles (64 x 128) tiles replaces its split by 64 x 64
+// tiles of eight K-groups in one block (kw), whose partial tiles meet in LDS: no partials
+// through memory and no split-K epilogue launch. With fewer tiles each block would stream
+// the whole activation range through one CU, which measured slower than the split (64 x
+// 2560 x 2560: 17.8 against 14.1 us; 64 x 2560 x 13824 with 108 tiles: 18.2 against 21.5 us
+// with four K-groups); at 32-48 rows the split was faster on every shape measured (32 x
+// 2048 x 6144: 12.9 against 16.5 us).
 struct Plan {
   int wm, wn, ksplit, kw;
 };
@@ -706,10 +718,14 @@ Plan plan_of(const GemmArgs& a) {
   // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
-  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && tiles >= kKGroupTiles && nst >= 8) {
-    // (a 4-wave-wide tile never splits: it has >= 256 tiles)
-    p.kw = 4;
-    p.wn = 2;  // 8 waves of 64 x 64 per block: the 512-thread limit of the accumulators' registers
+  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && tiles >= kKGroupTiles && nst >= 16) {
+    // (a 4-wave-wide tile never splits: it has >= 256 tiles) 64 x 64 tiles of eight K-groups,
+    // one wave each, 32-position stages: twice the blocks of 64 x 128 tiles with four K-groups
+    // of two waves, each wave a quarter of the chain of stages (64 rows, FixedQ510: i/f/g
+    // 2560 x 3 x 2560 18.1 -> 16.3 us, gate/up 2560 x 13824 20.1 -> 18.6 us per launch in a
+    // step; the o/down shapes stay on the split, which measured faster than this tiling)
+    p.kw = 8;
+    p.wn = 1;
     p.ksplit = 1;
   }
   // 128 x 128 tiles at one block per CU (the 2048-column o/down GEMMs of a long prefill):
@@ -719,12 +735,12 @@ Plan plan_of(const GemmArgs& a) {
   return p;
 }
 
-template <int MODE, int EPI, int WM, int WN, int KW>
+template <int MODE, int EPI, int WM, int WN, int KW, int KQ = kStageKQ>
 hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream_t s) {
   const int ntile = tiles_of<WM, WN>(a);
   const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
   dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
-  if (!mfma_launch<MODE, EPI, WM, WN, kStageKQ, KW>(a, act, grid, s)) return hipErrorInvalidConfiguration;
+  if (!mfma_launch<MODE, EPI, WM, WN, KQ, KW>(a, act, grid, s)) return hipErrorInvalidConfiguration;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ksplit == 1) return e;
   GemmArgs b = a;
@@ -740,7 +756,7 @@ template <int MODE, int EPI>
 hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Plan p = plan_of(a);
   const int ks = a.ws ? p.ksplit : 1;
-  if (p.kw == 4) return mfma_inst<MODE, EPI, 1, 2, 4>(a, act, ks, s);
+  if (p.kw == 8) return mfma_inst<MODE, EPI, 1, 1, 8, 1>(a, act, ks, s);
   if (p.kw == 2) return mfma_inst<MODE, EPI, 2, 2, 2>(a, act, ks, s);
   if (p.wm == 1)
     return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2, 1>(a, act, ks, s);
