@@ -848,8 +848,8 @@ void k_rowpro_split(PrologueArgs a, ActBuf act) {
 // normwT are stored. Both order-fixed norm chains then run from registers (seg_sumsq: one
 // dependent FMA per step and a DPP shift between segments), and each lane encodes its own
 // steps, consecutive chain positions: float4 stores of y, or one word of four codes per
-// plane and step quad. Arithmetic and order are those of k_rowpro. (The swish-gate kinds
-// stay on k_rowpro: their silu, sigmoid and swiglu per element on one wave per row measured
+// plane and step quad. Arithmetic and order are those of k_rowpro. (The swish-gate kinds run
+// in k_rowseg_sw: their silu, sigmoid and swiglu per element on one wave per row measured
 // 13.8 us against k_rowpro's 10.7 us for 64 rows at K = 2560.)
 template <int MODE, int PRE, int NA, int RC>
 __global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
@@ -940,6 +940,122 @@ __global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
       }
       if (lane < 8) act.ct[ar * 8 + lane] = 0;
     }
+  }
+}
+
+// The swish-gate row prologues (kPreSwish, and kPreMixSwish with the recurrence step of
+// independent streams) of a few rows at the model widths, one 1024-thread block per row: all
+// 16 waves do the element-wise work in natural layout, one float4 per thread (the step's
+// sigmoid, swiglu and state update, then silu of the gate input), and write the row and the
+// gate into LDS in the lane-segment layout of the register chains; wave 0 then runs both
+// order-fixed norm chains from registers (seg_sumsq) and encodes its segments, as k_rowseg.
+// Arithmetic and order are those of k_rowpro (K % 8 == 0: no element is in the reference's
+// scalar tail).
+template <int MODE, int PRE, int RC>
+__global__ __launch_bounds__(1024) void k_rowseg_sw(PrologueArgs a, ActBuf act) {
+  static_assert(PRE == kPreSwish || PRE == kPreMixSwish, "the swish-gate kinds");
+  constexpr bool MIX = PRE == kPreMixSwish;
+  constexpr int Lc = 32 * RC, K = 8 * Lc, LS = Lc + 4, NQ = K / 4;
+  __shared__ float X[8 * LS], S[8 * LS];
+  const int row = xcd_row(blockIdx.x);
+  if (row >= act.rows) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const size_t rK = static_cast<size_t>(row) * K;
+  // wave 0: the stage-1 weight's segments (needed after the LDS round)
+  float4 ws[RC];
+  if (tid < 64) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) ws[c] = reinterpret_cast<const float4*>(a.pre_wT)[lane * RC + c];
+  }
+  for (int q = tid; q < NQ; q += 1024) {
+    const float4 xv = reinterpret_cast<const float4*>(a.x + rK)[q];
+    float4 gv = reinterpret_cast<const float4*>(a.x2 + rK)[q];
+    if constexpr (MIX) {
+      const float4 fv = reinterpret_cast<const float4*>(a.mix_f + rK)[q];
+      const float4 sv = reinterpret_cast<const float4*>(a.mix_state + rK)[q];
+      const float4 lv = a.mix_lb ? reinterpret_cast<const float4*>(a.mix_lb)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float st[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float f = sigmoid_of(f4el(fv, c), false);
+        if (a.mix_lb) {
+          const float lb = f4el(lv, c);
+          f = __builtin_fmaf(1.0f - lb, f, lb);
+        }
+        const float in = swiglu_of(f4el(gv, c), 1.0f - f, false);
+        st[c] = __builtin_fmaf(f, f4el(sv, c), in);
+      }
+      gv = make_float4(st[0], st[1], st[2], st[3]);
+      reinterpret_cast<float4*>(a.mix_state + rK)[q] = gv;
+    }
+    // natural float4 q holds elements 4q .. 4q+3: step q / 2 of chains 4 (q % 2) .. + 3
+    const int t = q >> 1, j0 = 4 * (q & 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      X[(j0 + c) * LS + t] = f4el(xv, c);
+      S[(j0 + c) * LS + t] = silu_of(f4el(gv, c), false);
+    }
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  const int j = lane >> 3, sg = lane & 7;
+  float4 xs[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c) xs[c] = reinterpret_cast<const float4*>(X + j * LS + 4 * RC * sg)[c];
+  const float zt[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const float r1 = rstd_of(seg_sumsq<RC>(xs, zt, 0), K, a.eps);
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    float4 x = xs[c];
+    const float4 w = ws[c];
+    const float4 g = reinterpret_cast<const float4*>(S + j * LS + 4 * RC * sg)[c];
+    x.x = ((x.x * r1) * w.x) * g.x; x.y = ((x.y * r1) * w.y) * g.y;
+    x.z = ((x.z * r1) * w.z) * g.z; x.w = ((x.w * r1) * w.w) * g.w;
+    xs[c] = x;
+  }
+  const float r2 = rstd_of(seg_sumsq<RC>(xs, zt, 0), K, a.eps);
+  const size_t ar = row;  // one projection
+  float4 y[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const float4 w = reinterpret_cast<const float4*>(a.normwT[0])[lane * RC + c];
+    const float4 x = xs[c];
+    y[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+  }
+  if constexpr (MODE == kFloat) {
+    float* yo = act.y + ar * act.ystride();
+#pragma unroll
+    for (int c = 0; c < RC; ++c) reinterpret_cast<float4*>(yo)[lane * RC + c] = y[c];
+    if (lane < 8) yo[8 * Lc + lane] = 0.0f;
+  } else {
+    float sa = 0.0f;
+    if constexpr (MODE == kInt8) {
+      float m = 0.0f;
+#pragma unroll
+      for (int c = 0; c < RC; ++c)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(y[c].x), fabsf(y[c].y)), fmaxf(fabsf(y[c].z), fabsf(y[c].w))));
+      m = wave_max(m);
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+      if (lane == 0) act.sa[ar] = sa;
+    }
+    int8_t* q = act.q + act.qoff(0, 0, row, 0);
+    const size_t lop = act.qplane();
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      int32_t cd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cd[e] = (MODE == kFixed) ? q510_body(f4el(y[c], e), a.qs) : q8_of(f4el(y[c], e), sa);
+      const size_t o = ActBuf::qpos(4 * (lane * RC + c));
+      if constexpr (MODE == kFixed) {
+        uint32_t h, l;
+        pack_split4(cd, h, l);
+        *reinterpret_cast<uint32_t*>(q + o) = h;
+        *reinterpret_cast<uint32_t*>(q + lop + o) = l;
+      } else {
+        *reinterpret_cast<uint32_t*>(q + o) = pack_low4(cd);
+      }
+    }
+    if (lane < 8) act.ct[ar * 8 + lane] = 0;
   }
 }
 
@@ -1868,13 +1984,17 @@ static bool rowseg_enabled() {
 // norm also 2816/5632/6912), one wave per row: kPreNorm up to kSegRows rows (64 rows at
 // K = 2560: 5.5 us against k_rowpro's 7.1 us), kPreNone (the operator API's BitLinear) up to
 // kSegRowsNone rows (the MLP down projection's 64-row input at K = 6912 measured 8.9 us
-// against k_rowpro's 8.1 us).
+// against k_rowpro's 8.1 us); the swish-gate kinds (one projection) on k_rowseg_sw up to
+// kSegRows rows.
 constexpr int kSegRows = 512, kSegRowsNone = 16;
 
 template <int MODE, int PRE, int NA, int RC>
 static hipError_t rowseg_inst(const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   if constexpr (PRE == kPreNorm || PRE == kPreNone) {
     k_rowseg<MODE, PRE, NA, RC><<<row_grid(act.rows), 64, 0, s>>>(a, act);
+    return hipGetLastError();
+  } else if constexpr (NA == 1) {
+    k_rowseg_sw<MODE, PRE, RC><<<row_grid(act.rows), 1024, 0, s>>>(a, act);
     return hipGetLastError();
   } else {
     return hipErrorNotSupported;
@@ -1883,7 +2003,6 @@ static hipError_t rowseg_inst(const PrologueArgs& a, ActBuf& act, hipStream_t s)
 
 template <int MODE, int PRE, int NA>
 static hipError_t rowseg_launch(const PrologueArgs& a, ActBuf& act, hipStream_t s) {
-  if (PRE != kPreNorm && PRE != kPreNone) return hipErrorNotSupported;
   if (act.rows > (PRE == kPreNone ? kSegRowsNone : kSegRows) || act.Lc % 32 != 0 || act.K != 8 * act.Lc ||
       act.nb != act.Lc || act.ntail != 0)
     return hipErrorNotSupported;
