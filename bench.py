@@ -614,8 +614,8 @@ def main():
     value = 1e6 / head["step_us"]
     kern = head["kernels"]
     dom = max(KINDS, key=lambda k: kern[k]["us_per_launch"] * kern[k]["launches_per_token"])
-    # that kind's average launch, each launch between its own event pair, graphs off (a child
-    # process: MMF_GRAPH is read once per process)
+    # that kind's average launch from events recorded at each launch's own start and end
+    # (hipExtLaunchKernelGGL), graphs off (a child process: MMF_GRAPH is read once per process)
     leg_us = None
     try:
         r = subprocess.run([sys.executable, os.path.abspath(__file__), "--roofline-leg", "--steps", str(args.steps),
@@ -644,8 +644,8 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": f"370M float {dom}" + (f" ({traffic_kernel})" if traffic_kernel else ""),
                 "bytes_per_launch": kern[dom]["bytes_per_launch"], "us_per_launch": us,
-                "timing": "event pair around each launch, HIP graphs off" if leg_us else
-                          "graph replay (the event-pair leg failed)",
+                "timing": "the kernel's own start and end events (hipExtLaunchKernelGGL), HIP graphs off" if leg_us
+                          else "graph replay (the event leg failed)",
                 "us_per_launch_graph_replay": kern[dom]["us_per_launch"]}
 
     cpu = None

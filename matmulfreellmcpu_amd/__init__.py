@@ -4,8 +4,11 @@ The engine itself is libmmfree_hip.so (HIP kernels + C ABI) with the C++17 ``mmf
 above it; this module is the ctypes plumbing that the tests and bench.py use. There is no
 fallback: if the library is not built, or no gfx950 device is present, ``Engine()`` raises.
 
-Device buffers for the operator entry points are passed as torch CUDA tensors (or raw
-integer device addresses); torch is only used for device memory.
+Device buffers for the operator entry points are raw device addresses (ints: the tests
+and bench.py allocate them with the library's own ``mmf_malloc`` and fill them with
+``mmf_upload``) or any object with a ``data_ptr()`` method on the same device. Nothing here
+imports torch: torch's bundled HIP runtime cannot open a device that this library's runtime
+already holds in the same process.
 """
 from __future__ import annotations
 
@@ -105,7 +108,7 @@ class MmfError(RuntimeError):
 
 
 def _ptr(x):
-    """Device address of a torch tensor / int, or None."""
+    """Device address of an int, or of an object with data_ptr(), or None."""
     if x is None:
         return None
     if isinstance(x, int):
