@@ -49,6 +49,7 @@ template <> struct KindTraits<kO> { static constexpr int NM = 1, NA = 1, NP = 4;
 template <> struct KindTraits<kGate> { static constexpr int NM = 2, NA = 1, NP = 3; };
 template <> struct KindTraits<kDown> { static constexpr int NM = 1, NA = 1, NP = 2; };
 template <> struct KindTraits<kLM> { static constexpr int NM = 1, NA = 1, NP = 3; };
+template <> struct KindTraits<kOp> { static constexpr int NM = 1, NA = 1, NP = 2; };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -677,7 +678,9 @@ struct DecfShape {
   static constexpr int NW = (MODE == kFloat) ? 4 * RC : 2 * RC;        // slab words per chain
   // floats of a wave's activation area: float Y; integer: 2 planes, 8 tail codes, the scale
   static constexpr int ACT = (MODE == kFloat) ? WL : (16 * LQ) / 4 + 8 + 4;
-  static constexpr int SLICE = ACT + NW * 64;  // + the wave's words
+  // kOp: + the natural row turned into the chain-transposed layout (8 rows of LS floats)
+  static constexpr int TR = (KIND == kOp) ? 8 * LS : 0;
+  static constexpr int SLICE = ACT + NW * 64 + TR;  // + the wave's words (+ the staging)
 };
 
 template <int MODE, int KIND, int RC>
@@ -688,6 +691,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
                                                                    const float* __restrict__ nwb,
                                                                    const float* __restrict__ nwc, DecArgs a) {
   static_assert(KIND != kLM && KIND != kGate, "the lm_head and gate/up run k_decode");
+  constexpr bool ST1 = KIND != kDown && KIND != kOp;  // a stage-1 norm before the BitLinear
   using S = DecfShape<MODE, KIND, RC>;
   constexpr int NM = S::NM, LS = S::LS, LQ = S::LQ, NW = S::NW, SLICE = S::SLICE;
   extern __shared__ float smem[];
@@ -736,13 +740,38 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   // ---- this wave's lane segments (independent of the argument block except at layer 0) ------
   float4 xs[RC], ws[RC], gs[RC], ns[RC];
   float xt[8], wt[8], gt[8], nt8[8];
-  load_seg<RC>(src0, lane, xs, xt);
-  if constexpr (KIND != kDown) load_seg<RC>(prew, lane, ws, wt);
+  if constexpr (KIND == kOp) {
+    // the operator's row in natural order (K = 8 Lc: no tail): float4 q of lane l is
+    // q = l + 64 k, elements 4q .. 4q+3 = step q / 2 of chains 4 (q % 2) .. + 3; through this
+    // wave's staging rows into the lane segments
+    float* T = Y + S::ACT + NW * 64;
+    float4 nx[RC];
+#pragma unroll
+    for (int k = 0; k < RC; ++k) nx[k] = reinterpret_cast<const float4*>(src0)[lane + 64 * k];
+#pragma unroll
+    for (int k = 0; k < RC; ++k) {
+      const int q = lane + 64 * k, t = q >> 1, j0 = 4 * (q & 1);
+      T[(j0 + 0) * LS + t] = nx[k].x;
+      T[(j0 + 1) * LS + t] = nx[k].y;
+      T[(j0 + 2) * LS + t] = nx[k].z;
+      T[(j0 + 3) * LS + t] = nx[k].w;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int c = 0; c < RC; ++c) xs[c] = reinterpret_cast<const float4*>(T + (lane >> 3) * LS + 4 * RC * (lane & 7))[c];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) xt[t] = 0.0f;
+  } else {
+    load_seg<RC>(src0, lane, xs, xt);
+  }
+  if constexpr (ST1) load_seg<RC>(prew, lane, ws, wt);
   if constexpr (KIND == kO) load_seg<RC>(xg, lane, gs, gt);
   // kDown at RC >= 22: row, norm weight and slab words would be 3 RC > 63 loads in flight,
   // and the wave would stall issuing them until the first ones return; the norm weight's
   // loads are issued in the middle of the norm chain instead (they are needed after it)
-  constexpr bool DEFER_NW = KIND == kDown && 3 * RC > 60;
+  constexpr bool DEFER_NW = !ST1 && 3 * RC > 60;
   if constexpr (!DEFER_NW) load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
   // these loads issue first: nothing below (the DMA addresses need argument-block fields) may
   // move above them
@@ -761,7 +790,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   // ---- epilogue operands (lanes j == 0 of wave 0) ---------------------------------------------
   const int o = 8 * static_cast<int>(blockIdx.x) + ol;
   const bool epi = mi == 0 && j == 0 && o < nout;
-  const int po = epi ? ((o < a.oK8) ? (o & 7) * a.oLc + (o >> 3) : 8 * a.oLc + (o - a.oK8)) : 0;
+  const int po = epi ? (KIND == kOp ? o : ((o < a.oK8) ? (o & 7) * a.oLc + (o >> 3) : 8 * a.oLc + (o - a.oK8))) : 0;
   float e_lb = 0.0f, e_st = 0.0f, e_hin = 0.0f;
   if (epi) {
     if (KIND == kIFG) {
@@ -773,7 +802,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   // FixedQ510: the output's 128 * rowsum term (lane j == 0 of every matrix), fetched now
   const int32_t e_rs = (MODE == kFixed && j == 0 && o < nout) ? 128 * Pa.rowsum[o] : 0;
   // ---- both norm chains in every wave, then this wave's activation row -----------------------
-  if constexpr (KIND != kDown) {
+  if constexpr (ST1) {
     const float r1 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
@@ -853,6 +882,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   float val = 0.0f;
+  int32_t stot = 0;  // integer modes: the output's exact accumulator
   if constexpr (MODE == kFloat) {
     // ---- GEMV: chunks of 4 fp4 words, the reads of chunk c + 1 issued before chunk c's FMAs
     float facc = 0.0f;
@@ -955,6 +985,7 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
       int32_t s = sum;
       if (MODE == kFixed) s += e_rs;
       for (int t = 0; t < nt; ++t) s += static_cast<int32_t>(ptail[o * 8 + t]) * CT[t];
+      stot = s;
       val = (MODE == kFixed) ? static_cast<float>(s) * a.inv_fixed[KIND == kIFG ? mi : 0]
                              : static_cast<float>(s) / (Pa.scale_w * sa);
     }
@@ -979,6 +1010,9 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
     a.recur[p] = silu_of(s, tl);
     a.gout[p] = v2;
     if (a.out) a.out[p] = src0[p];  // layer 0: the embedding row becomes h
+  } else if (KIND == kOp) {
+    a.out[p] = val;
+    if (MODE != kFloat && a.acc) a.acc[p] = stot;
   } else {  // kO, kDown
     a.out[p] = e_hin + val;
   }
@@ -989,7 +1023,7 @@ hipError_t decf_rc(const DecArgs& a, hipStream_t s) {
   using S = DecfShape<MODE, KIND, RC>;
   const size_t lds = (static_cast<size_t>(S::NM) * S::SLICE + S::NM * 8) * sizeof(float);
   const int grid = (a.p[0].g.N + 7) / 8;
-  const float* prew = (KIND == kDown) ? nullptr : a.pre_w;
+  const float* prew = (KIND == kDown || KIND == kOp) ? nullptr : a.pre_w;
   const float* xg = (KIND == kO) ? a.x2 : nullptr;
   return launch_k(k_decf<MODE, KIND, RC>, grid, 64 * S::NM, lds, s, a.x, prew, xg, a.p[0].normwT, a.p[1].normwT,
                   a.p[2].normwT, a);
@@ -1020,6 +1054,19 @@ hipError_t decf_kind(const DecArgs& a, hipStream_t s) {
     // the integer modes: i/f/g and o up to hidden 2048 only; down and the 2560-wide kinds keep
     // k_decode, whose 2 to 4 parts per block split each chain's words (370M FixedQ510 down
     // 4.77 -> 4.94 us, 2.7B i/f/g 9.1 -> 10.1, o 6.5 -> 7.0, down 8.3 -> 10.8 on k_decf)
+    if constexpr (KIND == kOp) {
+      // one row of the operator API: the natural row must fill the chains exactly
+      if (a.p[0].g.ntail != 0 || a.p[0].g.nb != Lc) return hipErrorNotSupported;
+      switch (Lc / 32) {
+        case 4: return decf_rc<MODE, KIND, 4>(a, s);
+        case 8: return decf_rc<MODE, KIND, 8>(a, s);
+        case 10: return decf_rc<MODE, KIND, 10>(a, s);
+        case 11: return decf_rc<MODE, KIND, 11>(a, s);
+        case 22: return decf_rc<MODE, KIND, 22>(a, s);
+        case 27: return decf_rc<MODE, KIND, 27>(a, s);
+        default: return hipErrorNotSupported;
+      }
+    }
     if (MODE != kFloat && (KIND == kDown || Lc > 256)) return hipErrorNotSupported;
     if constexpr (KIND == kDown) {
       switch (Lc / 32) {
@@ -1113,6 +1160,7 @@ bool decf_enabled() {
 
 template <int MODE>
 hipError_t dec_mode(DecKind kind, const DecArgs& a, hipStream_t s) {
+  if (kind == kOp) return decf_kind<MODE, kOp>(a, s);
   if (kind != kLM && decf_enabled()) {
     hipError_t e = hipErrorNotSupported;
     switch (kind) {

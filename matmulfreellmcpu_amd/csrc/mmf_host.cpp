@@ -1187,6 +1187,15 @@ struct FixedScratch {
   size_t cap;
 };
 
+// MMF_OPFUSE=0: single-row BitLinear calls take the two-launch path too (comparisons).
+static bool fused_op_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("MMF_OPFUSE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // fs == nullptr: the activations and the split-K partials live in the context's grow-only
 // buffers; otherwise in fs, and nothing is allocated (sizes beyond fs->cap are refused
 // before any launch).
@@ -1207,6 +1216,25 @@ static void bitlinear_impl(mmf_ctx* c, const int* ids, int k, int mode, int frac
     if (!p.d.normw) fail(MMF_ERR_ARG, "projection registered without a norm weight");
   }
   const Mode md = static_cast<Mode>(mode);
+  // one row of one projection: norm, encoding and GEMV in one launch (the batch-1 decode
+  // kernel's operator kind), where it applies (integer modes, model widths, aligned row)
+  if (rows == 1 && k == 1 && fused_op_enabled() && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    DecArgs d{};
+    d.p[0] = p0.d;
+    d.inv_fixed[0] = inv_fixed_of(p0.d.scale_w, frac);
+    d.eps = eps;
+    d.qs = static_cast<float>(1u << frac);
+    d.x = x;
+    d.out = outs[0];
+    d.acc = acc;
+    tbeg(c, kRkGemmIFG);
+    const hipError_t e = launch_decode(kOp, md, d, c->stream);
+    tend(c);
+    if (e != hipErrorNotSupported) {
+      MMF_HIP(e);
+      return;
+    }
+  }
   GemmArgs ga = gemm_args(c, ids, k, static_cast<int>(rows), md, frac);
   for (int z = 0; z < k; ++z) ga.out[z] = outs[z];
   ga.acc[0] = acc;

@@ -61,7 +61,9 @@ struct ProjDev {
 };
 
 // ---- fused single-row decode kernels (mmf_decode.hip) -------------------------------
-enum DecKind : int { kIFG = 0, kO = 1, kGate = 2, kDown = 3, kLM = 4 };
+// kOp: one BitLinear of the operator API on one natural-layout row (no stage-1 norm, the
+// outputs stored in natural order, optional int32 accumulators)
+enum DecKind : int { kIFG = 0, kO = 1, kGate = 2, kDown = 3, kLM = 4, kOp = 5 };
 
 struct DecArgs {
   ProjDev p[3];
@@ -88,6 +90,8 @@ struct DecArgs {
   int hist_cap;
   int wgroups;            // set by launch_decode: output groups per block whose weight words
                           // are copied into LDS at entry (0: read from global in the GEMV)
+  int32_t* acc;           // kOp, integer modes: the int32 accumulators [N] (tails and the
+                          // Q5.10 bias included), or null
 };
 
 // Bytes of dynamic LDS one block may allocate on the current device.
