@@ -90,6 +90,33 @@ def test_op_sweep_int8(eng, oracle, M, K, N):  # noqa: F811
     assert_bitexact(dout.get(), want["out"], f"int8 out M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("mode", [FLOAT, FIXED, INT8])
+@pytest.mark.parametrize("K,N,off", [(1024, 1024, 0), (2560, 2560, 0), (6912, 2560, 0), (2048, 512, 1), (1000, 64, 0)])
+def test_single_row_bitlinear(eng, oracle, mode, K, N, off):  # noqa: F811
+    """One row of one projection: at the model widths (K = 256 RC, 16-byte aligned row) the
+    integer modes run norm, encoding and GEMV in one launch; a row one float off alignment,
+    a width of no register chain (K = 1000) and float mode take the two-launch path. Every
+    case against the oracle, with the int32 accumulators, and rows that saturate Q5.10."""
+    print(f"single row mode={mode} K={K} N={N} off={off}", flush=True)
+    rng = np.random.default_rng(K * 7 + N + mode)
+    x = (rng.standard_normal((1, K)) * 2).astype(np.float32)
+    x[0, :: 97] *= 1e4  # large values: codes at the Q5.10 clamp
+    nw = (1 + 0.2 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, mode)
+    pid = eng.register_proj(wq, sw, nw)
+    buf = np.zeros((1, K + 4), np.float32)
+    buf[0, off:off + K] = x[0]
+    dx, dout = Dev(eng, buf), Dev(eng, shape=(1, N))
+    dacc = Dev(eng, shape=(1, N), dtype=np.int32)
+    eng.bitlinear(pid, dx.ptr + 4 * off, dout.ptr, 1, mode=mode, acc=None if mode == FLOAT else dacc.ptr)
+    eng.sync()
+    if mode != FLOAT:
+        np.testing.assert_array_equal(dacc.get(), want["acc"])
+    assert_bitexact(dout.get(), want["out"], f"single row mode={mode} K={K} N={N}")
+
+
 @pytest.mark.parametrize("K,N", [(2048, 11264), (5632, 2048)])
 def test_op_sweep_fixed_2048(eng, oracle, K, N):  # noqa: F811
     """The two matrix-core-bound sweep shapes at M = 2048 in FixedQ510 (both code planes)."""
