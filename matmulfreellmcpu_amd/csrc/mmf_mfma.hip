@@ -404,6 +404,75 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
             acc[0][ai][bj][i] = 0;
           }
     }
+    // Eight one-wave groups on a whole in-range tile: the sums and the epilogue are shared.
+    // Every group stores its four fragments (two groups per ring slot); then group g adds
+    // row quad g % 4 of row fragment g / 4 (both column groups) over all eight groups and
+    // runs the epilogue for those rows -- eight waves instead of one reading and storing.
+    if constexpr (KW == 8 && NW == 1 && FM == 2 && FN == 2 && QB >= 2 * 4 * 4096 && D >= 4) {
+      const bool whole = row0 + BM <= act.rows && (cgb + BG) * 32 <= N && !accz && !rawacc && ntail == 0 &&
+                         (EPI != kEpiSwigluPair ||
+                          static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
+      if (whole) {
+        auto grp = [&](int g) -> v4i* {  // [fragment][quad][lane] as int4, 16 KB per group
+          const int sl = g >> 1;
+          return reinterpret_cast<v4i*>((sl == 0 ? q0 : (sl == 1 ? q1 : (sl == 2 ? q2 : q3))) + (g & 1) * 16384);
+        };
+        __syncthreads();
+        {
+          v4i* my = grp(kg);
+#pragma unroll
+          for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v16i& v = acc[P - 1][f / FN][f % FN];
+              my[(f * 4 + q) * 64 + lane] = v4i{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            }
+        }
+        __syncthreads();
+        const int ai = kg >> 2, q = kg & 3;
+        v4i tot[FN];
+#pragma unroll
+        for (int bj = 0; bj < FN; ++bj) tot[bj] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const v4i* src = grp(g);
+#pragma unroll
+          for (int bj = 0; bj < FN; ++bj) {
+            const v4i t = src[((ai * FN + bj) * 4 + q) * 64 + lane];
+            tot[bj] = tot[bj] + t;
+          }
+        }
+        // rows rbase + e of this quad (fragment row 8 q + 4 (lane / 32) + e), columns col[bj]
+        const int rb = row0 + ai * 32 + 4 * (lane >> 5) + 8 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb + e;
+          const size_t grow = static_cast<size_t>(r);
+          float val[FN];
+#pragma unroll
+          for (int bj = 0; bj < FN; ++bj) {
+            const int32_t sacc = tot[bj][e] + csum[bj];
+            if constexpr (MODE == kFixed) {
+              val[bj] = static_cast<float>(sacc) * invf;
+            } else {
+              const float den = srow[r - row0];
+              val[bj] = rcp_ok ? div_by_recip(static_cast<float>(sacc), den, srcp[r - row0])
+                               : static_cast<float>(sacc) / den;
+            }
+          }
+          if constexpr (EPI == kEpiSwigluPair) {
+            outz[grow * Nout + col[0]] = swiglu_of(val[0], val[1], false);
+          } else {
+#pragma unroll
+            for (int bj = 0; bj < FN; ++bj) {
+              const size_t o = grow * N + col[bj];
+              outz[o] = (EPI == kEpiAdd) ? addp[o] + val[bj] : val[bj];
+            }
+          }
+        }
+        return;
+      }
+    }
     // fragments per round: the most (up to all of them) for which every wave's fragments of
     // groups 1..KW-1 fit the first min(D, 4) ring slots, GPS groups sharing a slot
     constexpr int NS = D < 4 ? D : 4;
