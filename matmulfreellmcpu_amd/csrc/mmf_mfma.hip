@@ -787,12 +787,14 @@ Plan plan_of(const GemmArgs& a) {
   // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
-  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && tiles >= kKGroupTiles && nst >= 16) {
+  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && (tiles >= kKGroupTiles || nst <= 64) && nst >= 16) {
     // (a 4-wave-wide tile never splits: it has >= 256 tiles) 64 x 64 tiles of eight K-groups,
     // one wave each, 32-position stages: twice the blocks of 64 x 128 tiles with four K-groups
     // of two waves, each wave a quarter of the chain of stages (64 rows, FixedQ510: i/f/g
     // 2560 x 3 x 2560 18.1 -> 16.3 us, gate/up 2560 x 13824 20.1 -> 18.6 us per launch in a
-    // step; the o/down shapes stay on the split, which measured faster than this tiling)
+    // step, before the shared epilogue below); also where fewer tiles have a short K (the o
+    // projection, K = 2560: 16.7 -> 15.5 us against the split and its second kernel; the
+    // down projection, K = 6912, stays on the split: 20.1 against 23.7 us)
     p.kw = 8;
     p.wn = 1;
     p.ksplit = 1;
