@@ -405,23 +405,26 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
           }
     }
     // Eight one-wave groups on a whole in-range tile: the sums and the epilogue are shared.
-    // Every group stores its four fragments (two groups per ring slot); then group g adds
+    // Every group stores its fragments (GPS8 groups per ring slot); then group g < 4 FM adds
     // row quad g % 4 of row fragment g / 4 (both column groups) over all eight groups and
-    // runs the epilogue for those rows -- eight waves instead of one reading and storing.
-    if constexpr (KW == 8 && NW == 1 && FM == 2 && FN == 2 && QB >= 2 * 4 * 4096 && D >= 4) {
+    // runs the epilogue for those rows -- up to eight waves instead of one reading and storing.
+    constexpr int GR = FM * FN * 4096;  // bytes of one group's fragments
+    constexpr int GPS8 = QB / GR;       // groups per ring slot
+    if constexpr (KW == 8 && NW == 1 && FN == 2 && (FM == 1 || FM == 2) && GPS8 >= 2 &&
+                  (8 + GPS8 - 1) / GPS8 <= (D < 4 ? D : 4)) {
       const bool whole = row0 + BM <= act.rows && (cgb + BG) * 32 <= N && !accz && !rawacc && ntail == 0 &&
                          (EPI != kEpiSwigluPair ||
                           static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
       if (whole) {
-        auto grp = [&](int g) -> v4i* {  // [fragment][quad][lane] as int4, 16 KB per group
-          const int sl = g >> 1;
-          return reinterpret_cast<v4i*>((sl == 0 ? q0 : (sl == 1 ? q1 : (sl == 2 ? q2 : q3))) + (g & 1) * 16384);
+        auto grp = [&](int g) -> v4i* {  // [fragment][quad][lane] as int4, GR bytes per group
+          const int sl = g / GPS8;
+          return reinterpret_cast<v4i*>((sl == 0 ? q0 : (sl == 1 ? q1 : (sl == 2 ? q2 : q3))) + (g % GPS8) * GR);
         };
         __syncthreads();
         {
           v4i* my = grp(kg);
 #pragma unroll
-          for (int f = 0; f < 4; ++f)
+          for (int f = 0; f < FM * FN; ++f)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const v16i& v = acc[P - 1][f / FN][f % FN];
@@ -429,6 +432,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
             }
         }
         __syncthreads();
+        if (kg >= FM * 4) return;  // 32-row tiles: four row quads, four waves
         const int ai = kg >> 2, q = kg & 3;
         v4i tot[FN];
 #pragma unroll
@@ -725,10 +729,10 @@ __global__ void k_splitk_epi(GemmArgs a, ActBuf act) {
   }
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int FM = 2>
 int tiles_of(const GemmArgs& a) {
   const int ng32 = (a.p[0].g.N + 31) / 32;
-  return ((ng32 + 2 * WN - 1) / (2 * WN)) * ((a.rows + 64 * WM - 1) / (64 * WM));
+  return ((ng32 + 2 * WN - 1) / (2 * WN)) * ((a.rows + 32 * FM * WM - 1) / (32 * FM * WM));
 }
 
 // 32-position k-chunks per stage (one barrier per stage). 128-position stages measured
@@ -739,9 +743,9 @@ constexpr int kStageKQ = 2;
 // K-group. (Waves of 32 x 128, one row fragment by four column groups, read 40% fewer
 // operand bytes from LDS per product but measured 10-20% slower on every long-prefill
 // shape: twice the weight expansion per product, for no fewer stalls.)
-template <int MODE, int EPI, int TM, int TN, int KQ, int KW>
+template <int MODE, int EPI, int TM, int TN, int KQ, int KW, int FM = 2>
 bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s) {
-  constexpr int WM = TM, WN = TN, FM = 2, FN = 2;
+  constexpr int WM = TM, WN = TN, FN = 2;
   constexpr int bytes =
       ring_depth<MODE, WM, WN, FM, FN, KQ, KW>() * KW * stage_bytes<MODE, WM, WN, FM, FN, KQ>() + row_scale_bytes<MODE, WM, FM>();
   if (bytes > lds_limit()) return false;
@@ -761,7 +765,15 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 // 2048 x 6144: 12.9 against 16.5 us).
 struct Plan {
   int wm, wn, ksplit, kw;
+  int fm = 2;  // 32-row fragments per wave (1: 32-row tiles)
 };
+static bool kw8_rows32() {
+  static const bool on = [] {
+    const char* e = std::getenv("MMF_KW8_32");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
 constexpr int kKGroupTiles = 48;
 
 Plan plan_of(const GemmArgs& a) {
@@ -787,6 +799,10 @@ Plan plan_of(const GemmArgs& a) {
   // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
+  if (kw8_rows32() && a.rows > 16 && a.rows <= 32 && p.ksplit > 1 && nst <= 64 && nst >= 16) {
+    p = Plan{1, 1, 1, 8, 1};
+    return p;
+  }
   if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && (tiles >= kKGroupTiles || nst <= 64) && nst >= 16) {
     // (a 4-wave-wide tile never splits: it has >= 256 tiles) 64 x 64 tiles of eight K-groups,
     // one wave each, 32-position stages: twice the blocks of 64 x 128 tiles with four K-groups
@@ -806,12 +822,12 @@ Plan plan_of(const GemmArgs& a) {
   return p;
 }
 
-template <int MODE, int EPI, int WM, int WN, int KW, int KQ = kStageKQ>
+template <int MODE, int EPI, int WM, int WN, int KW, int KQ = kStageKQ, int FM = 2>
 hipError_t mfma_inst(const GemmArgs& a, const ActBuf& act, int ksplit, hipStream_t s) {
-  const int ntile = tiles_of<WM, WN>(a);
+  const int ntile = tiles_of<WM, WN, FM>(a);
   const int nz = EPI == kEpiSwigluPair ? 1 : a.nmat;
   dim3 grid(8 * ((ntile + 7) / 8), ksplit, nz);
-  if (!mfma_launch<MODE, EPI, WM, WN, KQ, KW>(a, act, grid, s)) return hipErrorInvalidConfiguration;
+  if (!mfma_launch<MODE, EPI, WM, WN, KQ, KW, FM>(a, act, grid, s)) return hipErrorInvalidConfiguration;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ksplit == 1) return e;
   GemmArgs b = a;
@@ -827,7 +843,8 @@ template <int MODE, int EPI>
 hipError_t mfma_epi(const GemmArgs& a, const ActBuf& act, hipStream_t s) {
   const Plan p = plan_of(a);
   const int ks = a.ws ? p.ksplit : 1;
-  if (p.kw == 8) return mfma_inst<MODE, EPI, 1, 1, 8, 1>(a, act, ks, s);
+  if (p.kw == 8)
+    return p.fm == 1 ? mfma_inst<MODE, EPI, 1, 1, 8, 1, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 1, 8, 1>(a, act, ks, s);
   if (p.kw == 2) return mfma_inst<MODE, EPI, 2, 2, 2>(a, act, ks, s);
   if (p.wm == 1)
     return p.wn == 4 ? mfma_inst<MODE, EPI, 1, 4, 1>(a, act, ks, s) : mfma_inst<MODE, EPI, 1, 2, 1>(a, act, ks, s);
