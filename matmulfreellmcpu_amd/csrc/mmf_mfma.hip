@@ -274,11 +274,13 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   // one stage of every K-group ([KW][SS] bytes). Every wave moves its share of a stage (DA
   // activation transfers of 1 KB, DB weight transfers of 256 B) from global memory straight
   // into a slot with buffer loads into LDS (lds_dma16/4: lane l's bytes land at the
-  // transfer's base + l * size), D - 1 stages ahead: no registers and no LDS stores on the way. Before stage st a
-  // wave waits until only the later stages' transfers are outstanding, and one barrier per
-  // stage publishes slot st % D to the block and frees the slot of stage st - 1 for stage
-  // st + D - 1. Loads past the block's last stage repeat that stage (never read), so every
-  // stage issues the same transfers and the wait count is a constant.
+  // transfer's base + l * size), D - 1 stages ahead: no registers and no LDS stores on the
+  // way. Before stage st a wave waits until only the later stages' transfers are
+  // outstanding, and one barrier per stage publishes slot st % D to the block and frees the
+  // slot of stage st - 1 for stage st + D - 1. Nothing is issued past the loop's last stage
+  // (the wait counts shrink over the last D - 2 stages): repeated loads there took a third
+  // of the transfers of a 10-stage loop through the CU's memory pipeline, which bounds
+  // these loops.
   constexpr int D = ring_depth<MODE, WM, WN, FM, FN, KQ, KW>();
   constexpr int NT = DA + DB;  // transfers per wave per stage
   static_assert(D >= 3 && D <= 6 && (D - 2) * NT < 64, "ring depth");
@@ -306,13 +308,25 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   };
   auto stage = [&](auto sc, int st) {
     constexpr int S = decltype(sc)::value;
-    // this wave's reads of the previous stage have returned (a group past its run issues
-    // reads it never waits for) and its transfers of stage st have landed
+    // this wave's reads of the previous stage have returned and its transfers of stage st
+    // have landed: only the transfers of the later stages already issued (up to D - 2 of
+    // them; fewer in the last stages, which issue nothing past the run) may be outstanding
     wait_lds();
-    wait_vm<(D - 2) * NT>();
+    const int ahead = min(D - 2, cnt - 1 - st);
+    if (ahead >= D - 2) {
+      wait_vm<(D - 2) * NT>();
+    } else if (ahead == 0) {
+      wait_vm<0>();
+    } else if (ahead == 1) {
+      wait_vm<NT>();
+    } else if (ahead == 2) {
+      wait_vm<2 * NT>();
+    } else {
+      wait_vm<3 * NT>();
+    }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    issue(ic<(S + D - 1) % D>{}, st + D - 1);
+    if (st + D - 1 < cnt) issue(ic<(S + D - 1) % D>{}, st + D - 1);
     const unsigned char* sb = slot(sc) + kg * SS;
     uint32_t bw[KQ][FN];
     v4i av[KQ][P][FM];
@@ -350,10 +364,10 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   };
   if (cnt > 0) {
     issue(ic<0>{}, 0);
-    issue(ic<1>{}, 1);
-    if constexpr (D > 3) issue(ic<2>{}, 2);
-    if constexpr (D > 4) issue(ic<3>{}, 3);
-    if constexpr (D > 5) issue(ic<4>{}, 4);
+    if (cnt > 1) issue(ic<1>{}, 1);
+    if constexpr (D > 3) if (cnt > 2) issue(ic<2>{}, 2);
+    if constexpr (D > 4) if (cnt > 3) issue(ic<3>{}, 3);
+    if constexpr (D > 5) if (cnt > 4) issue(ic<4>{}, 4);
     int st = 0;
     for (; st + D <= cnt; st += D) {  // straight-line runs of D stages: compile-time slots
       stage(ic<0>{}, st);
@@ -755,14 +769,11 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 
 // Tile shape: 64 rows for short row ranges (batched decode), else 128; 256 columns when
 // that still gives every CU a block (all blocks of all matrices), else 128. Then K is
-// split in powers of two until there are 128 blocks (each split >= 4 stages). A GEMM of
-// 49-64 rows with at least kKGroupTiles (64 x 128) tiles replaces its split by 64 x 64
-// tiles of eight K-groups in one block (kw), whose partial tiles meet in LDS: no partials
-// through memory and no split-K epilogue launch. With fewer tiles each block would stream
-// the whole activation range through one CU, which measured slower than the split (64 x
-// 2560 x 2560: 17.8 against 14.1 us; 64 x 2560 x 13824 with 108 tiles: 18.2 against 21.5 us
-// with four K-groups); at 32-48 rows the split was faster on every shape measured (32 x
-// 2048 x 6144: 12.9 against 16.5 us).
+// split in powers of two until there are 128 blocks (each split >= 4 stages). A split GEMM
+// of 49-64 rows with K <= 6912 and enough tiles (at least kKGroupTiles 64 x 128 tiles, or
+// at least 64 32 x 64 tiles, or at most 64 stages) runs instead on tiles of eight K-groups
+// in one block (kw), whose partial tiles meet in LDS: no partials through memory and no
+// split-K epilogue launch; 17-32 rows take 32 x 64 such tiles at K <= 4096.
 struct Plan {
   int wm, wn, ksplit, kw;
   int fm = 2;  // 32-row fragments per wave (1: 32-row tiles)
@@ -803,17 +814,23 @@ Plan plan_of(const GemmArgs& a) {
     p = Plan{1, 1, 1, 8, 1};
     return p;
   }
-  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && (tiles >= kKGroupTiles || nst <= 64) && nst >= 16) {
-    // (a 4-wave-wide tile never splits: it has >= 256 tiles) 64 x 64 tiles of eight K-groups,
-    // one wave each, 32-position stages: twice the blocks of 64 x 128 tiles with four K-groups
+  const int t32 = tiles_of<1, 1, 1>(a) * nz;  // 32 x 64 tiles
+  if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && nst >= 16 && nst <= 216 &&
+      (tiles >= kKGroupTiles || nst <= 64 || t32 >= 64)) {
+    // (a 4-wave-wide tile never splits: it has >= 256 tiles) tiles of eight K-groups, one
+    // wave each, 32-position stages: twice the blocks of 64 x 128 tiles with four K-groups
     // of two waves, each wave a quarter of the chain of stages (64 rows, FixedQ510: i/f/g
     // 2560 x 3 x 2560 18.1 -> 16.3 us, gate/up 2560 x 13824 20.1 -> 18.6 us per launch in a
-    // step, before the shared epilogue below); also where fewer tiles have a short K (the o
-    // projection, K = 2560: 16.7 -> 15.5 us against the split and its second kernel; the
-    // down projection, K = 6912, stays on the split: 20.1 against 23.7 us)
+    // step, before the shared epilogue below). 32 x 64 tiles where they still fit one block
+    // per CU: twice the blocks, half the activation rows streamed through each CU (2.7B x 64
+    // FixedQ510 step, per launch: i/f/g 11.0 -> 8.2 us, o 12.9 -> 9.8 us; the down
+    // projection, K = 6912, 14.5 us against 10.7 us for the split plus 5.1 us for its
+    // epilogue launch, whose writes also delayed the next launch by 3.5 us); else 64 x 64
+    // (gate/up: 432 32 x 64 tiles would take two rounds, 18.0 against 11.8 us).
     p.kw = 8;
     p.wn = 1;
     p.ksplit = 1;
+    if (t32 <= 256) p.fm = 1;
   }
   // 128 x 128 tiles at one block per CU (the 2048-column o/down GEMMs of a long prefill):
   // two K-groups per block give each SIMD two waves instead of one, with the same tile
