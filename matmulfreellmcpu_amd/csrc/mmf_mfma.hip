@@ -176,12 +176,29 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   const int z = blockIdx.z;
   const ProjDev& W = a.p[z];
   const int N = W.g.N, Lc = act.Lc;
+  // every argument the block reads, in one batch of scalar loads before the first branch
+  // (a load placed after a branch waits for its own round trip)
+  float* const outz = a.out[EPI == kEpiSwigluPair ? 0 : z];
+  int32_t* const accz = a.acc[z];
+  int32_t* const wsp = a.ws;
+  const float* const addp = a.add;
+  const int8_t* const tailp = W.tail;
+  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = W.g.ntail;
+  const float invf = a.inv_fixed[z], scw = W.scale_w;
+  const int8_t* const aq = act.q;
+  const uint32_t* const pkm = W.pkm;
+  const int32_t* const rsum = W.rowsum;
+  const float* const asa = act.sa;
+  const int32_t* const act_ct = act.ct;
+  const int arows = act.rows, ana = act.na, ksp = gridDim.y;
+  MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rawacc), "s"(swn), "s"(ntail), "s"(invf),
+          "s"(scw), "s"(aq), "s"(pkm), "s"(rsum), "s"(asa), "s"(act_ct), "s"(arows), "s"(ana), "s"(ksp), "s"(Lc));
   const int ng32 = (N + 31) / 32;
   // XCD-aware tile order: blocks are dealt to the 8 XCDs round-robin by block index, so
   // block i runs on XCD i % 8; that XCD takes the i / 8-th tile of its own contiguous
   // share of the row-major tile list. Concurrent blocks of one XCD then walk the column
   // tiles of the same row tiles, and their activation rows stay in that XCD's L2.
-  const int nct = (ng32 + BG - 1) / BG, nrt = (act.rows + BM - 1) / BM;
+  const int nct = (ng32 + BG - 1) / BG, nrt = (arows + BM - 1) / BM;
   const int ntile = nct * nrt, share = (ntile + 7) / 8;
   const int tile = (blockIdx.x & 7) * share + (blockIdx.x >> 3);
   if (tile >= ntile) return;
@@ -194,15 +211,17 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   const int wm = wave / WN, wn = wave % WN;  // this wave: row fragments wm*FM.., groups wn*FN..
   const int row0 = (tile / nct) * BM;
   const int cgb = (tile % nct) * BG;
-  const int am = (act.na > 1) ? z : 0;
+  const int am = (ana > 1) ? z : 0;
   // stage range of this block's split (all stages without split-K)
-  const int nall = Lc / (4 * KQ), ksp = gridDim.y, ks = blockIdx.y;
-  const int st0 = static_cast<int>((static_cast<long>(nall) * ks) / ksp);
-  const int nst = static_cast<int>((static_cast<long>(nall) * (ks + 1)) / ksp) - st0;
+  const int nall = Lc / (4 * KQ), ks = blockIdx.y;
+  // (nall * ksp < 2^31: 32-bit quotients; none without a split)
+  const int st0 = ksp == 1 ? 0 : static_cast<int>(static_cast<unsigned>(nall * ks) / static_cast<unsigned>(ksp));
+  const int nst = ksp == 1 ? nall
+                           : static_cast<int>(static_cast<unsigned>(nall * (ks + 1)) / static_cast<unsigned>(ksp)) - st0;
   const int cnt = (nst + KW - 1) / KW;           // loop stages of every group
   const int gb = kg * cnt;                       // the group's first stage (from st0)
   const int ng = max(0, min(cnt, nst - gb));     // stages the group multiplies
-  const int8_t* qbase = act.q + 2 * static_cast<size_t>(am) * act.qplane();
+  const int8_t* qbase = aq + 2 * static_cast<size_t>(am) * act.qplane();
 
   // per-lane sources of this wave's transfers (advanced by KQ fragments = KQ KB of the
   // fragment-tiled activations / KQ x 256 B of weights per stage). Row groups past the last
@@ -210,7 +229,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   // again; their products are never stored. (Byte offsets from the matrix's planes and
   // from its weights: both below 2^31, which launch_gemm checks.)
   const u32x4 arsrc = raw_rsrc(qbase, static_cast<uint32_t>(P * act.qplane()));
-  const u32x4 brsrc = raw_rsrc(W.pkm, static_cast<uint32_t>(ng32 * (Lc / 4) * 256));
+  const u32x4 brsrc = raw_rsrc(pkm, static_cast<uint32_t>(ng32 * (Lc / 4) * 256));
   uint32_t aoff[DA];
   const int lastg = act.rows32() / 32 - 1;
 #pragma unroll
@@ -232,12 +251,14 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
 
   // epilogue operands that do not depend on the accumulators, fetched before the main loop
   // so their latency hides behind it: per-row int8 scales (one per lane, to LDS after the
-  // loop), per-column Q5.10 offsets (128 * rowsum)
+  // loop), per-column Q5.10 offsets (128 * rowsum). Every wave loads them, from clamped
+  // (in-range) indices, and selects afterwards: a load inside a branch is waited for at
+  // the branch's end, a memory round trip before the first transfer is issued.
   float sv = 0.0f;
-  if (MODE == kInt8 && kg == 0 && wave * 64 < BM) {
-    int row = row0 + wave * 64 + lane;
-    row = row < act.rows ? row : act.rows - 1;
-    sv = act.sa[static_cast<size_t>(am) * act.rows + row];
+  if constexpr (MODE == kInt8) {
+    int row = row0 + (wave * 64 + lane) % BM;
+    row = row < arows ? row : arows - 1;
+    sv = asa[static_cast<size_t>(am) * arows + row];
   }
   const int Nout = (EPI == kEpiSwigluPair) ? N / 2 : N;
   const int ol = lane & 31;
@@ -249,17 +270,12 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   for (int bj = 0; bj < FN; ++bj) {
     const int cg = cgb + wn * FN + bj;
     col[bj] = (EPI == kEpiSwigluPair) ? (cg >> 1) * 32 + ol + ((bj & 1) ? Nout : 0) : cg * 32 + ol;
-    csum[bj] = (MODE == kFixed && ksp == 1 && col[bj] < N) ? 128 * W.rowsum[col[bj]] : 0;
+    csum[bj] = 0;
+    if constexpr (MODE == kFixed) {
+      const int32_t rs = rsum[col[bj] < N ? col[bj] : N - 1];
+      csum[bj] = (ksp == 1 && col[bj] < N) ? 128 * rs : 0;
+    }
   }
-  float* const outz = a.out[EPI == kEpiSwigluPair ? 0 : z];
-  int32_t* const accz = a.acc[z];
-  int32_t* const wsp = a.ws;
-  const float* const addp = a.add;
-  const int8_t* const tailp = W.tail;
-  const int rawacc = a.raw_acc ? 1 : 0, swn = a.swiglu_n, ntail = W.g.ntail;
-  const float invf = a.inv_fixed[z], scw = W.scale_w;
-  MMF_PIN("s"(outz), "s"(accz), "s"(wsp), "s"(addp), "s"(tailp), "s"(rawacc), "s"(swn), "s"(ntail), "s"(invf),
-          "s"(scw));
 
   v16i acc[P][FM][FN];
 #pragma unroll
@@ -393,7 +409,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   bool rcp_ok = false;
   if (MODE == kInt8) {
     bool ok = true;
-    if (kg == 0 && wave * 64 < BM) {
+    if (kg == 0 && wave * 64 + lane < BM) {  // one lane per row of the block (BM may be 32)
       const float dn = scw * sv, y = 1.0f / dn;
       srow[wave * 64 + lane] = dn;
       srcp[wave * 64 + lane] = y;
@@ -773,7 +789,8 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 // of 49-64 rows with K <= 6912 and enough tiles (at least kKGroupTiles 64 x 128 tiles, or
 // at least 64 32 x 64 tiles, or at most 64 stages) runs instead on tiles of eight K-groups
 // in one block (kw), whose partial tiles meet in LDS: no partials through memory and no
-// split-K epilogue launch; 17-32 rows take 32 x 64 such tiles at K <= 4096.
+// split-K epilogue launch; 17-32 rows take 32 x 64 such tiles (K <= 4096, or K <= 6912
+// with at least 32 tiles).
 struct Plan {
   int wm, wn, ksplit, kw;
   int fm = 2;  // 32-row fragments per wave (1: 32-row tiles)
@@ -810,11 +827,16 @@ Plan plan_of(const GemmArgs& a) {
   // partial traffic growing with the split count), keeping >= 4 stages per split
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
-  if (kw8_rows32() && a.rows > 16 && a.rows <= 32 && p.ksplit > 1 && nst <= 64 && nst >= 16) {
+  const int t32 = tiles_of<1, 1, 1>(a) * nz;  // 32 x 64 tiles
+  // 17-32 rows: 32 x 64 tiles of eight K-groups where K <= 4096, or K <= 6912 with at least
+  // 32 tiles (the 1.3B down projection, K = 5632: 12.2 us per launch against 9.4 us for the
+  // split plus 2.0 us for its epilogue launch, whose writes also delayed the next launch by
+  // 2.4 us)
+  if (kw8_rows32() && a.rows > 16 && a.rows <= 32 && p.ksplit > 1 && nst >= 16 &&
+      (nst <= 64 || (nst <= 216 && t32 >= 32))) {
     p = Plan{1, 1, 1, 8, 1};
     return p;
   }
-  const int t32 = tiles_of<1, 1, 1>(a) * nz;  // 32 x 64 tiles
   if (p.wm == 1 && a.rows > 48 && p.ksplit > 1 && nst >= 16 && nst <= 216 &&
       (tiles >= kKGroupTiles || nst <= 64 || t32 >= 64)) {
     // (a 4-wave-wide tile never splits: it has >= 256 tiles) tiles of eight K-groups, one
