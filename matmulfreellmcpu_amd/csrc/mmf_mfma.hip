@@ -789,7 +789,7 @@ bool mfma_launch(const GemmArgs& a, const ActBuf& act, dim3 grid, hipStream_t s)
 // of 49-64 rows with K <= 6912 and enough tiles (at least kKGroupTiles 64 x 128 tiles, or
 // at least 64 32 x 64 tiles, or at most 64 stages) runs instead on tiles of eight K-groups
 // in one block (kw), whose partial tiles meet in LDS: no partials through memory and no
-// split-K epilogue launch; 17-32 rows take 32 x 64 such tiles (K <= 4096, or K <= 6912
+// split-K epilogue launch; 8-32 rows take 32 x 64 such tiles (K <= 4096, or K <= 6912
 // with at least 32 tiles).
 struct Plan {
   int wm, wn, ksplit, kw;
@@ -828,12 +828,13 @@ Plan plan_of(const GemmArgs& a) {
   const int nst = a.p[0].g.Lc / 8;
   while (tiles * p.ksplit < 128 && nst / (2 * p.ksplit) >= 4 && p.ksplit < 16) p.ksplit *= 2;
   const int t32 = tiles_of<1, 1, 1>(a) * nz;  // 32 x 64 tiles
-  // 17-32 rows: 32 x 64 tiles of eight K-groups where K <= 4096, or K <= 6912 with at least
-  // 32 tiles (the 1.3B down projection, K = 5632: 12.2 us per launch against 9.4 us for the
-  // split plus 2.0 us for its epilogue launch, whose writes also delayed the next launch by
-  // 2.4 us)
-  if (kw8_rows32() && a.rows > 16 && a.rows <= 32 && p.ksplit > 1 && nst >= 16 &&
-      (nst <= 64 || (nst <= 216 && t32 >= 32))) {
+  // 8-32 rows: 32 x 64 tiles of eight K-groups where K <= 4096 (16-row op calls: 2048 x
+  // 11264 15.8 -> 11.6 us, 1024 x 1024 10.5 -> 9.6 us per call), or over 16 rows K <= 6912
+  // with at least 32 tiles (the 1.3B down projection, K = 5632: 12.2 us per launch against
+  // 9.4 us for the split plus 2.0 us for its epilogue launch, whose writes also delayed the
+  // next launch by 2.4 us; at 16 rows the split stays faster, 15.5 against 17.2 us)
+  if (kw8_rows32() && a.rows >= 8 && a.rows <= 32 && p.ksplit > 1 && nst >= 16 &&
+      (nst <= 64 || (nst <= 216 && t32 >= 32 && a.rows > 16))) {
     p = Plan{1, 1, 1, 8, 1};
     return p;
   }

@@ -36,6 +36,33 @@ def test_bitlinear_rows(eng, oracle, rows, K, N, mode):  # noqa: F811
     assert_bitexact(dout.get(), want["out"], f"bitlinear out mode {mode}")
 
 
+# 8-32 rows on 32 x 64 tiles of eight K-groups (the row tile partly past the last row):
+# K up to 4096, and over 16 rows up to 6912 with at least 32 tiles (16 x 5632 x 2048 takes
+# the K split); with int32 accumulators (the general
+# K-group sum and epilogue) and without (where the whole tile is in range: the shared one).
+@pytest.mark.parametrize("rows,K,N", [(8, 1024, 1024), (12, 2048, 640), (16, 5632, 2048), (24, 6912, 2560),
+                                      (31, 4096, 2112), (32, 2560, 2560)])
+@pytest.mark.parametrize("mode", [FIXED, INT8])
+@pytest.mark.parametrize("with_acc", [True, False])
+def test_kgroup_few_rows(eng, oracle, rows, K, N, mode, with_acc):  # noqa: F811
+    print(f"k-group few-row bitlinear rows={rows} K={K} N={N} mode={mode} acc={with_acc}", flush=True)
+    rng = np.random.default_rng(rows * 11 + K + N + mode)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    x[rows // 3] *= 40.0  # saturating Q5.10 codes in one row
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, mode)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    dacc = Dev(eng, shape=(rows, N), dtype=np.int32) if with_acc else None
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=mode, acc=dacc.ptr if with_acc else None)
+    eng.sync()
+    if with_acc:
+        np.testing.assert_array_equal(dacc.get(), want["acc"])
+    assert_bitexact(dout.get(), want["out"], f"k-group few-row bitlinear out mode {mode}")
+
+
 # Many-row Float and FixedQ510 prologues of long rows take the half-row LDS kernel (nb >=
 # 512; Int8Absmax keeps the whole-row kernel): 4100 (pass B is only the tail group), 4231 (a
 # 7-element tail; K % 4 != 0 takes the general prologue), 5632 and 6912 (the MLP down widths:
