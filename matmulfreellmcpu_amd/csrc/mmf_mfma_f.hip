@@ -8,8 +8,8 @@
 // v_mfma_f32_32x32x1_2b_f32, v_mfma_f32_16x16x1_4b_f32) compute D = C + A*B, so a chain of
 // them on one accumulator, fed the chain's positions in t order, reproduces acc_j bit for bit
 // (denormals included). Each chain is its own accumulator tile, run by its own wave: 8 waves
-// per tile, wave j running chain j, and wave 0 adds the 8 chain tiles through LDS in the
-// hsum_ps order where each output is stored.
+// per tile, wave j running chain j; the 8 chain tiles meet in LDS, and each wave adds an
+// eighth of the outputs in the hsum_ps order where it stores them.
 //
 // Operands go straight to registers, 3 chunks of 16 chain positions in flight per wave (no
 // wave shares another's activations, so there is no LDS staging and no barrier until the
@@ -72,44 +72,60 @@ __global__ __launch_bounds__(512) void k_mfma_f32w(GemmArgs a, ActBuf act) {
     nok = n < N;
   }
   const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8 + j;
+  // every lane loads from an in-range row and chunk (rows past the last are multiplied but
+  // never stored; a column past the last multiplies zero codes), so every chunk issues the
+  // same five loads unconditionally and the compiler waits for each chunk with a constant
+  // count, S - 1 chunks of loads still in flight (a conditional load made it wait for all)
   const int ri = lane & 31;
-  const bool rok = row0 + ri < a.rows;
-  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride() + j * Lc;
+  const int rl = min(row0 + ri, a.rows - 1);
+  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + rl) * act.ystride() + j * Lc;
   auto load = [&](int c, float4 (&v)[4], uint32_t& w) {
+    c = min(c, Wc - 1);
 #pragma unroll
-    for (int tq = 0; tq < 4; ++tq)
-      v[tq] = rok ? *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq) : make_float4(0.f, 0.f, 0.f, 0.f);
-    w = nok ? wrow[static_cast<size_t>(c) * 128] : 0u;
+    for (int tq = 0; tq < 4; ++tq) v[tq] = *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq);
+    w = wrow[static_cast<size_t>(c) * 128];
   };
   v32f acc = v32f{};
   float4 ar[S][4];
   uint32_t wr[S];
+  // (issued in chunk order, which the scheduler must keep: the first chunk's loads issued
+  // last would make every wait count zero)
 #pragma unroll
-  for (int u = 0; u < S; ++u)
-    if (u < Wc) load(u, ar[u], wr[u]);
-  for (int c0 = 0; c0 < Wc; c0 += S) {
+  for (int u = 0; u < S; ++u) {
+    load(u, ar[u], wr[u]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto chunk = [&](int u) {  // the 16 positions of the chunk in ring slot u, in t order
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float4 v = ar[u][tq];
+        const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(y, code_f(nok ? wr[u] : 0u, 4 * tq + tt), acc, 0, 0, 0);
+      }
+  };
+  // whole runs of S chunks (no exit inside a run: the same loads and waits in every run),
+  // then the last Wc % S chunks, which load nothing
+  int c0 = 0;
+  for (; c0 + S <= Wc; c0 += S) {
 #pragma unroll
     for (int u = 0; u < S; ++u) {
-      const int c = c0 + u;
-      if (c >= Wc) break;
-#pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const float4 v = ar[u][tq];
-          const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
-          acc = __builtin_amdgcn_mfma_f32_32x32x1f32(y, code_f(wr[u], 4 * tq + tt), acc, 0, 0, 0);
-        }
-      if (c + S < Wc) load(c + S, ar[u], wr[u]);
+      chunk(u);
+      load(c0 + u + S, ar[u], wr[u]);  // refilled as soon as its chunk has used it
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // chain tiles through LDS [j][r][lane]; wave 0 adds them in the hsum_ps order
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (c0 + u < Wc) chunk(u);
+  // chain tiles through LDS [j][r][lane]; then every wave adds, in the hsum_ps order, and
+  // stores the outputs of accumulator rows r = j (mod 8): an eighth of the tile each
+  // (wave 0 alone took 10.7k cycles for a 32 x 64 tile)
   constexpr int PS = 32 * 64;
 #pragma unroll
   for (int r = 0; r < 32; ++r) smem[j * PS + r * 64 + lane] = acc[r];
   __syncthreads();
-  if (j != 0) return;
-  // each output's 8 chain values are added where it is stored (no 32-value array live)
   auto hsum = [&](int r) {
     const float* p = smem + r * 64 + lane;
     return ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(512) void k_mfma_f32w(GemmArgs a, ActBuf act) {
   };
   const int col = lane & 31, rq = 4 * (lane >> 5);
   if (PAIR) {
-    for (int r = 0; r < 16; ++r) {
+    for (int r = j; r < 16; r += 8) {
       const int row = row0 + 8 * (r >> 2) + rq + (r & 3);
       const int c = cbase + col;
       if (row >= a.rows || c >= Nh) continue;
@@ -134,7 +150,7 @@ __global__ __launch_bounds__(512) void k_mfma_f32w(GemmArgs a, ActBuf act) {
       a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
     }
   } else {
-    for (int r = 0; r < 32; ++r) {
+    for (int r = j; r < 32; r += 8) {
       const int rr = r & 15;
       const int row = row0 + 8 * (rr >> 2) + rq + (rr & 3);
       const int o = cbase + 32 * (r >> 4) + col;
@@ -174,42 +190,54 @@ __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
   }
   const uint32_t* wrow = P.pk + static_cast<size_t>(nok ? (n >> 4) : 0) * Wc * 128 + (n & 15) * 8 + j;
   const int ri = lane & 15;
-  const bool rok = row0 + ri < a.rows;
-  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + row0 + ri) * act.ystride() + j * Lc;
+  const int rl = min(row0 + ri, a.rows - 1);  // in-range loads only, as in k_mfma_f32w
+  const float* yrow = act.y + (static_cast<size_t>(am) * act.rows + rl) * act.ystride() + j * Lc;
   auto load = [&](int c, float4 (&v)[4], uint32_t& w) {
+    c = min(c, Wc - 1);
 #pragma unroll
-    for (int tq = 0; tq < 4; ++tq)
-      v[tq] = rok ? *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq) : make_float4(0.f, 0.f, 0.f, 0.f);
-    w = nok ? wrow[static_cast<size_t>(c) * 128] : 0u;
+    for (int tq = 0; tq < 4; ++tq) v[tq] = *reinterpret_cast<const float4*>(yrow + 16 * c + 4 * tq);
+    w = wrow[static_cast<size_t>(c) * 128];
   };
   v16f acc = v16f{};
   float4 ar[S][4];
   uint32_t wr[S];
+  // (issued in chunk order, which the scheduler must keep: the first chunk's loads issued
+  // last would make every wait count zero)
 #pragma unroll
-  for (int u = 0; u < S; ++u)
-    if (u < Wc) load(u, ar[u], wr[u]);
-  for (int c0 = 0; c0 < Wc; c0 += S) {
+  for (int u = 0; u < S; ++u) {
+    load(u, ar[u], wr[u]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto chunk = [&](int u) {  // the 16 positions of the chunk in ring slot u, in t order
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float4 v = ar[u][tq];
+        const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
+        acc = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(nok ? wr[u] : 0u, 4 * tq + tt), acc, 0, 0, 0);
+      }
+  };
+  // whole runs of S chunks (no exit inside a run: the same loads and waits in every run),
+  // then the last Wc % S chunks, which load nothing
+  int c0 = 0;
+  for (; c0 + S <= Wc; c0 += S) {
 #pragma unroll
     for (int u = 0; u < S; ++u) {
-      const int c = c0 + u;
-      if (c >= Wc) break;
-#pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const float4 v = ar[u][tq];
-          const float y = tt == 0 ? v.x : tt == 1 ? v.y : tt == 2 ? v.z : v.w;
-          acc = __builtin_amdgcn_mfma_f32_16x16x1f32(y, code_f(wr[u], 4 * tq + tt), acc, 0, 0, 0);
-        }
-      if (c + S < Wc) load(c + S, ar[u], wr[u]);
+      chunk(u);
+      load(c0 + u + S, ar[u], wr[u]);  // refilled as soon as its chunk has used it
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (c0 + u < Wc) chunk(u);
   constexpr int PS = 16 * 64;  // floats of one chain's tile in LDS [j][r][lane]
 #pragma unroll
   for (int r = 0; r < 16; ++r) smem[j * PS + r * 64 + lane] = acc[r];
   __syncthreads();
-  if (j != 0) return;
-  // each output's 8 chain values are added where it is stored
+  // each output's 8 chain values are added where it is stored, wave j taking accumulator
+  // rows r = j (mod 8), as in k_mfma_f32w
   auto hsum = [&](int r) {
     const float* p = smem + r * 64 + lane;
     return ((p[0] + p[4 * PS]) + (p[PS] + p[5 * PS])) + ((p[2 * PS] + p[6 * PS]) + (p[3 * PS] + p[7 * PS]));
@@ -225,7 +253,7 @@ __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
   };
   const int col = lane & 15, rq = 4 * (lane >> 4);
   if (PAIR) {
-    for (int r = 0; r < 8; ++r) {
+    for (int r = j; r < 8; r += 8) {
       const int row = row0 + rq + (r & 3);
       const int c = cbase + 16 * (r >> 2) + col;
       if (row >= a.rows || c >= Nh) continue;
@@ -234,7 +262,7 @@ __global__ __launch_bounds__(512) void k_mfma_f1(GemmArgs a, ActBuf act) {
       a.out[0][e] = swiglu_of(vg, vu, static_cast<int64_t>(e) >= (a.swiglu_n & ~7));
     }
   } else {
-    for (int r = 0; r < 16; ++r) {
+    for (int r = j; r < 16; r += 8) {
       const int row = row0 + rq + (r & 3);
       const int o = cbase + 16 * (r >> 2) + col;
       if (row >= a.rows || o >= N) continue;
