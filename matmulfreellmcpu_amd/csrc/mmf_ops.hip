@@ -840,44 +840,63 @@ void k_rowpro_split(PrologueArgs a, ActBuf act) {
 }
 
 // The row prologue of a few rows at the model widths (K = 256 RC: no tail, no padding) for
-// the stage kinds without element-wise work (kPreNorm, kPreNone), one wave per row and no
-// wait on other waves. The wave loads its row coalesced (float4 q of lane l is q = l + 64 k)
-// and turns it through LDS into the lane-segment layout of the register chains: lane 8j + s
-// holds steps [4 RC s, 4 RC (s + 1)) of chain j, i.e. chain-transposed floats
-// [4 RC l, 4 RC (l + 1)), the layout in which the stage-1 weight pre_wT and the norm weights
-// normwT are stored. Both order-fixed norm chains then run from registers (seg_sumsq: one
-// dependent FMA per step and a DPP shift between segments), and each lane encodes its own
-// steps, consecutive chain positions: float4 stores of y, or one word of four codes per
-// plane and step quad. Arithmetic and order are those of k_rowpro. (The swish-gate kinds run
-// in k_rowseg_sw: their silu, sigmoid and swiglu per element on one wave per row measured
-// 13.8 us against k_rowpro's 10.7 us for 64 rows at K = 2560.)
+// the stage kinds without element-wise work (kPreNorm, kPreNone): one wave per projection
+// (NA waves per row) and no wait on other blocks. The waves load the row coalesced (float4
+// q = l + 64 k, a share of the k each) and turn it through LDS into the lane-segment layout
+// of the register chains: lane 8j + s holds steps [4 RC s, 4 RC (s + 1)) of chain j, i.e.
+// chain-transposed floats [4 RC l, 4 RC (l + 1)), the layout in which the stage-1 weight
+// pre_wT and the norm weights normwT are stored. Every wave then runs both order-fixed norm
+// chains from registers (seg_sumsq: one dependent FMA per step and a DPP shift between
+// segments; the same chains in every wave, side by side on the CU's SIMDs) and encodes its
+// own projection, whose norm weights it loads at entry. Arithmetic and order are those of
+// k_rowpro. (One wave encoding all three i/f/g projections: 6.9 us per launch at hidden
+// 2560 and 64 rows, against 6.0 us with a wave each; splitting one projection's steps over
+// two waves measured no faster. The swish-gate kinds run in k_rowseg_sw: their silu, sigmoid
+// and swiglu per element on one wave per row measured 13.8 us against k_rowpro's 10.7 us for
+// 64 rows at K = 2560.)
 template <int MODE, int PRE, int NA, int RC>
-__global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
+__global__ __launch_bounds__(64 * NA) void k_rowseg(PrologueArgs a, ActBuf act) {
   static_assert(PRE == kPreNorm || PRE == kPreNone, "element-wise stage kinds run in k_rowpro");
+  constexpr int W = NA;
   constexpr int Lc = 32 * RC, K = 8 * Lc, LS = Lc + 4;
+  constexpr int KW = (RC + W - 1) / W;  // row float4 per lane per wave at entry
   __shared__ float X[8 * LS];
   const int row = xcd_row(blockIdx.x);
   if (row >= act.rows) return;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  // this wave's projection (a compile-time 0 with one projection: no run-time guards)
+  const int ai = (NA > 1) ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
+  const int wv = ai;
   const float4* xr = reinterpret_cast<const float4*>(a.x + static_cast<size_t>(row) * K);
 
-  // entry loads: the row (natural layout) and the stage-1 weight (segment layout)
-  float4 nx[RC];
+  // entry loads: this wave's share of the row (natural layout), the stage-1 weight and,
+  // with several projections, the norm weights of its own (segment layout; one projection
+  // loads them after the chains: at entry, 40 more registers in flight measured 0.5 us
+  // slower)
+  float4 nx[KW];
 #pragma unroll
-  for (int k = 0; k < RC; ++k) nx[k] = xr[lane + 64 * k];
+  for (int k = 0; k < KW; ++k)
+    if (wv * KW + k < RC) nx[k] = xr[lane + 64 * (wv * KW + k)];
   float4 ws[PRE != kPreNone ? RC : 1];
   if constexpr (PRE != kPreNone) {
 #pragma unroll
     for (int c = 0; c < RC; ++c) ws[c] = reinterpret_cast<const float4*>(a.pre_wT)[lane * RC + c];
   }
+  float4 nw[NA > 1 ? RC : 1];
+  if constexpr (NA > 1) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) nw[c] = reinterpret_cast<const float4*>(a.normwT[ai])[lane * RC + c];
+  }
   // natural float4 q holds elements 4q .. 4q+3: step q / 2 of chains 4 (q % 2) .. 4 (q % 2) + 3
 #pragma unroll
-  for (int k = 0; k < RC; ++k) {
-    const int q = lane + 64 * k, t = q >> 1, j0 = 4 * (q & 1);
+  for (int k = 0; k < KW; ++k) {
+    if (wv * KW + k < RC) {
+      const int q = lane + 64 * (wv * KW + k), t = q >> 1, j0 = 4 * (q & 1);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) X[(j0 + c) * LS + t] = f4el(nx[k], c);
+      for (int c = 0; c < 4; ++c) X[(j0 + c) * LS + t] = f4el(nx[k], c);
+    }
   }
-  __syncthreads();  // one wave: orders the LDS writes before the reads below
+  __syncthreads();
   const int j = lane >> 3, sg = lane & 7;
   float4 xs[RC];
 #pragma unroll
@@ -895,51 +914,48 @@ __global__ __launch_bounds__(64) void k_rowseg(PrologueArgs a, ActBuf act) {
   }
   const float r2 = rstd_of(seg_sumsq<RC>(xs, zt, 0), K, a.eps);
 
+  const size_t ar = static_cast<size_t>(ai) * act.rows + row;
+  float4 y[RC];
 #pragma unroll
-  for (int ai = 0; ai < NA; ++ai) {
-    const size_t ar = static_cast<size_t>(ai) * act.rows + row;
-    float4 y[RC];
+  for (int c = 0; c < RC; ++c) {
+    const float4 w = (NA > 1) ? nw[c] : reinterpret_cast<const float4*>(a.normwT[ai])[lane * RC + c];
+    const float4 x = xs[c];
+    y[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
+  }
+  if constexpr (MODE == kFloat) {
+    float* yo = act.y + ar * act.ystride();
+#pragma unroll
+    for (int c = 0; c < RC; ++c) reinterpret_cast<float4*>(yo)[lane * RC + c] = y[c];
+    if (lane < 8) yo[8 * Lc + lane] = 0.0f;
+  } else {
+    float sa = 0.0f;
+    if constexpr (MODE == kInt8) {
+      float m = 0.0f;
+#pragma unroll
+      for (int c = 0; c < RC; ++c)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(y[c].x), fabsf(y[c].y)), fmaxf(fabsf(y[c].z), fabsf(y[c].w))));
+      m = wave_max(m);
+      sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
+      if (lane == 0) act.sa[ar] = sa;
+    }
+    int8_t* q = act.q + act.qoff(ai, 0, row, 0);
+    const size_t lop = act.qplane();
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
-      const float4 w = reinterpret_cast<const float4*>(a.normwT[ai])[lane * RC + c];
-      const float4 x = xs[c];
-      y[c] = make_float4((x.x * r2) * w.x, (x.y * r2) * w.y, (x.z * r2) * w.z, (x.w * r2) * w.w);
-    }
-    if constexpr (MODE == kFloat) {
-      float* yo = act.y + ar * act.ystride();
+      int32_t cd[4];
 #pragma unroll
-      for (int c = 0; c < RC; ++c) reinterpret_cast<float4*>(yo)[lane * RC + c] = y[c];
-      if (lane < 8) yo[8 * Lc + lane] = 0.0f;
-    } else {
-      float sa = 0.0f;
-      if constexpr (MODE == kInt8) {
-        float m = 0.0f;
-#pragma unroll
-        for (int c = 0; c < RC; ++c)
-          m = fmaxf(m, fmaxf(fmaxf(fabsf(y[c].x), fabsf(y[c].y)), fmaxf(fabsf(y[c].z), fabsf(y[c].w))));
-        m = wave_max(m);
-        sa = 127.0f / (m > 1e-5f ? m : 1e-5f);
-        if (lane == 0) act.sa[ar] = sa;
+      for (int e = 0; e < 4; ++e) cd[e] = (MODE == kFixed) ? q510_body(f4el(y[c], e), a.qs) : q8_of(f4el(y[c], e), sa);
+      const size_t o = ActBuf::qpos(4 * (lane * RC + c));
+      if constexpr (MODE == kFixed) {
+        uint32_t h, l;
+        pack_split4(cd, h, l);
+        *reinterpret_cast<uint32_t*>(q + o) = h;
+        *reinterpret_cast<uint32_t*>(q + lop + o) = l;
+      } else {
+        *reinterpret_cast<uint32_t*>(q + o) = pack_low4(cd);
       }
-      int8_t* q = act.q + act.qoff(ai, 0, row, 0);
-      const size_t lop = act.qplane();
-#pragma unroll
-      for (int c = 0; c < RC; ++c) {
-        int32_t cd[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cd[e] = (MODE == kFixed) ? q510_body(f4el(y[c], e), a.qs) : q8_of(f4el(y[c], e), sa);
-        const size_t o = ActBuf::qpos(4 * (lane * RC + c));
-        if constexpr (MODE == kFixed) {
-          uint32_t h, l;
-          pack_split4(cd, h, l);
-          *reinterpret_cast<uint32_t*>(q + o) = h;
-          *reinterpret_cast<uint32_t*>(q + lop + o) = l;
-        } else {
-          *reinterpret_cast<uint32_t*>(q + o) = pack_low4(cd);
-        }
-      }
-      if (lane < 8) act.ct[ar * 8 + lane] = 0;
     }
+    if (lane < 8) act.ct[ar * 8 + lane] = 0;
   }
 }
 
@@ -1991,7 +2007,7 @@ constexpr int kSegRows = 512, kSegRowsNone = 16;
 template <int MODE, int PRE, int NA, int RC>
 static hipError_t rowseg_inst(const PrologueArgs& a, ActBuf& act, hipStream_t s) {
   if constexpr (PRE == kPreNorm || PRE == kPreNone) {
-    k_rowseg<MODE, PRE, NA, RC><<<row_grid(act.rows), 64, 0, s>>>(a, act);
+    k_rowseg<MODE, PRE, NA, RC><<<row_grid(act.rows), 64 * NA, 0, s>>>(a, act);
     return hipGetLastError();
   } else if constexpr (NA == 1) {
     k_rowseg_sw<MODE, PRE, RC><<<row_grid(act.rows), 1024, 0, s>>>(a, act);
