@@ -340,8 +340,12 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
     } else {
       wait_vm<3 * NT>();
     }
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // one barrier per stage where a K-group's slots are shared by several waves; a one-wave
+    // group owns its slots (the waits above order its own reads and transfers)
+    if constexpr (NW > 1) {
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
     if (st + D - 1 < cnt) issue(ic<(S + D - 1) % D>{}, st + D - 1);
     const unsigned char* sb = slot(sc) + kg * SS;
     uint32_t bw[KQ][FN];
