@@ -117,6 +117,29 @@ def test_bitlinear_op_float_mfma(eng, oracle, rows, K, N):
     assert_bitexact(dout.get(), want["out"], "bitlinear float mfma")
 
 
+@pytest.mark.parametrize("rows,K,N", [(64, 1024, 512), (256, 1000, 1600)])
+def test_bitlinear_op_float_mfma_denormal(eng, oracle, rows, K, N):
+    """The fp32 matrix-core chains through the denormal range: norm weights near 1e-38 make
+    the BitLinear inputs and most chain sums denormal, so each matrix op must keep the
+    reference's denormal sums and roundings (16 x 64 tiles at 64 rows, 32 x 64 tiles at 256
+    rows)."""
+    print(f"bitlinear float mfma denormal rows={rows} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(rows + K * 7 + N)
+    x = (rng.standard_normal((rows, K)) * 2).astype(np.float32)
+    nw = (rng.uniform(0.05, 3.0, K) * 1e-38).astype(np.float32)
+    nw[::7] *= -1.0
+    wq = rng.integers(-1, 2, (N, K)).astype(np.int8)
+    sw = float(np.float32(1.0 / 0.0157))
+    want = oracle.bitlinear(x, nw, wq, sw, 1e-6, FLOAT)
+    tiny = np.abs(want["out"]) < np.float32(1.17549435e-38)
+    assert tiny.mean() > 0.5  # most outputs are denormal (the check exercises that range)
+    pid = eng.register_proj(wq, sw, nw)
+    dx, dout = Dev(eng, x), Dev(eng, shape=(rows, N))
+    eng.bitlinear(pid, dx.ptr, dout.ptr, rows, mode=FLOAT)
+    eng.sync()
+    assert_bitexact(dout.get(), want["out"], "bitlinear float mfma denormal")
+
+
 def test_measured_ceilings(eng):
     """The calibration kernels run and give rates below the published peaks (HBM 8 TB/s,
     int8 dense 5.0 POP/s, fp32 vector FMA without packing 78.6 TFLOP/s) and well above zero."""
