@@ -301,6 +301,9 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   constexpr int NT = DA + DB;  // transfers per wave per stage
   static_assert(D >= 3 && D <= 6 && (D - 2) * NT < 64, "ring depth");
   constexpr int QB = KW * SS;
+  // two-group split of the sum and the epilogue (see after the main loop): each group's four
+  // waves send one fragment pair (FN x 4 KB) through two ring slots
+  constexpr bool KW2S = KW == 2 && FM == 2 && NW == 4 && D >= 4 && 2 * FN * 4096 <= QB;
   __shared__ __align__(16) unsigned char q0[QB], q1[QB], q2[QB], q3[D > 3 ? QB : 16], q4[D > 4 ? QB : 16],
       q5[D > 5 ? QB : 16];
   __shared__ float srow[BM];  // Int8: the divisor of each row, scale_w * scale_a
@@ -511,6 +514,48 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
         return;
       }
     }
+    // Two K-groups of two row fragments each (the long-prefill 128 x 128 tiles): the groups
+    // split the sum and the epilogue by row fragment. Group g keeps fragment g, sends its
+    // fragment 1 - g to the same wave of the other group through LDS and adds the one it
+    // receives (exact int32 sums: any order), then stores its own 32-row half of the tile.
+    if constexpr (KW2S) {
+      // (kept and sent fragments as compile-time indices: a run-time index into the
+      // accumulator array would put it in scratch memory)
+      auto exch = [&](auto keepc) {
+        constexpr int KEEP = decltype(keepc)::value, SEND = 1 - KEEP;
+        __syncthreads();
+        {
+          v4i* out = reinterpret_cast<v4i*>((KEEP == 0 ? (wave < 2 ? q0 : q1) : (wave < 2 ? q2 : q3)) +
+                                            (wave & 1) * (FN * 4 * 64 * 16));
+#pragma unroll
+          for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v16i& v = acc[P - 1][SEND][bj];
+              out[(bj * 4 + q) * 64 + lane] = v4i{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            }
+        }
+        __syncthreads();
+        {
+          const v4i* in = reinterpret_cast<const v4i*>((KEEP == 1 ? (wave < 2 ? q0 : q1) : (wave < 2 ? q2 : q3)) +
+                                                       (wave & 1) * (FN * 4 * 64 * 16));
+#pragma unroll
+          for (int bj = 0; bj < FN; ++bj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v4i t = in[(bj * 4 + q) * 64 + lane];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[P - 1][KEEP][bj][4 * q + e] += t[e];
+            }
+        }
+        if constexpr (KEEP == 1) {  // the kept fragment to slot 0: the epilogue runs on slot 0
+#pragma unroll
+          for (int bj = 0; bj < FN; ++bj) acc[P - 1][0][bj] = acc[P - 1][1][bj];
+        }
+      };
+      if (kg == 0) exch(std::integral_constant<int, 0>{});
+      else exch(std::integral_constant<int, 1>{});
+    } else {
     // fragments per round: the most (up to all of them) for which every wave's fragments of
     // groups 1..KW-1 fit the first min(D, 4) ring slots, GPS groups sharing a slot
     constexpr int NS = D < 4 ? D : 4;
@@ -558,8 +603,13 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
       }
     }
     if (kg != 0) return;
+    }
   }
 
+  // with the two-group split each group stores one row fragment, held in slot 0, whose rows
+  // are shifted by its group index
+  constexpr int FME = KW2S ? 1 : FM;
+  const int ash = KW2S ? kg : 0;
   if (ksp > 1) {
     // split-K: exact partial sums of this stage range, logical column order
     int32_t* wp = wsp + (static_cast<size_t>(ks) * a.nmat + z) * act.rows * static_cast<size_t>(N);
@@ -570,10 +620,10 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
       const int o = (EPI == kEpiSwigluPair) ? ((cg & 1) ? Nh : 0) + (cg >> 1) * 32 + ol : cg * 32 + ol;
       if (cg >= ng32 || o >= N) continue;
 #pragma unroll
-      for (int ai = 0; ai < FM; ++ai)
+      for (int ai = 0; ai < FME; ++ai)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int row = row0 + (wm * FM + ai) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+          const int row = row0 + (wm * FM + ai + ash) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
           if (row >= act.rows) continue;
           wp[static_cast<size_t>(row) * N + o] =
               (MODE == kFixed) ? acc[0][ai][bj][i] * 256 + acc[P - 1][ai][bj][i] : acc[0][ai][bj][i];
@@ -593,10 +643,10 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
   float addv[FM][16][NB];
   if (EPI == kEpiAdd) {
 #pragma unroll
-    for (int ai = 0; ai < FM; ++ai)
+    for (int ai = 0; ai < FME; ++ai)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        int row = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5) + 8 * (i >> 2) + (i & 3);
+        int row = row0 + (wm * FM + ai + ash) * 32 + 4 * (lane >> 5) + 8 * (i >> 2) + (i & 3);
         row = row < act.rows ? row : act.rows - 1;
 #pragma unroll
         for (int b = 0; b < NB; ++b) addv[ai][i][b] = cok[b] ? addp[static_cast<size_t>(row) * N + col[b]] : 0.0f;
@@ -609,8 +659,8 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
                     (EPI != kEpiSwigluPair || static_cast<size_t>(row0 + BM) * Nout <= static_cast<size_t>(swn & ~7));
   auto fast_epi = [&](auto use_rcp) {
 #pragma unroll
-    for (int ai = 0; ai < FM; ++ai) {
-      const int rbase = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5);
+    for (int ai = 0; ai < FME; ++ai) {
+      const int rbase = row0 + (wm * FM + ai + ash) * 32 + 4 * (lane >> 5);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = rbase + 8 * (i >> 2) + (i & 3);
@@ -641,8 +691,8 @@ __global__ __launch_bounds__(64 * WM * WN * KW, (mfma_min_waves<MODE, EPI, WM, W
     return;
   }
 #pragma unroll
-  for (int ai = 0; ai < FM; ++ai) {
-    const int rbase = row0 + (wm * FM + ai) * 32 + 4 * (lane >> 5);
+  for (int ai = 0; ai < FME; ++ai) {
+    const int rbase = row0 + (wm * FM + ai + ash) * 32 + 4 * (lane >> 5);
     float den[16];
     if (MODE == kInt8) {
 #pragma unroll
