@@ -1006,7 +1006,7 @@ void mmf_destroy(mmf_ctx* c) {
     b->release();
   RowScratch& s = m.rs;
   for (DBuf* b : {&s.ids, &s.h, &s.resid, &s.i, &s.f, &s.g, &s.recur, &s.scan, &s.z, &s.logits, &s.state0, &s.am,
-                  &s.acty, &s.actq, &s.actct, &s.actsa, &s.segs})
+                  &s.acty, &s.actq, &s.actct, &s.actsa, &s.segs, &s.chunk})
     b->release();
   for (DBuf* b : {&c->raw, &c->opy, &c->opq, &c->opct, &c->opsa, &c->opstate, &c->gws, &c->hmx, &c->hmacc})
     b->release();
