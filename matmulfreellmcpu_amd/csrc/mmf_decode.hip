@@ -253,16 +253,26 @@ void k_decode(DecArgs a) {
   // the weight words of the block's output groups (after the input, which the norms need
   // first): straight into LDS in the slab order, 16 bytes per lane, so one instruction of a
   // wave moves 1 KB (two slab rows); the 2 KS waves of a matrix take every 2 KS-th KB. A slab
-  // of an odd number of rows ends in half a KB, which lanes 32..63 skip.
+  // of an odd number of rows ends in half a KB, which lanes 32..63 skip. With register chains
+  // wave 0 issues none of them: its chains wait for every load the wave has in flight (the
+  // copy loops' counts are not known at compile time), and behind its share of the copies
+  // the 2.7B lm_head's first chain waited 3.3 us for the launch's whole weight stream; the
+  // other waves of matrix 0 take its share (2.7B float decode 819 -> 862 tok/s). Not in the
+  // integer gate/up kernel, held to 128 VGPRs: there it spilled more and ran 0.4 us slower.
   {
     const int nwords = Ww * 128, wv = part * 2 + (lt >> 6), lane = lt & 63;
-    for (int gi = 0; gi < G; ++gi) {
-      const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
-      if (og_i >= ngroups_out) break;
-      const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * nwords;
-      uint32_t* dx = WX + (mi * G + gi) * nwords;
-      for (int c = wv * 256; c < nwords; c += 512 * KS)
-        if (c + 4 * lane < nwords) __builtin_amdgcn_global_load_lds(sx + c + 4 * lane, (lds_void*)(dx + c), 16, 0, 0);
+    constexpr bool SKIP0 = RC > 0 && !(MODE != kFloat && KIND == kGate);
+    const int nwv = 2 * KS - ((SKIP0 && mi == 0) ? 1 : 0);  // copying waves of this matrix
+    const int cw = (SKIP0 && mi == 0) ? wv - 1 : wv;        // this wave's index among them
+    if (cw >= 0) {
+      for (int gi = 0; gi < G; ++gi) {
+        const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
+        if (og_i >= ngroups_out) break;
+        const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * nwords;
+        uint32_t* dx = WX + (mi * G + gi) * nwords;
+        for (int c = cw * 256; c < nwords; c += 256 * nwv)
+          if (c + 4 * lane < nwords) __builtin_amdgcn_global_load_lds(sx + c + 4 * lane, (lds_void*)(dx + c), 16, 0, 0);
+      }
     }
   }
   // LDS float4 index of each of this thread's global float4s
