@@ -257,19 +257,21 @@ void k_decode(DecArgs a) {
   // wave 0 issues none of them: its chains wait for every load the wave has in flight (the
   // copy loops' counts are not known at compile time), and behind its share of the copies
   // the 2.7B lm_head's first chain waited 3.3 us for the launch's whole weight stream; the
-  // other waves of matrix 0 take its share (2.7B float decode 819 -> 862 tok/s). Not in the
-  // integer gate/up kernel, held to 128 VGPRs: there it spilled more and ran 0.4 us slower.
+  // other waves of matrix 0 take its share (2.7B float decode 819 -> 862 tok/s). The wave
+  // indices are scalars (one value per wave).
   {
-    const int nwords = Ww * 128, wv = part * 2 + (lt >> 6), lane = lt & 63;
-    constexpr bool SKIP0 = RC > 0 && !(MODE != kFloat && KIND == kGate);
-    const int nwv = 2 * KS - ((SKIP0 && mi == 0) ? 1 : 0);  // copying waves of this matrix
-    const int cw = (SKIP0 && mi == 0) ? wv - 1 : wv;        // this wave's index among them
+    const int w64 = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wmi = (w64 % (2 * NM)) >> 1, wv = (w64 / (2 * NM)) * 2 + (w64 & 1), lane = lt & 63;
+    const int nwords = Ww * 128;
+    constexpr bool SKIP0 = RC > 0;
+    const int nwv = 2 * KS - ((SKIP0 && wmi == 0) ? 1 : 0);  // copying waves of this matrix
+    const int cw = (SKIP0 && wmi == 0) ? wv - 1 : wv;        // this wave's index among them
     if (cw >= 0) {
       for (int gi = 0; gi < G; ++gi) {
         const int og_i = static_cast<int>(blockIdx.x) + gi * static_cast<int>(gridDim.x);
         if (og_i >= ngroups_out) break;
         const uint32_t* sx = pk + static_cast<size_t>(og_i + mrow) * nwords;
-        uint32_t* dx = WX + (mi * G + gi) * nwords;
+        uint32_t* dx = WX + (wmi * G + gi) * nwords;
         for (int c = cw * 256; c < nwords; c += 256 * nwv)
           if (c + 4 * lane < nwords) __builtin_amdgcn_global_load_lds(sx + c + 4 * lane, (lds_void*)(dx + c), 16, 0, 0);
       }
