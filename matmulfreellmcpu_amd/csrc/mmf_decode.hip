@@ -784,7 +784,12 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   // and the wave would stall issuing them until the first ones return; the norm weight's
   // loads are issued in the middle of the norm chain instead (they are needed after it)
   constexpr bool DEFER_NW = !ST1 && 3 * RC > 60;
-  if constexpr (!DEFER_NW) load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
+  // kO at hidden 2048 and 2560: row, stage-1 weight, gate and norm weight are 4 (RC + 2)
+  // float4 per lane, and issuing them took 1.4 us at RC = 10 before the first chain could
+  // start; the norm weight's loads go into the middle of the first chain instead
+  constexpr bool DEFER_NW1 = KIND == kO && RC >= 8;
+  if constexpr (!DEFER_NW && !DEFER_NW1)
+    load_seg<RC>(KIND == kIFG ? (mi == 0 ? nwa : (mi == 1 ? nwb : nwc)) : nwa, lane, ns, nt8);
   // these loads issue first: nothing below (the DMA addresses need argument-block fields) may
   // move above them
   __builtin_amdgcn_sched_barrier(0);
@@ -815,7 +820,10 @@ __global__ __launch_bounds__(64 * KindTraits<KIND>::NM) void k_decf(const float*
   const int32_t e_rs = (MODE == kFixed && j == 0 && o < nout) ? 128 * Pa.rowsum[o] : 0;
   // ---- both norm chains in every wave, then this wave's activation row -----------------------
   if constexpr (ST1) {
-    const float r1 = rstd_of(seg_sumsq<RC>(xs, xt, nt), gK, aeps);
+    float ss1;
+    if constexpr (DEFER_NW1) ss1 = seg_sumsq_at<RC, 3>(xs, xt, nt, [&] { load_seg<RC>(nwa, lane, ns, nt8); });
+    else ss1 = seg_sumsq<RC>(xs, xt, nt);
+    const float r1 = rstd_of(ss1, gK, aeps);
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
       float4 x = xs[c];
