@@ -16,8 +16,8 @@
 // Weights ("pkm" layout): for physical 32-column group cg and 32-position block kb, the 64
 // words of lanes l = 32*kq + ol are contiguous: pkm[(cg * nK32 + kb) * 64 + l] holds the 16
 // codes of column 32*cg + ol at positions 32*kb + 16*kq + [0, 16) -- one word of the slab
-// layout, so a wave reads 256 contiguous bytes per fragment and expands each word to its
-// 16-byte B operand with four v_perm_b32. For the MLP gate matrix the groups are interleaved
+// layout with -1 stored as 10 instead of 11 -- so a wave reads 256 contiguous bytes per
+// fragment and expands each word to its 16-byte B operand with four v_perm_b32 (expand_w). For the MLP gate matrix the groups are interleaved
 // (gate group c at cg = 2c, its up partner N/2 + 32c at cg = 2c + 1) so that one wave holds
 // both halves of swiglu(gate, up) (hgrn_model.cpp:171-185) in registers.
 //
@@ -72,16 +72,25 @@ __global__ void k_pack_mfma(const uint32_t* __restrict__ pk, Geom g, int pair, u
     const int col = lcg * 32 + (l & 31), kq = l >> 5;
     const int p0 = kb * 32 + kq * 16;
     const int j = p0 / g.Lc, m = (p0 % g.Lc) >> 4;
-    pkm[w] = col < g.N ? pk[(static_cast<size_t>((col >> 4) * g.Wc + m) * 16 + (col & 15)) * 8 + j] : 0u;
+    // -1 (11) becomes 10, so that expand_w selects every byte with a single permute
+    const uint32_t x = col < g.N ? pk[(static_cast<size_t>((col >> 4) * g.Wc + m) * 16 + (col & 15)) * 8 + j] : 0u;
+    pkm[w] = x ^ ((x >> 1) & 0x55555555u);
   }
 }
 
+// A matrix-core slab word (codes 00 = 0, 01 = +1, 10 = -1; code t of the word at bit
+// 8 (t % 4) + 2 (t / 4)) as the 16 int8 weights of one operand, four per dword. Each dword is
+// one AND and one v_perm_b32 over the byte array {S0, S1}: with the codes at bits 0-1 of each
+// selector byte (values 0, 1, 2) the selector picks byte 0, 1 or 2 of S1 = {0x00, 0x01, 0xFF};
+// at bits 2-3 (values 0, 4, 8) it picks byte 0 of S1 (0x00), byte 0 of S0 (0x01), or with 8
+// the sign of S1's byte 1 (0x80) replicated (0xFF). The upper two dwords share one shift.
 __device__ __forceinline__ v4i expand_w(uint32_t w) {
+  const uint32_t h = w >> 4;
   v4i b;
-  b[0] = static_cast<int>(w4_i8(w, 0));
-  b[1] = static_cast<int>(w4_i8(w, 1));
-  b[2] = static_cast<int>(w4_i8(w, 2));
-  b[3] = static_cast<int>(w4_i8(w, 3));
+  b[0] = static_cast<int>(__builtin_amdgcn_perm(0u, 0x00FF0100u, w & 0x03030303u));
+  b[1] = static_cast<int>(__builtin_amdgcn_perm(0x01u, 0x00008000u, w & 0x0C0C0C0Cu));
+  b[2] = static_cast<int>(__builtin_amdgcn_perm(0u, 0x00FF0100u, h & 0x03030303u));
+  b[3] = static_cast<int>(__builtin_amdgcn_perm(0x01u, 0x00008000u, h & 0x0C0C0C0Cu));
   return b;
 }
 
